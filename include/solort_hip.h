@@ -1,0 +1,135 @@
+/*
+ * solort_hip.h - C ABI of the gfx950 (MI355X) attention hot path of a
+ * Qwen3 static-KV decode/prefill/verify step.
+ *
+ * The reference (SoloRT) runs this path as inline torch code inside
+ * _GraphQwen3Runner (src/solort/model/cuda_graph_executor.py); it has no FFI.
+ * Each entry point below replaces one block of that inline code and is cited
+ * to it.  Plain pointers and sizes only: every buffer is owned by the caller,
+ * nothing here allocates, frees, synchronises or reads device memory back, so
+ * every call can be recorded into a hipGraph.  The position of the token(s)
+ * is read on the device from `pos0_dev`, exactly like the reference's
+ * `pos_buf` (cuda_graph_executor.py:71), so one captured graph serves every
+ * position inside its bucket.
+ *
+ * Element types: bf16 buffers are passed as raw 16-bit words (uint16_t bits
+ * of a bfloat16).  head_dim must be 128.  KV caches are addressed with
+ * explicit token and head strides (in elements), so both the reference's
+ * token-major layout [max_len, nkv, hd] (cuda_graph_executor.py:67-69) and a
+ * head-major [nkv, max_len, hd] layout are accepted.  Every pointer passed
+ * to these functions must be 16-byte aligned and every stride a multiple of 8
+ * elements.
+ *
+ * Return value: 0 on success; SOLORT_EINVAL (negative) when an argument is
+ * rejected before launch; otherwise the hipError_t reported by the launch.
+ * solort_last_error() returns the message of the last failure on the calling
+ * thread.
+ */
+#ifndef SOLORT_HIP_H
+#define SOLORT_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SOLORT_EINVAL (-22)
+
+#define SOLORT_DTYPE_BF16 0
+#define SOLORT_DTYPE_F32 1
+
+/* hipStream_t, passed opaquely (torch.cuda.current_stream().cuda_stream). */
+typedef void* solort_stream_t;
+
+/* Version of this ABI; bumped when a signature changes. */
+int solort_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* solort_last_error(void);
+
+/*
+ * Per-head QK-RMSNorm + RoPE prologue with the in-place KV-cache write.
+ * Replaces, per layer, cuda_graph_executor.py:117-123 (prefill),
+ * :173-179 (decode) and :254-260 (verify):
+ *   q = rope(rmsnorm(q, qn_w, eps), cos, sin); k = rope(rmsnorm(k, kn_w, eps), cos, sin)
+ *   k_cache[pos] = k; v_cache[pos] = v            (rmsnorm :25-28, rope :100-102)
+ * qkv      [T, (nh + 2*nkv) * 128] bf16, row stride `qkv_row_stride` elements
+ *          (the fused QKV projection output, q | k | v column blocks).
+ * qn_w, kn_w [128] bf16 (q_norm / k_norm weights).
+ * cos_tab, sin_tab [tab_rows, 64] bf16: row p holds cos/sin of p * inv_freq,
+ *          i.e. the first half of the reference's _cos_sin row (:95-98); the
+ *          second half of that row is identical.
+ * pos0_dev int64 on the device: token t sits at position *pos0_dev + t
+ *          (NULL means position 0, the prefill case, :111).
+ * q_out    [T, nh, 128] bf16.
+ * k_cache, v_cache: this layer's cache; row `pos`, head h starts at
+ *          pos * kv_tok_stride + h * kv_head_stride.
+ * Positions outside [0, min(max_len, tab_rows)) are skipped on the device.
+ * The K/V rows written are bit-exact with the reference's op sequence given
+ * the same cos/sin table; the sum of squares uses a fixed reduction order.
+ */
+int solort_qknorm_rope_kvwrite(const void* qkv, int64_t qkv_row_stride, int T, int nh, int nkv,
+                               int hd, const void* qn_w, const void* kn_w, float eps,
+                               const void* cos_tab, const void* sin_tab, int64_t tab_rows,
+                               const int64_t* pos0_dev, void* q_out, void* k_cache, void* v_cache,
+                               int64_t kv_tok_stride, int64_t kv_head_stride, int64_t max_len,
+                               solort_stream_t stream);
+
+/* Workspace bytes needed by solort_decode_attn / solort_verify_attn for
+ * `nq` query tokens and `n_split` key splits.  The caller allocates it once,
+ * zero-fills it once, and reuses it: the kernels leave it ready for the next
+ * call.  Calls that overlap in time must not share a workspace. */
+size_t solort_attn_workspace_bytes(int nq, int nh, int nkv, int hd, int n_split);
+
+/*
+ * Grouped-query attention of `nq` new tokens over the static KV cache, split
+ * across `n_split` workgroups per KV head (flash-decoding) with the
+ * log-sum-exp combine fused into the same launch.
+ * Replaces the decode block cuda_graph_executor.py:168, :180-184 (nq = 1:
+ * softmax(q K^T * scale, keys > pos masked) V over the bucket) and the verify
+ * block :247-250, :261-263 (nq = K+1, query t at position pos0+t sees keys
+ * 0..pos0+t).  No KV repeat: query head h reads KV head h / (nh / nkv).
+ * q        [nq, nh, 128] bf16 (prologue output).
+ * pos0_dev int64 on the device (position of query 0).
+ * bound    static bucket: keys at or beyond `bound` are never read
+ *          (requires pos0 + nq <= bound <= max_len).
+ * scale    softmax scale (head_dim ** -0.5 in the reference, :44).
+ * ws       solort_attn_workspace_bytes(nq, nh, nkv, hd, n_split) bytes.
+ * out      [nq, nh * 128], bf16 (out_dtype 0) or fp32 (out_dtype 1).
+ */
+int solort_decode_attn(const void* q, int nq, int nh, int nkv, int hd, const void* k_cache,
+                       const void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride,
+                       int64_t max_len, const int64_t* pos0_dev, int bound, float scale, void* ws,
+                       int n_split, void* out, int out_dtype, solort_stream_t stream);
+
+/* Speculative-verify attention (cuda_graph_executor.py:245-263): the same
+ * kernel as solort_decode_attn with nq = K+1 query tokens at positions
+ * pos0..pos0+K, each causal over the cache.  Only the live keys
+ * 0..pos0+K are read (the reference scans all max_len keys with a mask). */
+int solort_verify_attn(const void* q, int nq, int nh, int nkv, int hd, const void* k_cache,
+                       const void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride,
+                       int64_t max_len, const int64_t* pos0_dev, int bound, float scale, void* ws,
+                       int n_split, void* out, int out_dtype, solort_stream_t stream);
+
+/* Workspace bytes for solort_argmax_rows with `rows` rows. Allocate once,
+ * zero-fill once, reuse; overlapping calls must not share it. */
+size_t solort_argmax_workspace_bytes(int rows);
+
+/*
+ * Greedy argmax over each row of logits [rows, vocab] (row stride
+ * `row_stride` elements), bf16 (dtype 0) or fp32 (dtype 1), into int64
+ * out_idx[rows].  Ties go to the lowest index and NaN counts as the maximum
+ * (first NaN wins), as torch.argmax does.
+ * Replaces cuda_graph_executor.py:201/:206 (in-graph), :234 (draft) and
+ * :475 (verify) `argmax(-1)`.
+ */
+int solort_argmax_rows(const void* logits, int dtype, int rows, int64_t vocab, int64_t row_stride,
+                       int64_t* out_idx, void* ws, solort_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* SOLORT_HIP_H */

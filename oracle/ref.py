@@ -1,0 +1,132 @@
+"""Torch-on-CPU restatement of the reference runner's attention math.
+
+TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).  Each function follows
+src/solort/model/cuda_graph_executor.py at the cited lines, op for op and in
+the same dtype, so that bf16 inputs give the reference's bf16 rounding of
+scores, probabilities and outputs.  Inputs are plain torch CPU tensors.
+"""
+from __future__ import annotations
+
+import torch
+import torch.nn.functional as F
+
+
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """cuda_graph_executor.py:25-28: fp32 upcast, x * rsqrt(mean(x^2) + eps), times w in fp32, cast back."""
+    xf = x.to(torch.float32)
+    inv_rms = torch.rsqrt(xf.square().mean(dim=-1, keepdim=True) + eps)
+    return ((xf * inv_rms) * w.to(torch.float32)).to(x.dtype)
+
+
+def inv_freq(hd: int, theta: float) -> torch.Tensor:
+    """cuda_graph_executor.py:64-66: 1 / theta^(2i/hd) in fp32."""
+    exps = torch.arange(0, hd, 2).to(torch.float32) / hd
+    return 1.0 / (float(theta) ** exps)
+
+
+def cos_sin(positions: torch.Tensor, inv_f: torch.Tensor, dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+    """cuda_graph_executor.py:95-98: angles pos * inv_freq in fp32, duplicated halves, cast to dtype."""
+    ang = positions.reshape(-1, 1).to(torch.float32) * inv_f.reshape(1, -1)
+    full = torch.cat((ang, ang), dim=-1)
+    return full.cos().to(dtype), full.sin().to(dtype)
+
+
+def rope(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """cuda_graph_executor.py:100-102: x*cos + rotate_half(x)*sin, each op in x's dtype."""
+    half = x.shape[-1] // 2
+    rotated = torch.cat((x[..., half:].neg(), x[..., :half]), dim=-1)
+    return x * cos + rotated * sin
+
+
+def prologue(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps: float,
+             cos: torch.Tensor, sin: torch.Tensor, nh: int, nkv: int, hd: int = 128):
+    """cuda_graph_executor.py:116-121 (and :172-177, :253-258).
+
+    qkv [T, (nh+2nkv)*hd] -> q [nh,T,hd], k [nkv,T,hd] (normed + roped), v [nkv,T,hd] (raw).
+    cos/sin are [T, hd] rows for the T positions.
+    """
+    T = qkv.shape[0]
+    q, k, v = torch.split(qkv, [nh * hd, nkv * hd, nkv * hd], dim=-1)
+    q = q.reshape(T, nh, hd).transpose(0, 1)
+    k = k.reshape(T, nkv, hd).transpose(0, 1)
+    v = v.reshape(T, nkv, hd).transpose(0, 1)
+    q = rope(rmsnorm(q, qn_w, eps), cos, sin)
+    k = rope(rmsnorm(k, kn_w, eps), cos, sin)
+    return q, k, v
+
+
+def write_kv(kc_l: torch.Tensor, vc_l: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pos0: int) -> None:
+    """cuda_graph_executor.py:122-123, :178-179, :259-260: rows pos0..pos0+T-1 of one layer's cache."""
+    T = k.shape[1]
+    idx = torch.arange(pos0, pos0 + T)
+    kc_l.index_copy_(0, idx, k.transpose(0, 1))
+    vc_l.index_copy_(0, idx, v.transpose(0, 1))
+
+
+def decode_attn(q: torch.Tensor, kc_l: torch.Tensor, vc_l: torch.Tensor, pos: int, bound: int,
+                scale: float) -> torch.Tensor:
+    """cuda_graph_executor.py:168, :180-184: grouped single-token attention over the bucket.
+
+    q [nh,1,hd]; kc_l/vc_l [max_len,nkv,hd]; keys with index > pos are masked.
+    Returns ctx [1, nh*hd] in q's dtype.
+    """
+    nh, hd = q.shape[0], q.shape[-1]
+    nkv = kc_l.shape[1]
+    qg = q.reshape(nkv, nh // nkv, hd)
+    keys_t = kc_l[:bound].permute(1, 2, 0)
+    vals = vc_l[:bound].permute(1, 0, 2)
+    ignore = (torch.arange(bound) > pos).view(1, 1, bound)
+    scores = (torch.matmul(qg, keys_t) * scale).masked_fill(ignore, float("-inf"))
+    probs = torch.softmax(scores, dim=-1).to(q.dtype)
+    return torch.matmul(probs, vals).reshape(1, nh * hd)
+
+
+def prefill_attn(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, scale: float) -> torch.Tensor:
+    """cuda_graph_executor.py:124-130: causal SDPA with K/V repeated over the query group.
+
+    q [nh,T,hd], k/v [nkv,T,hd] -> ctx [T, nh*hd].
+    """
+    nh, T, hd = q.shape
+    g = nh // k.shape[0]
+    kk = k.repeat_interleave(g, dim=0)
+    vv = v.repeat_interleave(g, dim=0)
+    out = F.scaled_dot_product_attention(q, kk, vv, is_causal=True, scale=scale)
+    return out.transpose(0, 1).reshape(T, nh * hd)
+
+
+def verify_attn(q: torch.Tensor, kc_l: torch.Tensor, vc_l: torch.Tensor, pos0: int,
+                scale: float) -> torch.Tensor:
+    """cuda_graph_executor.py:247-250, :261-263: K+1 queries over all max_len keys, key <= pos kept.
+
+    q [nh,K1,hd] -> ctx [K1, nh*hd].
+    """
+    nh, k1, hd = q.shape
+    max_len, nkv = kc_l.shape[0], kc_l.shape[1]
+    g = nh // nkv
+    pos = pos0 + torch.arange(k1)
+    keep = (torch.arange(max_len).view(1, -1) <= pos.view(-1, 1)).view(1, k1, max_len)
+    kk = kc_l.permute(1, 0, 2).repeat_interleave(g, dim=0)
+    vv = vc_l.permute(1, 0, 2).repeat_interleave(g, dim=0)
+    ctx = F.scaled_dot_product_attention(q, kk, vv, attn_mask=keep, scale=scale)
+    return ctx.transpose(0, 1).reshape(k1, nh * hd)
+
+
+def argmax(logits: torch.Tensor) -> torch.Tensor:
+    """cuda_graph_executor.py:190, :206 (and :234, :475): argmax(-1) of fp32 logits."""
+    return logits.to(torch.float32).argmax(dim=-1)
+
+
+def decode_layers(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps: float,
+                  cos: torch.Tensor, sin: torch.Tensor, kc: torch.Tensor, vc: torch.Tensor,
+                  pos: int, bound: int, nh: int, nkv: int, scale: float) -> torch.Tensor:
+    """The attention part of _decode_forward (cuda_graph_executor.py:164, :169-184) over all layers.
+
+    qkv [L, 1, (nh+2nkv)*hd] per-layer projections; qn_w/kn_w [L, hd]; kc/vc [L, max_len, nkv, hd]
+    (written in place); cos/sin [1, hd].  Returns ctx [L, nh*hd].
+    """
+    out = []
+    for li in range(qkv.shape[0]):
+        q, k, v = prologue(qkv[li], qn_w[li], kn_w[li], eps, cos, sin, nh, nkv)
+        write_kv(kc[li], vc[li], k, v, pos)
+        out.append(decode_attn(q, kc[li], vc[li], pos, bound, scale))
+    return torch.cat(out, dim=0)

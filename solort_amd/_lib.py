@@ -1,0 +1,75 @@
+"""ctypes binding of libsolort_hip.so (the C ABI declared in include/solort_hip.h).
+
+The library must already be built (``python -m solort_amd.build``); there is
+no fallback: a missing or stale library raises ``RuntimeError``.  torch is
+imported first so that the HIP runtime torch ships is the one the library
+binds to (both carry the soname libamdhip64.so.7), which makes torch's
+stream handles valid arguments.
+"""
+from __future__ import annotations
+
+import ctypes
+from ctypes import c_float, c_int, c_int64, c_size_t, c_void_p
+from pathlib import Path
+
+import torch  # noqa: F401  (loads torch's HIP runtime before ours)
+
+LIB_PATH = Path(__file__).resolve().parent / "libsolort_hip.so"
+ABI_VERSION = 1
+
+# name -> (restype, argtypes); mirrors include/solort_hip.h
+SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "solort_abi_version": (c_int, []),
+    "solort_last_error": (ctypes.c_char_p, []),
+    "solort_qknorm_rope_kvwrite": (
+        c_int,
+        [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p,
+         c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64,
+         c_void_p],
+    ),
+    "solort_attn_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
+    "solort_decode_attn": (
+        c_int,
+        [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_int64,
+         c_void_p, c_int, c_float, c_void_p, c_int, c_void_p, c_int, c_void_p],
+    ),
+    "solort_verify_attn": (
+        c_int,
+        [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_int64,
+         c_void_p, c_int, c_float, c_void_p, c_int, c_void_p, c_int, c_void_p],
+    ),
+    "solort_argmax_workspace_bytes": (c_size_t, [c_int]),
+    "solort_argmax_rows": (
+        c_int, [c_void_p, c_int, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p]
+    ),
+}
+
+_lib: ctypes.CDLL | None = None
+
+
+def load() -> ctypes.CDLL:
+    """Loads (once) and returns the library; raises RuntimeError if it is missing."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not LIB_PATH.exists():
+        raise RuntimeError(
+            f"{LIB_PATH} is not built; run `python -m solort_amd.build` (hipcc, gfx950)"
+        )
+    lib = ctypes.CDLL(str(LIB_PATH))
+    for name, (restype, argtypes) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = restype
+        fn.argtypes = argtypes
+    ver = lib.solort_abi_version()
+    if ver != ABI_VERSION:
+        raise RuntimeError(f"{LIB_PATH} has ABI {ver}, expected {ABI_VERSION}; rebuild it")
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raises RuntimeError with the library's message when rc != 0."""
+    if rc != 0:
+        msg = load().solort_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed ({rc}): {msg}")

@@ -1,0 +1,31 @@
+// Library-wide pieces of the C ABI: version and the per-thread error message.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "capi_internal.h"
+
+namespace {
+thread_local char g_err[512] = "";
+}
+
+namespace solort {
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error((int)e, "%s: launch failed: %s", what, hipGetErrorString(e));
+  return 0;
+}
+
+}  // namespace solort
+
+extern "C" int solort_abi_version(void) { return 1; }
+
+extern "C" const char* solort_last_error(void) { return g_err; }

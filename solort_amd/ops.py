@@ -1,0 +1,167 @@
+"""torch-tensor front end of the HIP kernels (one function per C-ABI entry point).
+
+Each function validates shapes, dtypes and devices on the host, then launches
+on the current torch stream with no host synchronisation, so it can be
+recorded inside ``torch.cuda.graph``.  Tensors must live on a ROCm device;
+there is no CPU or torch fallback.
+
+Layouts follow the reference runner (src/solort/model/cuda_graph_executor.py):
+  qkv      [T, (nh + 2*nkv) * 128] bf16   fused QKV projection output (:115, :171, :253)
+  cache    [max_len, nkv, 128] bf16       one layer of kc / vc (:67-69); any
+                                           token/head strides with unit dim stride
+  q        [T, nh, 128] bf16              prologue output
+  ctx      [T, nh * 128]                  attention output, head-major (:129, :184, :264)
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+HD = 128
+DTYPE_BF16 = 0
+DTYPE_F32 = 1
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _need(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _on_gpu(name: str, t: torch.Tensor, dtype: torch.dtype) -> None:
+    _need(t.is_cuda, f"{name} must be a ROCm device tensor (got {t.device})")
+    _need(t.dtype == dtype, f"{name} must be {dtype} (got {t.dtype})")
+    _need(t.data_ptr() % 16 == 0, f"{name} must be 16-byte aligned")
+
+
+def _cache_strides(name: str, c: torch.Tensor, nkv: int) -> tuple[int, int, int]:
+    _on_gpu(name, c, torch.bfloat16)
+    _need(c.dim() == 3 and c.shape[1] == nkv and c.shape[2] == HD,
+          f"{name} must be [max_len, {nkv}, {HD}] (got {tuple(c.shape)})")
+    _need(c.stride(2) == 1, f"{name} needs unit stride along head_dim")
+    return c.stride(0), c.stride(1), c.shape[0]
+
+
+def rope_tables(max_pos: int, hd: int, theta: float, device: torch.device | str,
+                dtype: torch.dtype = torch.bfloat16) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos/sin tables [max_pos, hd/2] for positions 0..max_pos-1.
+
+    Row p equals the first half of the reference's ``_cos_sin(p)`` row
+    (cuda_graph_executor.py:64-66, :95-98), built with the same torch
+    expression on the same device; the second half of that row repeats the
+    first because ``emb = cat(freqs, freqs)``.
+    """
+    inv_freq = 1.0 / (float(theta) ** (torch.arange(0, hd, 2, device=device).float() / hd))
+    freqs = torch.arange(max_pos, device=device)[:, None].float() * inv_freq[None, :]
+    return freqs.cos().to(dtype).contiguous(), freqs.sin().to(dtype).contiguous()
+
+
+def qknorm_rope_kvwrite(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps: float,
+                        cos_tab: torch.Tensor, sin_tab: torch.Tensor, pos0: torch.Tensor | None,
+                        q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                        nh: int, nkv: int) -> None:
+    """QK-RMSNorm + RoPE of T tokens at positions pos0..pos0+T-1, writing q_out and the caches.
+
+    pos0: int64 [1] on the device (None = position 0).  See solort_qknorm_rope_kvwrite.
+    """
+    _on_gpu("qkv", qkv, torch.bfloat16)
+    _need(qkv.dim() == 2 and qkv.shape[1] == (nh + 2 * nkv) * HD and qkv.stride(1) == 1,
+          f"qkv must be [T, {(nh + 2 * nkv) * HD}] with unit column stride")
+    T = qkv.shape[0]
+    for name, w in (("qn_w", qn_w), ("kn_w", kn_w)):
+        _on_gpu(name, w, torch.bfloat16)
+        _need(w.shape == (HD,) and w.is_contiguous(), f"{name} must be [{HD}] contiguous")
+    for name, tab in (("cos_tab", cos_tab), ("sin_tab", sin_tab)):
+        _on_gpu(name, tab, torch.bfloat16)
+        _need(tab.dim() == 2 and tab.shape[1] == HD // 2 and tab.is_contiguous(),
+              f"{name} must be [rows, {HD // 2}] contiguous")
+    _need(cos_tab.shape == sin_tab.shape, "cos_tab and sin_tab differ in shape")
+    _on_gpu("q_out", q_out, torch.bfloat16)
+    _need(q_out.shape == (T, nh, HD) and q_out.is_contiguous(), f"q_out must be [{T}, {nh}, {HD}]")
+    ts, hs, max_len = _cache_strides("k_cache", k_cache, nkv)
+    _need(v_cache.shape == k_cache.shape and v_cache.stride() == k_cache.stride(),
+          "v_cache must match k_cache in shape and strides")
+    _on_gpu("v_cache", v_cache, torch.bfloat16)
+    pos_ptr = None
+    if pos0 is not None:
+        _need(pos0.is_cuda and pos0.dtype == torch.int64 and pos0.numel() >= 1, "pos0 must be int64 on the device")
+        pos_ptr = pos0.data_ptr()
+    lib = _lib.load()
+    rc = lib.solort_qknorm_rope_kvwrite(
+        qkv.data_ptr(), qkv.stride(0), T, nh, nkv, HD, qn_w.data_ptr(), kn_w.data_ptr(), float(eps),
+        cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0], pos_ptr, q_out.data_ptr(),
+        k_cache.data_ptr(), v_cache.data_ptr(), ts, hs, max_len, _stream(qkv))
+    _lib.check(rc, "qknorm_rope_kvwrite")
+
+
+def attn_workspace(nq: int, nh: int, nkv: int, n_split: int, device: torch.device | str) -> torch.Tensor:
+    """Zero-filled workspace for decode_attn/verify_attn (allocate once, reuse)."""
+    nbytes = _lib.load().solort_attn_workspace_bytes(nq, nh, nkv, HD, n_split)
+    _need(nbytes > 0, f"bad workspace request nq={nq} nh={nh} nkv={nkv} n_split={n_split}")
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+
+def _attn(fn_name: str, q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+          pos0: torch.Tensor, bound: int, scale: float, ws: torch.Tensor, n_split: int,
+          out: torch.Tensor) -> None:
+    _on_gpu("q", q, torch.bfloat16)
+    _need(q.dim() == 3 and q.shape[2] == HD and q.is_contiguous(), "q must be [nq, nh, 128] contiguous")
+    nq, nh = q.shape[0], q.shape[1]
+    nkv = k_cache.shape[1] if k_cache.dim() == 3 else -1
+    ts, hs, max_len = _cache_strides("k_cache", k_cache, nkv)
+    _on_gpu("v_cache", v_cache, torch.bfloat16)
+    _need(v_cache.shape == k_cache.shape and v_cache.stride() == k_cache.stride(),
+          "v_cache must match k_cache in shape and strides")
+    _need(pos0.is_cuda and pos0.dtype == torch.int64 and pos0.numel() >= 1, "pos0 must be int64 on the device")
+    _need(out.is_cuda and out.dtype in (torch.bfloat16, torch.float32), "out must be bf16 or fp32 on the device")
+    _need(out.shape == (nq, nh * HD) and out.is_contiguous(), f"out must be [{nq}, {nh * HD}] contiguous")
+    _need(out.data_ptr() % 16 == 0, "out must be 16-byte aligned")
+    lib = _lib.load()
+    need = lib.solort_attn_workspace_bytes(nq, nh, nkv, HD, n_split)
+    _need(ws.is_cuda and ws.numel() * ws.element_size() >= need and ws.data_ptr() % 16 == 0,
+          f"workspace too small: need {need} bytes")
+    dt = DTYPE_F32 if out.dtype == torch.float32 else DTYPE_BF16
+    rc = getattr(lib, fn_name)(
+        q.data_ptr(), nq, nh, nkv, HD, k_cache.data_ptr(), v_cache.data_ptr(), ts, hs, max_len,
+        pos0.data_ptr(), int(bound), float(scale), ws.data_ptr(), int(n_split), out.data_ptr(), dt,
+        _stream(q))
+    _lib.check(rc, fn_name)
+
+
+def decode_attn(q, k_cache, v_cache, pos0, bound, scale, ws, n_split, out) -> None:
+    """Single-token (or few-token) GQA attention over cache rows 0..pos0+nq-1; see solort_decode_attn."""
+    _attn("solort_decode_attn", q, k_cache, v_cache, pos0, bound, scale, ws, n_split, out)
+
+
+def verify_attn(q, k_cache, v_cache, pos0, bound, scale, ws, n_split, out) -> None:
+    """K+1 query tokens at pos0..pos0+K, each causal over the cache; see solort_verify_attn."""
+    _attn("solort_verify_attn", q, k_cache, v_cache, pos0, bound, scale, ws, n_split, out)
+
+
+def argmax_workspace(rows: int, device: torch.device | str) -> torch.Tensor:
+    """Zero-filled workspace for argmax_rows (allocate once, reuse)."""
+    nbytes = _lib.load().solort_argmax_workspace_bytes(rows)
+    _need(nbytes > 0, f"bad argmax workspace request rows={rows}")
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+
+def argmax_rows(logits: torch.Tensor, out: torch.Tensor, ws: torch.Tensor) -> None:
+    """out[r] = index of the max of logits[r] (lowest index on ties, NaN is max)."""
+    _need(logits.is_cuda, f"logits must be a ROCm device tensor (got {logits.device})")
+    _need(logits.dtype in (torch.bfloat16, torch.float32), f"logits must be bf16 or fp32 (got {logits.dtype})")
+    _need(logits.dim() == 2 and logits.stride(1) == 1, "logits must be [rows, vocab] with unit column stride")
+    rows, vocab = logits.shape
+    _need(out.is_cuda and out.dtype == torch.int64 and out.shape == (rows,) and out.is_contiguous(),
+          f"out must be int64 [{rows}] on the device")
+    lib = _lib.load()
+    need = lib.solort_argmax_workspace_bytes(rows)
+    _need(ws.is_cuda and ws.numel() * ws.element_size() >= need and ws.data_ptr() % 16 == 0,
+          f"argmax workspace too small: need {need} bytes")
+    dt = DTYPE_F32 if logits.dtype == torch.float32 else DTYPE_BF16
+    rc = lib.solort_argmax_rows(logits.data_ptr(), dt, rows, vocab, logits.stride(0), out.data_ptr(),
+                                ws.data_ptr(), _stream(logits))
+    _lib.check(rc, "argmax_rows")

@@ -1,0 +1,98 @@
+"""C-ABI checks that need no GPU: the library loads, exports every function the
+header declares with the bound signature, and rejects bad arguments before any
+launch.  The torch front end refuses CPU tensors (no CPU fallback)."""
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+import torch
+
+from solort_amd import _lib, ops
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "solort_hip.h"
+EINVAL = -22
+
+
+def _declared() -> list[str]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(solort_[a-z0-9_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_header_and_binding_agree():
+    assert _declared() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    for name in _declared():
+        assert hasattr(lib, name), name
+    assert lib.solort_abi_version() == _lib.ABI_VERSION
+
+
+def test_workspace_sizes(lib):
+    n = lib.solort_attn_workspace_bytes(1, 32, 8, 128, 32)
+    # partial outputs [8][32][4][128] fp32 + (max, sum) + 8 tickets
+    assert n >= 8 * 32 * 4 * 128 * 4 + 8 * 32 * 4 * 2 * 4 + 8 * 4
+    assert n % 256 == 0
+    assert lib.solort_attn_workspace_bytes(1, 32, 8, 64, 32) == 0
+    assert lib.solort_attn_workspace_bytes(1, 30, 8, 128, 32) == 0
+    assert lib.solort_argmax_workspace_bytes(5) >= 5 * 12
+    assert lib.solort_argmax_workspace_bytes(0) == 0
+
+
+def _err(lib) -> str:
+    return lib.solort_last_error().decode()
+
+
+def test_decode_rejects_bad_arguments_without_launching(lib):
+    p = ctypes.c_void_p(16 * 1024)  # never dereferenced: validation fails first
+    args = dict(q=p, nq=1, nh=32, nkv=8, hd=128, k=p, v=p, ts=1024, hs=128, max_len=1024, pos=p,
+                bound=1024, scale=0.088, ws=p, n_split=32, out=p, dt=0, stream=None)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return lib.solort_decode_attn(a["q"], a["nq"], a["nh"], a["nkv"], a["hd"], a["k"], a["v"], a["ts"],
+                                      a["hs"], a["max_len"], a["pos"], a["bound"], a["scale"], a["ws"],
+                                      a["n_split"], a["out"], a["dt"], a["stream"])
+
+    assert call(hd=64) == EINVAL and "head_dim" in _err(lib)
+    assert call(nh=30) == EINVAL
+    assert call(nh=24, nkv=8) == EINVAL and "group" in _err(lib)
+    assert call(nq=9) == EINVAL
+    assert call(bound=2048) == EINVAL and "bound" in _err(lib)
+    assert call(n_split=0) == EINVAL
+    assert call(ts=1004) == EINVAL
+    assert call(q=ctypes.c_void_p(16 * 1024 + 2)) == EINVAL and "aligned" in _err(lib)
+    assert call(pos=None) == EINVAL
+    assert call(dt=7) == EINVAL
+
+
+def test_prologue_and_argmax_reject_bad_arguments(lib):
+    p = ctypes.c_void_p(4096)
+    rc = lib.solort_qknorm_rope_kvwrite(p, 6144, 1, 32, 8, 100, p, p, 1e-6, p, p, 1024, None, p, p, p,
+                                        1024, 128, 1024, None)
+    assert rc == EINVAL and "head_dim" in _err(lib)
+    rc = lib.solort_qknorm_rope_kvwrite(p, 6000, 1, 32, 8, 128, p, p, 1e-6, p, p, 1024, None, p, p, p,
+                                        1024, 128, 1024, None)
+    assert rc == EINVAL and "stride" in _err(lib)
+    rc = lib.solort_argmax_rows(p, 3, 1, 10, 10, p, p, None)
+    assert rc == EINVAL and "dtype" in _err(lib)
+    rc = lib.solort_argmax_rows(p, 0, 1, 10, 5, p, p, None)
+    assert rc == EINVAL
+
+
+def test_torch_front_end_refuses_cpu_tensors():
+    q = torch.zeros(1, 32, 128, dtype=torch.bfloat16)
+    kc = torch.zeros(1024, 8, 128, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        ops.decode_attn(q, kc, kc, torch.zeros(1, dtype=torch.long), 1024, 0.088,
+                        torch.zeros(1 << 20, dtype=torch.uint8), 32, torch.zeros(1, 4096))
+    with pytest.raises(RuntimeError, match="ROCm device"):
+        ops.argmax_rows(torch.zeros(1, 10), torch.zeros(1, dtype=torch.long), torch.zeros(512, dtype=torch.uint8))

@@ -1,0 +1,286 @@
+"""Pins the CPU oracle (oracle/ref.py, oracle/exact.py) with checks that do not
+retype its formulas: fp64 closed forms, invariants, special cases and brute
+force, plus the reference's own bottom-right-causal test inputs."""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import exact, ref
+from solort_amd import workloads as wl
+
+HD = 128
+SCALE = HD ** -0.5
+
+
+def _bf(t):
+    return t.to(torch.bfloat16)
+
+
+# ------------------------------------------------------------------ rmsnorm
+
+def test_rmsnorm_matches_fp64_closed_form():
+    g = torch.Generator().manual_seed(1)
+    x = _bf(torch.randn(64, HD, generator=g) * 3)
+    w = _bf(1 + 0.1 * torch.randn(HD, generator=g))
+    y = ref.rmsnorm(x, w, 1e-6).float().numpy()
+    xd = x.double().numpy()
+    want = xd / np.sqrt((xd ** 2).mean(-1, keepdims=True) + 1e-6) * w.double().numpy()
+    # one bf16 rounding of the result: relative error <= 2^-8
+    assert np.all(np.abs(y - want) <= np.abs(want) * 2.0 ** -8 + 1e-30)
+
+
+def test_rmsnorm_constant_row_gives_signed_weight():
+    w = _bf(torch.linspace(0.5, 1.5, HD))
+    for c in (3.0, -0.25, 17.0):
+        x = _bf(torch.full((1, HD), c))
+        y = ref.rmsnorm(x, w, 0.0)
+        want = _bf(math.copysign(1.0, c) * w.float())
+        assert torch.equal(y[0], want)
+
+
+def test_rmsnorm_scale_invariant_by_power_of_two():
+    g = torch.Generator().manual_seed(2)
+    x = _bf(torch.randn(32, HD, generator=g))
+    w = _bf(1 + 0.1 * torch.randn(HD, generator=g))
+    assert torch.equal(ref.rmsnorm(x, w, 0.0), ref.rmsnorm(_bf(x.float() * 8), w, 0.0))
+
+
+def test_fixed_order_rmsnorm_agrees_with_torch_restatement():
+    """Same math, different (unspecified in torch) sum order: equal except rare 1-ulp flips."""
+    g = torch.Generator().manual_seed(3)
+    x = _bf(torch.randn(4096, HD, generator=g))
+    w = _bf(1 + 0.1 * torch.randn(HD, generator=g))
+    a = ref.rmsnorm(x, w, 1e-6).float().numpy()
+    b = exact.rmsnorm_fixed_order(x.float().numpy(), w.float().numpy(), 1e-6)
+    diff = a != b
+    assert diff.mean() < 1e-3
+    if diff.any():
+        ulp = np.abs(exact.bf16_round(a[diff] * (1 + 2.0 ** -7)) - a[diff])
+        assert np.all(np.abs(a[diff] - b[diff]) <= ulp * 1.01)
+
+
+def test_fixed_order_sum_is_a_valid_fp32_sum():
+    g = np.random.default_rng(4)
+    x = exact.bf16_round(g.standard_normal((1000, HD)).astype(np.float32))
+    s = exact.sum_squares_fixed_order(x)
+    want = (x.astype(np.float64) ** 2).sum(-1)
+    assert np.allclose(s, want, rtol=2e-6)
+
+
+# ------------------------------------------------------------------ rope
+
+def test_rope_position_zero_is_identity():
+    g = torch.Generator().manual_seed(5)
+    x = _bf(torch.randn(8, 3, HD, generator=g))
+    cos, sin = ref.cos_sin(torch.zeros(3, dtype=torch.long), ref.inv_freq(HD, 1e6), torch.bfloat16)
+    assert torch.equal(ref.rope(x, cos, sin), x)
+
+
+def test_inv_freq_closed_form():
+    f = ref.inv_freq(HD, 1e6).double().numpy()
+    want = 1e6 ** (-np.arange(0, HD, 2) / HD)
+    assert np.allclose(f, want, rtol=1e-6)
+    assert f[0] == 1.0
+
+
+def test_rope_rotation_preserves_pair_norms_and_relative_position():
+    """In fp32, rotating pairs (i, i+64) keeps their norm, and q.k after rotation depends on p'-p only."""
+    g = torch.Generator().manual_seed(6)
+    q = torch.randn(HD, generator=g)
+    k = torch.randn(HD, generator=g)
+    inv = ref.inv_freq(HD, 1e6)
+
+    def rot(x, p):
+        c, s = ref.cos_sin(torch.tensor([p]), inv, torch.float32)
+        return ref.rope(x[None], c, s)[0]
+
+    for p in (1, 37, 1000):
+        r = rot(q, p)
+        assert torch.allclose(r[:64] ** 2 + r[64:] ** 2, q[:64] ** 2 + q[64:] ** 2, rtol=1e-4, atol=1e-5)
+    d1 = torch.dot(rot(q, 10), rot(k, 13))
+    d2 = torch.dot(rot(q, 500), rot(k, 503))
+    assert abs(d1 - d2) < 1e-3 * (1 + abs(d1))
+    # dropping the negation in rotate_half breaks the relative-position property
+    def bad_rot(x, p):
+        c, s = ref.cos_sin(torch.tensor([p]), inv, torch.float32)
+        return x * c[0] + torch.cat((x[64:], x[:64])) * s[0]
+    assert abs(torch.dot(bad_rot(q, 10), bad_rot(k, 13)) - torch.dot(bad_rot(q, 500), bad_rot(k, 503))) > 1e-2
+
+
+def test_fixed_order_prologue_agrees_with_torch_restatement():
+    case = wl.decode_case(4, layers=1)
+    sh = case.shape
+    pos = torch.arange(case.pos, case.pos + case.nq)
+    cos, sin = ref.cos_sin(pos, ref.inv_freq(HD, wl.THETA), torch.bfloat16)
+    q, k, v = ref.prologue(case.qkv[0], case.qn_w[0], case.kn_w[0], wl.EPS, cos, sin, sh.nh, sh.nkv)
+    q2, k2, v2 = exact.prologue_fixed_order(case.qkv[0].float().numpy(), case.qn_w[0].float().numpy(),
+                                            case.kn_w[0].float().numpy(), wl.EPS,
+                                            cos[:, :64].float().numpy(), sin[:, :64].float().numpy(),
+                                            sh.nh, sh.nkv)
+    assert np.array_equal(v.transpose(0, 1).float().numpy(), v2)
+    for a, b in ((q, q2), (k, k2)):
+        a = a.transpose(0, 1).float().numpy()
+        assert (a != b).mean() < 2e-3
+        assert np.max(np.abs(a - b)) <= 2.0 ** -6 * max(1.0, np.abs(a).max())
+
+
+def test_bf16_rounding_matches_torch():
+    g = np.random.default_rng(7)
+    x = np.concatenate([g.standard_normal(10000).astype(np.float32) * 10,
+                        np.array([np.inf, -np.inf, np.nan, 0.0, -0.0, 1e-40, 3.3895314e38], np.float32)])
+    want = torch.from_numpy(x).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+    got = exact.bf16_bits(x)
+    nan = np.isnan(x)
+    # NaN payloads differ between torch's scalar (0x7FC0) and vector CPU paths; NaN-ness must not
+    assert np.array_equal(got[~nan], want[~nan])
+    assert np.all(np.isnan(exact.bf16_to_f32(got[nan]))) and np.all(got[nan] == 0x7FC0)
+
+
+# ------------------------------------------------------------------ decode
+
+def _small_cache(seed, L, nkv, max_len=None, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    max_len = max_len or L
+    kc = torch.randn(max_len, nkv, HD, generator=g).to(dtype)
+    vc = torch.randn(max_len, nkv, HD, generator=g).to(dtype)
+    return kc, vc
+
+
+@pytest.mark.parametrize("nh,nkv", [(16, 8), (32, 8)])
+def test_decode_ref_matches_fp64_bruteforce(nh, nkv):
+    kc, vc = _small_cache(8, 256, nkv)
+    q = torch.randn(nh, 1, HD, generator=torch.Generator().manual_seed(9))
+    pos, bound = 200, 256
+    got = ref.decode_attn(q, kc, vc, pos, bound, SCALE).double().numpy().reshape(nh, HD)
+    want = exact.causal_decode_fp64(q.transpose(0, 1).numpy(), kc.numpy(), vc.numpy(), pos, SCALE)[0]
+    assert np.allclose(got, want, atol=2e-6)
+
+
+def test_decode_single_key_returns_v0():
+    kc, vc = _small_cache(10, 128, 8, dtype=torch.bfloat16)
+    q = _bf(torch.randn(32, 1, HD))
+    out = ref.decode_attn(q, kc, vc, 0, 128, SCALE).reshape(32, HD)
+    assert torch.equal(out, vc[0].repeat_interleave(4, 0))
+
+
+def test_decode_equal_keys_give_mean_of_values():
+    kc, vc = _small_cache(11, 64, 8)
+    kc[:] = kc[0]
+    q = torch.randn(32, 1, HD)
+    out = ref.decode_attn(q, kc, vc, 63, 64, SCALE).reshape(32, HD)
+    want = vc.mean(0).repeat_interleave(4, 0)
+    assert torch.allclose(out, want, atol=1e-5)
+
+
+def test_decode_dominant_key_selects_its_value_row():
+    kc, vc = _small_cache(12, 64, 8)
+    q = torch.randn(32, 1, HD)
+    qg = q.reshape(8, 4, HD)
+    kc[17] = qg.mean(1) * 1000
+    out = ref.decode_attn(q, kc, vc, 63, 64, SCALE).reshape(8, 4, HD)
+    assert torch.allclose(out, vc[17][:, None, :].expand(8, 4, HD), atol=1e-4)
+
+
+def test_decode_invariant_under_key_permutation_and_bucket():
+    kc, vc = _small_cache(13, 256, 8)
+    q = torch.randn(32, 1, HD)
+    base = ref.decode_attn(q, kc, vc, 150, 256, SCALE)
+    perm = torch.randperm(151, generator=torch.Generator().manual_seed(1))
+    kc2, vc2 = kc.clone(), vc.clone()
+    kc2[:151], vc2[:151] = kc[perm], vc[perm]
+    assert torch.allclose(ref.decode_attn(q, kc2, vc2, 150, 256, SCALE), base, atol=1e-5)
+    # a larger bucket only adds masked keys
+    assert torch.allclose(ref.decode_attn(q, kc, vc, 150, 151, SCALE), base, atol=1e-6)
+
+
+def test_grouped_map_equals_repeat_interleave():
+    kc, vc = _small_cache(14, 96, 8)
+    q = torch.randn(32, 1, HD)
+    out = ref.decode_attn(q, kc, vc, 95, 96, SCALE)
+    kk = kc.permute(1, 0, 2).repeat_interleave(4, 0)
+    vv = vc.permute(1, 0, 2).repeat_interleave(4, 0)
+    want = torch.softmax((q @ kk.transpose(1, 2)) * SCALE, -1) @ vv
+    assert torch.allclose(out, want.reshape(1, -1), atol=1e-5)
+
+
+@pytest.mark.parametrize("L,n_split", [(1, 4), (100, 1), (513, 16), (1024, 32), (3000, 7)])
+def test_splitkv_combine_equals_unsplit(L, n_split):
+    g = np.random.default_rng(L)
+    q = g.standard_normal((4, HD))
+    keys = g.standard_normal((L, HD))
+    vals = g.standard_normal((L, HD))
+    keys[::50] *= 8
+    a = exact.splitkv_combine(q, keys, vals, SCALE, n_split)
+    b = exact.attn_fp64(q, keys, vals, SCALE)
+    assert np.allclose(a, b, atol=1e-12)
+
+
+# ------------------------------------------------------------------ prefill / verify
+
+def test_prefill_ref_rows_pinned():
+    g = torch.Generator().manual_seed(15)
+    T, nh, nkv = 64, 32, 8
+    q = torch.randn(nh, T, HD, generator=g)
+    k = torch.randn(nkv, T, HD, generator=g)
+    v = torch.randn(nkv, T, HD, generator=g)
+    out = ref.prefill_attn(q, k, v, SCALE).reshape(T, nh, HD)
+    assert torch.allclose(out[0], v[:, 0].repeat_interleave(4, 0), atol=1e-6)
+    # last row == decode at position T-1 over the same cache
+    kc, vc = k.transpose(0, 1).contiguous(), v.transpose(0, 1).contiguous()
+    dec = ref.decode_attn(q[:, T - 1:T], kc, vc, T - 1, T, SCALE).reshape(nh, HD)
+    assert torch.allclose(out[T - 1], dec, atol=1e-5)
+    # every row equals the fp64 brute force over its causal prefix
+    want = exact.causal_decode_fp64(q.transpose(0, 1).numpy(), kc.numpy(), vc.numpy(), 0, SCALE)
+    assert np.allclose(out.double().numpy(), want, atol=1e-5)
+
+
+def test_verify_equals_sequential_decode_steps():
+    kc, vc = _small_cache(16, 300, 8, max_len=320)
+    q = torch.randn(32, 5, HD)
+    pos0 = 250
+    out = ref.verify_attn(q, kc, vc, pos0, SCALE).reshape(5, 32, HD)
+    for t in range(5):
+        dec = ref.decode_attn(q[:, t:t + 1], kc, vc, pos0 + t, 320, SCALE).reshape(32, HD)
+        assert torch.allclose(out[t], dec, atol=1e-5)
+
+
+def test_verify_mask_is_bottom_right_causal_on_reference_test_inputs():
+    """tests/test_transformers_flashinfer.py:20-48 inputs: seed 0, q [1,2,3,8], k/v [1,2,7,8]; the query
+    block sits at the end of the cache, so query i sees keys 0..4+i (atol 1e-5)."""
+    torch.manual_seed(0)
+    q = torch.randn(1, 2, 3, 8)
+    k = torch.randn(1, 2, 7, 8)
+    v = torch.randn(1, 2, 7, 8)
+    scale = 1.0 / math.sqrt(8)
+    # verify_attn with pos0 = kv_len - q_len over a 7-row cache, 2 heads, group 1
+    got = ref.verify_attn(q[0], k[0].transpose(0, 1), v[0].transpose(0, 1), 4, scale).reshape(3, 2, 8)
+    scores = (q @ k.transpose(-1, -2)) * scale
+    allowed = torch.arange(7)[None, :] <= (torch.arange(3)[:, None] + 4)
+    want = (torch.softmax(scores.masked_fill(~allowed, float("-inf")), -1) @ v)[0].transpose(0, 1)
+    assert torch.allclose(got, want, atol=1e-5)
+    topleft = torch.nn.functional.scaled_dot_product_attention(q, k, v, is_causal=True, scale=scale)
+    assert not torch.allclose(got, topleft[0].transpose(0, 1), atol=1e-3)
+
+
+# ------------------------------------------------------------------ argmax
+
+def test_argmax_first_index_on_ties_and_nan():
+    x = np.array([[1, 5, 5, 2], [0, -0.0, 0, -1], [1, np.nan, 9, np.nan], [-np.inf] * 4], np.float32)
+    assert list(exact.argmax_first(x)) == [1, 0, 1, 0]
+    assert list(ref.argmax(torch.from_numpy(x))) == [1, 0, 1, 0]
+
+
+def test_planted_logits_answer_is_smallest_plant():
+    g = torch.Generator().manual_seed(1004)
+    x = wl.planted_logits(g, 5, wl.VOCAB)
+    idx = exact.argmax_first(x.float().numpy())
+    top = x.float().max(-1).values
+    for r in range(5):
+        plants = torch.nonzero(x[r].float() == top[r]).flatten()
+        assert len(plants) >= 2 and idx[r] == plants.min() and plants.min() < 1024
+        assert plants.max() >= wl.VOCAB - 1024
+    assert torch.equal(ref.argmax(x), torch.from_numpy(idx))
