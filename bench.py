@@ -1,0 +1,232 @@
+"""Benchmark of the gfx950 attention hot path on one MI355X.
+
+Step = one graph replay of a Qwen3-4B decode step's attention block at KV
+length 1024: for each of 36 layers, the QK-RMSNorm + RoPE prologue with the
+KV write, then split-KV GQA decode attention (32 q / 8 kv heads, head_dim
+128, bf16), then the greedy argmax over a 151,936-entry logits row.  The
+reported value is microseconds per layer.  Eight independent KV caches
+(1.2 GB) are rotated so that every step reads its KV from HBM, not from the
+256 MB infinity cache.
+
+Alongside: the time of one decode-attention call (the split-KV kernel and its
+combine kernel; HIP events around graph replays of 36 x 8 calls over distinct
+KV slices) against the HBM roofline, prefill attention TFLOP/s when the
+prefill kernel is built, and the CPU baseline: the oracle's fp32 torch
+restatement of the reference path timed on the host cores.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def decode_bytes(live: int, nh: int = 32, nkv: int = 8, hd: int = 128) -> int:
+    """Algorithmic HBM bytes of one decode-attention launch: K and V rows 0..live-1 of every KV head,
+    plus q in and the output out (bf16)."""
+    return 2 * nkv * live * hd * 2 + 2 * nh * hd * 2
+
+
+def prefill_flops(T: int, nh: int = 32, hd: int = 128) -> int:
+    """Causal attention flops: 2 matmuls x 2 flop x nh x hd over the T(T+1)/2 visible pairs."""
+    return 4 * nh * hd * T * (T + 1) // 2
+
+
+def parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=200)
+    p.add_argument("--warmup", type=int, default=20)
+    p.add_argument("--live", type=int, default=1024, help="KV live length of the decode workload")
+    p.add_argument("--kv-sets", type=int, default=8, help="independent KV caches rotated per step")
+    p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
+    p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    p.add_argument("--no-sweep", action="store_true", help="skip the per-bucket and prefill extras")
+    return p.parse_args()
+
+
+def main() -> int:
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no multi-GPU path; "
+              "each GPU would run its own KV heads or key splits (see DESIGN.md).", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from solort_amd import ops
+    from solort_amd import workloads as wl
+    from solort_amd.runner import GraphQwen3Attention, decode_splits
+
+    dev = torch.device("cuda:0")
+    sh = wl.QWEN3_4B
+    live = int(args.live)
+    pos = live - 1
+    bound = next(b for b in (128, 256, 512, 1024) if b > pos) if live <= 1024 else live
+    max_len = max(1024, bound)
+    gen = torch.Generator(device=dev).manual_seed(1001)
+
+    def rnd(*shape, std=1.0, mean=0.0):
+        return (torch.randn(*shape, generator=gen, device=dev) * std + mean).to(torch.bfloat16)
+
+    qn_w = rnd(sh.layers, 128, std=0.1, mean=1.0)
+    kn_w = rnd(sh.layers, 128, std=0.1, mean=1.0)
+    runners = []
+    for _ in range(args.kv_sets):
+        r = GraphQwen3Attention(sh.nh, sh.nkv, sh.layers, max_len, qn_w, kn_w, device=dev)
+        r.kc[:, :pos].copy_(rnd(sh.layers, pos, sh.nkv, 128))
+        r.vc[:, :pos].copy_(rnd(sh.layers, pos, sh.nkv, 128))
+        r.qkv_dec.copy_(rnd(sh.layers, 1, sh.qkv_width))
+        r.logits_dec.copy_(torch.randn(1, wl.VOCAB, generator=gen, device=dev) * 3)
+        r.pos_buf.fill_(pos)
+        r._capture(bound)
+        runners.append(r)
+    torch.cuda.synchronize()
+
+    # ---------------------------------------------------------------- timed graph replays
+    for i in range(args.warmup):
+        runners[i % len(runners)]._graphs[bound].replay()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        runners[i % len(runners)]._graphs[bound].replay()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = wall * 1e3 / args.steps
+    us_per_layer = ms_per_step * 1e3 / sh.layers
+
+    # ---------------------------------------------------------------- decode kernel alone (roofline)
+    ns = decode_splits(bound, sh.nkv)
+    kern_us = time_decode_kernel(torch, ops, runners, bound, ns, sh, dev, reps=4)
+    kbytes = decode_bytes(live, sh.nh, sh.nkv)
+    achieved = kbytes / (kern_us * 1e-6) / 1e9
+
+    result = {
+        "metric": "decode-attn us/layer + HBM GB/s (Qwen3-4B, KV 1024); prefill attn TFLOP/s",
+        "value": round(us_per_layer, 4),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,1) KV/qkv, norm weights N(1,0.1), logits N(0,3))",
+        "config": {"workload": f"Qwen3-4B decode attention, batch 1, 32q/8kv heads, head_dim 128, "
+                               f"KV live {live} (bucket {bound}), 36 layers per step, {args.kv_sets} rotated "
+                               f"KV sets", "live": live, "bucket": bound, "layers": sh.layers,
+                   "n_split": ns},
+        "decode_gbps": round(kbytes / (us_per_layer * 1e-6) / 1e9, 1),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "solort_decode_layer = decode_kernel<1,4,2,fused> + combine_kernel<1,4>",
+                     "kernel_us": round(kern_us, 3),
+                     "algorithmic_bytes": kbytes},
+    }
+
+    if not args.no_sweep:
+        result["extras"] = extras(torch, ops, wl, runners, dev, sh)
+
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, live)
+
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def time_decode_kernel(torch, ops, runners, bound, ns, sh, dev, reps=3, pos=None) -> float:
+    """Mean time (us) of one solort_decode_layer call (its split-KV kernel plus its combine kernel),
+    from HIP events around replays of a graph holding one call per layer of every KV set, so each
+    call reads a distinct KV slice from HBM.  Each call rewrites the new token's K/V row with the same
+    bits."""
+    stream = torch.cuda.current_stream(dev)
+    ws = ops.attn_workspace(1, sh.nh, sh.nkv, ns, dev)
+    out = torch.empty(1, sh.nh * 128, dtype=torch.bfloat16, device=dev)
+    order = [(r, li) for r in runners for li in range(sh.layers)]
+
+    def run_all():
+        for r, li in order:
+            ops.decode_layer(r.qkv_dec[li], r.qn_w[li], r.kn_w[li], r.eps, r.inv_freq,
+                             r.pos_buf if pos is None else pos, r.kc[li], r.vc[li], bound, sh.scale, ws, ns, out,
+                             sh.nh, sh.nkv)
+
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        run_all()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * len(order))
+
+
+def extras(torch, ops, wl, runners, dev, sh) -> dict:
+    """Decode attention call times per bucket (same rotation), and a split-count sweep at KV 1024."""
+    from solort_amd.runner import decode_splits
+
+    out: dict = {"decode_call_us": {}, "n_split_sweep_kv1024": {}}
+    for live in (128, 256, 512, 1024):
+        ns = decode_splits(live, sh.nkv)
+        pos = torch.tensor([live - 1], dtype=torch.long, device=dev)
+        us = time_decode_kernel(torch, ops, runners, live, ns, sh, dev, reps=3, pos=pos)
+        gbs = decode_bytes(live) / (us * 1e-6) / 1e9
+        out["decode_call_us"][str(live)] = {"us": round(us, 3), "gbps": round(gbs, 1),
+                                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "n_split": ns}
+    pos = torch.tensor([1023], dtype=torch.long, device=dev)
+    for ns in (8, 16, 32, 64, 128):
+        us = time_decode_kernel(torch, ops, runners, 1024, ns, sh, dev, reps=3, pos=pos)
+        out["n_split_sweep_kv1024"][str(ns)] = round(us, 3)
+    return out
+
+
+def cpu_baseline(budget_s: float, live: int) -> dict:
+    """The oracle's fp32 torch restatement of the reference's decode attention block
+    (prologue + KV write + grouped attention, 36 layers) on the host cores."""
+    import torch
+
+    from oracle import ref
+    from solort_amd import workloads as wl
+
+    cores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(cores)
+    sh = wl.QWEN3_4B
+    case = wl.decode_case(1, live=live, layers=sh.layers, dtype=torch.float32)
+    cos, sin = ref.cos_sin(torch.tensor([case.pos]), ref.inv_freq(128, wl.THETA), torch.float32)
+    times = []
+    t_end = time.perf_counter() + budget_s
+    n = 0
+    while n < 5 or (time.perf_counter() < t_end and n < 200):
+        t0 = time.perf_counter_ns()
+        ref.decode_layers(case.qkv, case.qn_w, case.kn_w, wl.EPS, cos, sin, case.kc, case.vc, case.pos,
+                          case.bound, sh.nh, sh.nkv, sh.scale)
+        times.append((time.perf_counter_ns() - t0) / 1e3)
+        n += 1
+    steady = times[2:] if len(times) > 4 else times
+    us_layer = statistics.median(steady) / sh.layers
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"value": round(us_layer, 2), "unit": "us/layer", "cores": cores, "kind": "port",
+            "sample": f"{len(times)} decode steps (36 layers, Qwen3-4B, KV live {live}) in fp32 torch on "
+                      f"{cores} threads of '{model}'; median per step / 36"}
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -58,35 +58,46 @@ const char* solort_last_error(void);
  * qkv      [T, (nh + 2*nkv) * 128] bf16, row stride `qkv_row_stride` elements
  *          (the fused QKV projection output, q | k | v column blocks).
  * qn_w, kn_w [128] bf16 (q_norm / k_norm weights).
- * cos_tab, sin_tab [tab_rows, 64] bf16: row p holds cos/sin of p * inv_freq,
- *          i.e. the first half of the reference's _cos_sin row (:95-98); the
- *          second half of that row is identical.
+ * inv_freq [64] fp32 RoPE frequencies as the reference computes them (:64-66);
+ *          cos/sin of pos * inv_freq are evaluated on the device, with the
+ *          same values solort_rope_table produces.
  * pos0_dev int64 on the device: token t sits at position *pos0_dev + t
  *          (NULL means position 0, the prefill case, :111).
  * q_out    [T, nh, 128] bf16.
  * k_cache, v_cache: this layer's cache; row `pos`, head h starts at
  *          pos * kv_tok_stride + h * kv_head_stride.
- * Positions outside [0, min(max_len, tab_rows)) are skipped on the device.
+ * Positions outside [0, max_len) are not written.
  * The K/V rows written are bit-exact with the reference's op sequence given
- * the same cos/sin table; the sum of squares uses a fixed reduction order.
+ * the same cos/sin values; the sum of squares uses a fixed reduction order.
  */
 int solort_qknorm_rope_kvwrite(const void* qkv, int64_t qkv_row_stride, int T, int nh, int nkv,
                                int hd, const void* qn_w, const void* kn_w, float eps,
-                               const void* cos_tab, const void* sin_tab, int64_t tab_rows,
-                               const int64_t* pos0_dev, void* q_out, void* k_cache, void* v_cache,
-                               int64_t kv_tok_stride, int64_t kv_head_stride, int64_t max_len,
-                               solort_stream_t stream);
+                               const float* inv_freq, const int64_t* pos0_dev, void* q_out,
+                               void* k_cache, void* v_cache, int64_t kv_tok_stride,
+                               int64_t kv_head_stride, int64_t max_len, solort_stream_t stream);
 
-/* Workspace bytes needed by solort_decode_attn / solort_verify_attn for
- * `nq` query tokens and `n_split` key splits.  The caller allocates it once,
- * zero-fills it once, and reuses it: the kernels leave it ready for the next
- * call.  Calls that overlap in time must not share a workspace. */
+/*
+ * RoPE table on the device: cos_out/sin_out [rows, half_dim] bf16 with row p
+ * = bf16(cos/sin(float(p) * inv_freq[i])), the first half of the reference's
+ * _cos_sin(p) row (cuda_graph_executor.py:95-98); inv_freq [half_dim] fp32 as
+ * the reference computes it (:64-66).
+ */
+int solort_rope_table(const float* inv_freq, int half_dim, int64_t rows, void* cos_out, void* sin_out,
+                      solort_stream_t stream);
+
+/* Workspace bytes needed by solort_decode_attn / solort_verify_attn /
+ * solort_decode_layer for `nq` query tokens and `n_split` key splits.  The
+ * caller allocates it once, zero-fills it once, and reuses it: the kernels
+ * leave it ready for the next call.  A workspace sized for (nq, n_split)
+ * serves any call with the same nh/nkv and no larger nq or n_split.  Calls
+ * that overlap in time must not share a workspace. */
 size_t solort_attn_workspace_bytes(int nq, int nh, int nkv, int hd, int n_split);
 
 /*
  * Grouped-query attention of `nq` new tokens over the static KV cache, split
- * across `n_split` workgroups per KV head (flash-decoding) with the
- * log-sum-exp combine fused into the same launch.
+ * across `n_split` workgroups per KV head (flash-decoding), followed by the
+ * log-sum-exp combine of the splits (a second launch on the same stream, or,
+ * with SOLORT_DECODE_COMBINE=ticket, inside the first launch).
  * Replaces the decode block cuda_graph_executor.py:168, :180-184 (nq = 1:
  * softmax(q K^T * scale, keys > pos masked) V over the bucket) and the verify
  * block :247-250, :261-263 (nq = K+1, query t at position pos0+t sees keys
@@ -106,12 +117,34 @@ int solort_decode_attn(const void* q, int nq, int nh, int nkv, int hd, const voi
 
 /* Speculative-verify attention (cuda_graph_executor.py:245-263): the same
  * kernel as solort_decode_attn with nq = K+1 query tokens at positions
- * pos0..pos0+K, each causal over the cache.  Only the live keys
- * 0..pos0+K are read (the reference scans all max_len keys with a mask). */
+ * pos0..pos0+K, each causal over the cache (the reference scans all max_len
+ * keys under a mask; here `bound` may be any bucket >= pos0+K+1).
+ *
+ * For both entry points the key range [0, bound) is cut into n_split static
+ * chunks whose first step is loaded before the position is known, so keys
+ * between the live length and `bound` may be fetched and discarded: pass the
+ * tightest bucket. */
 int solort_verify_attn(const void* q, int nq, int nh, int nkv, int hd, const void* k_cache,
                        const void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride,
                        int64_t max_len, const int64_t* pos0_dev, int bound, float scale, void* ws,
                        int n_split, void* out, int out_dtype, solort_stream_t stream);
+
+/*
+ * The whole per-layer attention block: QK-RMSNorm + RoPE of the new tokens'
+ * q/k rows, the KV-cache write of their K/V rows, and the split-KV attention
+ * in one launch, then the combine of the splits as in solort_decode_attn.  Replaces, per layer,
+ * cuda_graph_executor.py:173-184 (decode, nq = 1) and :254-263 (verify,
+ * nq = K+1); results equal solort_qknorm_rope_kvwrite followed by
+ * solort_decode_attn on the same inputs (the KV rows bit for bit).
+ * Arguments as in those two functions; the workspace is sized by
+ * solort_attn_workspace_bytes(nq, nh, nkv, hd, n_split).  q is not
+ * materialised.
+ */
+int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int nq, int nh, int nkv, int hd,
+                        const void* qn_w, const void* kn_w, float eps, const float* inv_freq,
+                        const int64_t* pos0_dev, void* k_cache, void* v_cache, int64_t kv_tok_stride,
+                        int64_t kv_head_stride, int64_t max_len, int bound, float scale, void* ws,
+                        int n_split, void* out, int out_dtype, solort_stream_t stream);
 
 /* Workspace bytes for solort_argmax_rows with `rows` rows. Allocate once,
  * zero-fill once, reuse; overlapping calls must not share it. */

@@ -8,7 +8,7 @@ TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
   (cuda_graph_executor.py:25-28, :100-102) with the one unspecified step, the
   order of the fp32 sum of squares, fixed to the order the gfx950 kernel uses
   (per 8-element lane chunk left to right, then an xor butterfly over the 16
-  chunks at distances 8, 4, 2, 1).  Everything else is IEEE fp32 with a bf16
+  chunks at distances 1, 2, 4, 8).  Everything else is IEEE fp32 with a bf16
   rounding after each op the reference rounds.
 - attention in fp64 by brute force, with the decode/verify causal rule of
   cuda_graph_executor.py:168 and :250.
@@ -50,7 +50,7 @@ def sum_squares_fixed_order(x: np.ndarray) -> np.ndarray:
     for i in range(1, 8):
         s = s + sq[..., i]
     lanes = np.arange(16)
-    for off in (8, 4, 2, 1):
+    for off in (1, 2, 4, 8):
         s = s + s[..., lanes ^ off]
     return s[..., 0]
 

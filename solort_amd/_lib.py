@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before ours)
 
 LIB_PATH = Path(__file__).resolve().parent / "libsolort_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 # name -> (restype, argtypes); mirrors include/solort_hip.h
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -23,10 +23,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "solort_last_error": (ctypes.c_char_p, []),
     "solort_qknorm_rope_kvwrite": (
         c_int,
-        [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p,
-         c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64,
-         c_void_p],
+        [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p],
     ),
+    "solort_rope_table": (c_int, [c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p]),
     "solort_attn_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "solort_decode_attn": (
         c_int,
@@ -37,6 +37,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         c_int,
         [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_int64,
          c_void_p, c_int, c_float, c_void_p, c_int, c_void_p, c_int, c_void_p],
+    ),
+    "solort_decode_layer": (
+        c_int,
+        [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int, c_float, c_void_p, c_int, c_void_p, c_int,
+         c_void_p],
     ),
     "solort_argmax_workspace_bytes": (c_size_t, [c_int]),
     "solort_argmax_rows": (

@@ -44,6 +44,61 @@ __device__ __forceinline__ uint4 pack8(const float* x) {
 // Lane exchange within a wavefront (64 lanes); xor masks < 64.
 __device__ __forceinline__ float xshfl(float v, int mask) { return __shfl_xor(v, mask, 64); }
 
+// DPP lane moves inside a 16-lane row (VALU, no LDS round trip).
+//   0xB1 quad_perm [1,0,3,2]: lane i reads lane i^1
+//   0x4E quad_perm [2,3,0,1]: lane i reads lane i^2
+//   0x141 row_half_mirror:    lane i reads lane 7-i (within 8)
+//   0x140 row_mirror:         lane i reads lane 15-i
+//   0x128 row_ror:8:          lane i reads lane (i+8)%16 = i^8
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 16 lanes of a row, the same value in every lane: pairwise
+// over lane distance 1, then 2, then 4 (half mirror), then 8 (mirror), i.e.
+// an xor butterfly with offsets 1, 2, 4, 8.
+__device__ __forceinline__ float row16_sum(float v) {
+  v = v + dpp<0xB1>(v);
+  v = v + dpp<0x4E>(v);
+  v = v + dpp<0x141>(v);
+  v = v + dpp<0x140>(v);
+  return v;
+}
+
+// The value held by lane i^8 of the same 16-lane row.
+__device__ __forceinline__ float row16_swap8(float v) { return dpp<0x128>(v); }
+
+// Maximum / sum over all 64 lanes of a wavefront, the same value in every lane.
+__device__ __forceinline__ float wave_max(float v) {
+  v = fmaxf(v, dpp<0xB1>(v));
+  v = fmaxf(v, dpp<0x4E>(v));
+  v = fmaxf(v, dpp<0x141>(v));
+  v = fmaxf(v, dpp<0x140>(v));
+  v = fmaxf(v, xshfl(v, 16));
+  return fmaxf(v, xshfl(v, 32));
+}
+__device__ __forceinline__ float wave_sum(float v) {
+  v = row16_sum(v);
+  v = v + xshfl(v, 16);
+  return v + xshfl(v, 32);
+}
+
+// RoPE cos/sin of position `pos` for 8 consecutive frequencies inv_freq[0..7]:
+// bf16(cos(float(pos) * f)), bf16(sin(...)), the reference's _cos_sin
+// (src/solort/model/cuda_graph_executor.py:95-98) with the device library's
+// fp32 cosf/sinf.  The table kernel (rope.hip) uses this same function, and a
+// test checks that table against torch's for every position served.
+__device__ __forceinline__ void rope_cs8(int64_t pos, const float* inv_freq8, float* c, float* s) {
+  const float p = (float)pos;
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const float ang = p * inv_freq8[i];
+    c[i] = rbf(cosf(ang));
+    s[i] = rbf(sinf(ang));
+  }
+}
+
 // Device-scope (agent) fences used by the last-workgroup-combines pattern.
 __device__ __forceinline__ void fence_release_agent() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
 __device__ __forceinline__ void fence_acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }

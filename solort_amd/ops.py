@@ -46,27 +46,51 @@ def _cache_strides(name: str, c: torch.Tensor, nkv: int) -> tuple[int, int, int]
     return c.stride(0), c.stride(1), c.shape[0]
 
 
+def inv_freq(hd: int, theta: float, device: torch.device | str) -> torch.Tensor:
+    """RoPE frequencies 1 / theta^(2i/hd), fp32 [hd/2] on `device`: the reference's expression
+    (cuda_graph_executor.py:64-66) evaluated by torch on the same device."""
+    return (1.0 / (float(theta) ** (torch.arange(0, hd, 2, device=device).float() / hd))).contiguous()
+
+
 def rope_tables(max_pos: int, hd: int, theta: float, device: torch.device | str,
                 dtype: torch.dtype = torch.bfloat16) -> tuple[torch.Tensor, torch.Tensor]:
-    """cos/sin tables [max_pos, hd/2] for positions 0..max_pos-1.
+    """cos/sin tables [max_pos, hd/2] for positions 0..max_pos-1, computed by torch.
 
     Row p equals the first half of the reference's ``_cos_sin(p)`` row
     (cuda_graph_executor.py:64-66, :95-98), built with the same torch
     expression on the same device; the second half of that row repeats the
-    first because ``emb = cat(freqs, freqs)``.
+    first because ``emb = cat(freqs, freqs)``.  The kernels evaluate these
+    values themselves (solort_rope_table shows them); this torch version is
+    what they are checked against.
     """
-    inv_freq = 1.0 / (float(theta) ** (torch.arange(0, hd, 2, device=device).float() / hd))
-    freqs = torch.arange(max_pos, device=device)[:, None].float() * inv_freq[None, :]
+    freqs = torch.arange(max_pos, device=device)[:, None].float() * inv_freq(hd, theta, device)[None, :]
     return freqs.cos().to(dtype).contiguous(), freqs.sin().to(dtype).contiguous()
 
 
+def rope_tables_device(inv_freq: torch.Tensor, rows: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """cos/sin tables [rows, len(inv_freq)] computed by the library's kernel (solort_rope_table)."""
+    _on_gpu("inv_freq", inv_freq, torch.float32)
+    _need(inv_freq.dim() == 1 and inv_freq.is_contiguous(), "inv_freq must be 1-D contiguous")
+    cos = torch.empty(rows, inv_freq.numel(), dtype=torch.bfloat16, device=inv_freq.device)
+    sin = torch.empty_like(cos)
+    rc = _lib.load().solort_rope_table(inv_freq.data_ptr(), inv_freq.numel(), rows, cos.data_ptr(),
+                                       sin.data_ptr(), _stream(inv_freq))
+    _lib.check(rc, "rope_table")
+    return cos, sin
+
+
+def _inv_freq_ok(f: torch.Tensor) -> None:
+    _on_gpu("inv_freq", f, torch.float32)
+    _need(f.shape == (HD // 2,) and f.is_contiguous(), f"inv_freq must be [{HD // 2}] contiguous fp32")
+
+
 def qknorm_rope_kvwrite(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps: float,
-                        cos_tab: torch.Tensor, sin_tab: torch.Tensor, pos0: torch.Tensor | None,
-                        q_out: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
-                        nh: int, nkv: int) -> None:
+                        inv_f: torch.Tensor, pos0: torch.Tensor | None, q_out: torch.Tensor,
+                        k_cache: torch.Tensor, v_cache: torch.Tensor, nh: int, nkv: int) -> None:
     """QK-RMSNorm + RoPE of T tokens at positions pos0..pos0+T-1, writing q_out and the caches.
 
-    pos0: int64 [1] on the device (None = position 0).  See solort_qknorm_rope_kvwrite.
+    inv_f: fp32 [64] RoPE frequencies (inv_freq()); pos0: int64 [1] on the device (None = position 0).
+    See solort_qknorm_rope_kvwrite.
     """
     _on_gpu("qkv", qkv, torch.bfloat16)
     _need(qkv.dim() == 2 and qkv.shape[1] == (nh + 2 * nkv) * HD and qkv.stride(1) == 1,
@@ -75,11 +99,7 @@ def qknorm_rope_kvwrite(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tenso
     for name, w in (("qn_w", qn_w), ("kn_w", kn_w)):
         _on_gpu(name, w, torch.bfloat16)
         _need(w.shape == (HD,) and w.is_contiguous(), f"{name} must be [{HD}] contiguous")
-    for name, tab in (("cos_tab", cos_tab), ("sin_tab", sin_tab)):
-        _on_gpu(name, tab, torch.bfloat16)
-        _need(tab.dim() == 2 and tab.shape[1] == HD // 2 and tab.is_contiguous(),
-              f"{name} must be [rows, {HD // 2}] contiguous")
-    _need(cos_tab.shape == sin_tab.shape, "cos_tab and sin_tab differ in shape")
+    _inv_freq_ok(inv_f)
     _on_gpu("q_out", q_out, torch.bfloat16)
     _need(q_out.shape == (T, nh, HD) and q_out.is_contiguous(), f"q_out must be [{T}, {nh}, {HD}]")
     ts, hs, max_len = _cache_strides("k_cache", k_cache, nkv)
@@ -93,8 +113,8 @@ def qknorm_rope_kvwrite(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tenso
     lib = _lib.load()
     rc = lib.solort_qknorm_rope_kvwrite(
         qkv.data_ptr(), qkv.stride(0), T, nh, nkv, HD, qn_w.data_ptr(), kn_w.data_ptr(), float(eps),
-        cos_tab.data_ptr(), sin_tab.data_ptr(), cos_tab.shape[0], pos_ptr, q_out.data_ptr(),
-        k_cache.data_ptr(), v_cache.data_ptr(), ts, hs, max_len, _stream(qkv))
+        inv_f.data_ptr(), pos_ptr, q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), ts, hs, max_len,
+        _stream(qkv))
     _lib.check(rc, "qknorm_rope_kvwrite")
 
 
@@ -140,6 +160,42 @@ def decode_attn(q, k_cache, v_cache, pos0, bound, scale, ws, n_split, out) -> No
 def verify_attn(q, k_cache, v_cache, pos0, bound, scale, ws, n_split, out) -> None:
     """K+1 query tokens at pos0..pos0+K, each causal over the cache; see solort_verify_attn."""
     _attn("solort_verify_attn", q, k_cache, v_cache, pos0, bound, scale, ws, n_split, out)
+
+
+def decode_layer(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps: float, inv_f: torch.Tensor,
+                 pos0: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, bound: int, scale: float,
+                 ws: torch.Tensor, n_split: int, out: torch.Tensor, nh: int, nkv: int) -> None:
+    """One layer's attention block: prologue + KV write of the nq new tokens (qkv [nq, (nh+2nkv)*128])
+    at pos0.. and split-KV attention into out [nq, nh*128].
+
+    Equal to qknorm_rope_kvwrite followed by decode_attn; see solort_decode_layer.
+    """
+    _on_gpu("qkv", qkv, torch.bfloat16)
+    _need(qkv.dim() == 2 and qkv.shape[1] == (nh + 2 * nkv) * HD and qkv.stride(1) == 1,
+          f"qkv must be [nq, {(nh + 2 * nkv) * HD}] with unit column stride")
+    nq = qkv.shape[0]
+    for name, w in (("qn_w", qn_w), ("kn_w", kn_w)):
+        _on_gpu(name, w, torch.bfloat16)
+        _need(w.shape == (HD,) and w.is_contiguous(), f"{name} must be [{HD}] contiguous")
+    _inv_freq_ok(inv_f)
+    ts, hs, max_len = _cache_strides("k_cache", k_cache, nkv)
+    _on_gpu("v_cache", v_cache, torch.bfloat16)
+    _need(v_cache.shape == k_cache.shape and v_cache.stride() == k_cache.stride(),
+          "v_cache must match k_cache in shape and strides")
+    _need(pos0.is_cuda and pos0.dtype == torch.int64 and pos0.numel() >= 1, "pos0 must be int64 on the device")
+    _need(out.is_cuda and out.dtype in (torch.bfloat16, torch.float32), "out must be bf16 or fp32 on the device")
+    _need(out.shape == (nq, nh * HD) and out.is_contiguous() and out.data_ptr() % 16 == 0,
+          f"out must be [{nq}, {nh * HD}] contiguous and 16-byte aligned")
+    lib = _lib.load()
+    need = lib.solort_attn_workspace_bytes(nq, nh, nkv, HD, n_split)
+    _need(ws.is_cuda and ws.numel() * ws.element_size() >= need and ws.data_ptr() % 16 == 0,
+          f"workspace too small: need {need} bytes")
+    dt = DTYPE_F32 if out.dtype == torch.float32 else DTYPE_BF16
+    rc = lib.solort_decode_layer(
+        qkv.data_ptr(), qkv.stride(0), nq, nh, nkv, HD, qn_w.data_ptr(), kn_w.data_ptr(), float(eps),
+        inv_f.data_ptr(), pos0.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), ts, hs, max_len, int(bound),
+        float(scale), ws.data_ptr(), int(n_split), out.data_ptr(), dt, _stream(qkv))
+    _lib.check(rc, "decode_layer")
 
 
 def argmax_workspace(rows: int, device: torch.device | str) -> torch.Tensor:

@@ -1,0 +1,165 @@
+"""Attention block of the reference's CUDA-graph Qwen3 runner, on the gfx950 kernels.
+
+Mirrors the attention part of ``_GraphQwen3Runner``
+(src/solort/model/cuda_graph_executor.py:31-289): a runner-owned static KV
+cache ``kc``/``vc`` [layers, max_len, nkv, 128] (:67-69), a device-side
+position buffer ``pos_buf`` (:71), length-bucketed decode graphs captured
+lazily and routed by position (:75-77, :192-214), bucketed prefill graphs
+(:83-85, :137-161), a fixed K+1-token verify graph (:270-289) and the in-graph
+greedy argmax (:206).  Everything outside attention (embedding, QKV/o_proj
+GEMMs, MLP, lm_head) is not part of this library: each layer's fused QKV
+projection output is a static input buffer the caller fills (the role the
+QKV GEMM plays at :115, :171, :253), and each layer's attention output
+``ctx`` [T, nh*128] is left in a static output buffer (what o_proj consumes
+at :131, :185, :264).  Logits for the argmax are likewise a caller-filled
+buffer.
+
+Decode and verify run one launch per layer (solort_decode_layer: prologue,
+KV write, split-KV attention and combine); prefill runs the prologue launch
+then the MFMA causal attention launch.  No launch synchronises the host, so
+one graph replay runs a whole step.  Unlike the reference, which captures one
+verify graph over all max_len keys, verify graphs are bucketed like decode
+so that only the bucket holding the K+1 positions is scanned.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import ops
+
+HD = 128
+DECODE_BUCKETS = (128, 256, 512, 1024, 2048, 4096)
+PREFILL_BUCKETS = (16, 32, 64, 128, 256, 512, 1024)
+
+
+def decode_splits(bound: int, nkv: int) -> int:
+    """Key splits per KV head for a decode bucket: about 32 keys per split, enough
+    workgroups to cover the 256 CUs, at most 256 splits."""
+    return max(1, min(256, bound // 32))
+
+
+def verify_splits(bound: int) -> int:
+    """Key splits per KV head for a K+1-token verify bucket (64 keys per split, at most 64)."""
+    return max(1, min(64, bound // 64))
+
+
+class GraphQwen3Attention:
+    """Static-shape attention runner over a runner-owned bf16 KV cache, with hipGraph capture."""
+
+    def __init__(self, nh: int, nkv: int, layers: int, max_len: int, qn_w: torch.Tensor,
+                 kn_w: torch.Tensor, eps: float = 1e-6, theta: float = 1e6,
+                 device: torch.device | str = "cuda", verify_tokens: int = 5,
+                 vocab: int = 151936) -> None:
+        if nh % nkv:
+            raise RuntimeError(f"nh={nh} must be a multiple of nkv={nkv}")
+        self.dev = torch.device(device)
+        self.nh, self.nkv, self.L, self.max_len = nh, nkv, layers, int(max_len)
+        self.groups = nh // nkv
+        self.eps = float(eps)
+        self.scale = HD ** -0.5
+        self.width = (nh + 2 * nkv) * HD
+        self.qn_w = qn_w.to(self.dev, torch.bfloat16).contiguous()
+        self.kn_w = kn_w.to(self.dev, torch.bfloat16).contiguous()
+        if self.qn_w.shape != (layers, HD) or self.kn_w.shape != (layers, HD):
+            raise RuntimeError(f"norm weights must be [{layers}, {HD}]")
+        kv_shape = (layers, self.max_len, nkv, HD)
+        self.kc = torch.zeros(kv_shape, dtype=torch.bfloat16, device=self.dev)
+        self.vc = torch.zeros(kv_shape, dtype=torch.bfloat16, device=self.dev)
+        self.inv_freq = ops.inv_freq(HD, theta, self.dev)
+        self.pos_buf = torch.zeros(1, dtype=torch.long, device=self.dev)
+        self.buckets = sorted({b for b in DECODE_BUCKETS if b < self.max_len} | {self.max_len})
+        self.pre_buckets = sorted({b for b in PREFILL_BUCKETS if b <= self.max_len})
+        self.vocab = int(vocab)
+        # decode: static inputs/outputs of the captured graphs
+        self.qkv_dec = torch.zeros(layers, 1, self.width, dtype=torch.bfloat16, device=self.dev)
+        self.ctx_dec = torch.zeros(layers, 1, nh * HD, dtype=torch.bfloat16, device=self.dev)
+        self.logits_dec = torch.zeros(1, self.vocab, dtype=torch.float32, device=self.dev)
+        self.tok_dec = torch.zeros(1, dtype=torch.long, device=self.dev)
+        self.ws_dec = ops.attn_workspace(1, nh, nkv, max(decode_splits(b, nkv) for b in self.buckets), self.dev)
+        self.ws_arg = ops.argmax_workspace(max(1, verify_tokens), self.dev)
+        self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        # verify (K+1 tokens)
+        self.k1 = int(verify_tokens)
+        self.qkv_ver = torch.zeros(layers, self.k1, self.width, dtype=torch.bfloat16, device=self.dev)
+        self.ctx_ver = torch.zeros(layers, self.k1, nh * HD, dtype=torch.bfloat16, device=self.dev)
+        self.logits_ver = torch.zeros(self.k1, self.vocab, dtype=torch.float32, device=self.dev)
+        self.tok_ver = torch.zeros(self.k1, dtype=torch.long, device=self.dev)
+        self.vpos0 = torch.zeros(1, dtype=torch.long, device=self.dev)
+        self.ws_ver = ops.attn_workspace(self.k1, nh, nkv, max(verify_splits(b) for b in self.buckets), self.dev)
+        self._ver_graphs: dict[int, torch.cuda.CUDAGraph] = {}
+
+    # ------------------------------------------------------------ decode
+
+    def _decode_forward(self, bound: int) -> None:
+        ns = decode_splits(bound, self.nkv)
+        for li in range(self.L):
+            ops.decode_layer(self.qkv_dec[li], self.qn_w[li], self.kn_w[li], self.eps, self.inv_freq, self.pos_buf,
+                             self.kc[li], self.vc[li], bound, self.scale, self.ws_dec, ns,
+                             self.ctx_dec[li], self.nh, self.nkv)
+        ops.argmax_rows(self.logits_dec, self.tok_dec, self.ws_arg)
+
+    def _bucket_for(self, pos: int) -> int:
+        """cuda_graph_executor.py:192-193: the first bucket strictly above the position."""
+        for b in self.buckets:
+            if b > pos:
+                return b
+        raise RuntimeError(f"decode position {pos} exceeds max_len {self.max_len}")
+
+    def _capture(self, bound: int) -> None:
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            self._decode_forward(bound)
+        self._graphs[bound] = graph
+
+    def _replay(self, pos: int) -> int:
+        bound = self._bucket_for(pos)
+        if bound not in self._graphs:
+            self._capture(bound)
+        self._graphs[bound].replay()
+        return bound
+
+    def decode(self, qkv: torch.Tensor, pos: int) -> torch.Tensor:
+        """One decode step at `pos`: qkv [layers, 1, (nh+2nkv)*128] -> ctx [layers, 1, nh*128] (static buffer)."""
+        if not 0 <= pos < self.max_len:
+            raise RuntimeError(f"decode position {pos} outside [0, {self.max_len})")
+        self.qkv_dec.copy_(qkv)
+        self.pos_buf.fill_(int(pos))
+        self._replay(pos)
+        return self.ctx_dec
+
+    def decode_argmax(self, qkv: torch.Tensor, pos: int, logits: torch.Tensor) -> torch.Tensor:
+        """decode() plus the in-graph greedy argmax of `logits` [1, vocab]; returns the [1] token buffer."""
+        self.logits_dec.copy_(logits)
+        self.decode(qkv, pos)
+        return self.tok_dec
+
+    # ------------------------------------------------------------ verify
+
+    def _verify_forward(self, bound: int) -> None:
+        ns = verify_splits(bound)
+        for li in range(self.L):
+            ops.decode_layer(self.qkv_ver[li], self.qn_w[li], self.kn_w[li], self.eps, self.inv_freq, self.vpos0,
+                             self.kc[li], self.vc[li], bound, self.scale, self.ws_ver, ns,
+                             self.ctx_ver[li], self.nh, self.nkv)
+        ops.argmax_rows(self.logits_ver, self.tok_ver, self.ws_arg)
+
+    def verify(self, qkv: torch.Tensor, pos_start: int, logits: torch.Tensor | None = None) -> torch.Tensor:
+        """Score K+1 tokens at pos_start..pos_start+K (cuda_graph_executor.py:270-289).
+
+        qkv [layers, K+1, width]; returns ctx [layers, K+1, nh*128].  If logits [K+1, vocab] are
+        given, tok_ver holds their argmax after the replay.
+        """
+        if not 0 <= pos_start <= self.max_len - self.k1:
+            raise RuntimeError(f"verify positions {pos_start}..{pos_start + self.k1 - 1} exceed max_len")
+        bound = self._bucket_for(pos_start + self.k1 - 1)
+        if bound not in self._ver_graphs:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._verify_forward(bound)
+            self._ver_graphs[bound] = graph
+        self.qkv_ver.copy_(qkv)
+        if logits is not None:
+            self.logits_ver.copy_(logits)
+        self.vpos0.fill_(int(pos_start))
+        self._ver_graphs[bound].replay()
+        return self.ctx_ver

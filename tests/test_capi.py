@@ -76,12 +76,17 @@ def test_decode_rejects_bad_arguments_without_launching(lib):
 
 def test_prologue_and_argmax_reject_bad_arguments(lib):
     p = ctypes.c_void_p(4096)
-    rc = lib.solort_qknorm_rope_kvwrite(p, 6144, 1, 32, 8, 100, p, p, 1e-6, p, p, 1024, None, p, p, p,
-                                        1024, 128, 1024, None)
+    rc = lib.solort_qknorm_rope_kvwrite(p, 6144, 1, 32, 8, 100, p, p, 1e-6, p, None, p, p, p, 1024, 128, 1024,
+                                        None)
     assert rc == EINVAL and "head_dim" in _err(lib)
-    rc = lib.solort_qknorm_rope_kvwrite(p, 6000, 1, 32, 8, 128, p, p, 1e-6, p, p, 1024, None, p, p, p,
-                                        1024, 128, 1024, None)
+    rc = lib.solort_qknorm_rope_kvwrite(p, 6000, 1, 32, 8, 128, p, p, 1e-6, p, None, p, p, p, 1024, 128, 1024,
+                                        None)
     assert rc == EINVAL and "stride" in _err(lib)
+    rc = lib.solort_decode_layer(p, 6144, 1, 32, 8, 128, p, p, 1e-6, None, p, p, p, 1024, 128, 1024, 1024, 0.088,
+                                 p, 32, p, 0, None)
+    assert rc == EINVAL and "null" in _err(lib)
+    rc = lib.solort_rope_table(p, 60, 10, p, p, None)
+    assert rc == EINVAL and "half_dim" in _err(lib)
     rc = lib.solort_argmax_rows(p, 3, 1, 10, 10, p, p, None)
     assert rc == EINVAL and "dtype" in _err(lib)
     rc = lib.solort_argmax_rows(p, 0, 1, 10, 5, p, p, None)

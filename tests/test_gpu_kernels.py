@@ -29,17 +29,22 @@ def _say(msg: str) -> None:
 
 
 def _tables(dev, rows):
+    """torch's cos/sin table (the oracle's RoPE input; the kernels compute the same values)."""
     cos, sin = ops.rope_tables(rows, HD, wl.THETA, dev)
     return cos, sin
 
 
-def _run_prologue(dev, case, li, cos, sin, kc, vc):
+def _ifr(dev):
+    return ops.inv_freq(HD, wl.THETA, dev)
+
+
+def _run_prologue(dev, case, li, kc, vc):
     """Prologue for layer li of a decode case on the GPU; returns q [nq, nh, hd] (device)."""
     sh = case.shape
     q = torch.empty(case.nq, sh.nh, HD, dtype=torch.bfloat16, device=dev)
     pos = torch.tensor([case.pos], dtype=torch.long, device=dev)
     ops.qknorm_rope_kvwrite(case.qkv[li].to(dev), case.qn_w[li].to(dev), case.kn_w[li].to(dev), wl.EPS,
-                            cos, sin, pos, q, kc, vc, sh.nh, sh.nkv)
+                            _ifr(dev), pos, q, kc, vc, sh.nh, sh.nkv)
     return q, pos
 
 
@@ -83,7 +88,7 @@ def _decode_case_check(gpu, case, n_splits, layers=(0,)):
         _say(f"[{sh.name} pos={case.pos} nq={case.nq} bound={case.bound} layer={li}]")
         kc = case.kc[li].to(dev)
         vc = case.vc[li].to(dev)
-        q, pos = _run_prologue(dev, case, li, cos, sin, kc, vc)
+        q, pos = _run_prologue(dev, case, li, kc, vc)
         torch.cuda.synchronize()
         # KV rows: bit-exact against the fixed-order oracle; other rows untouched
         qx, kx, vx = _fixed_order_kv(case, li, cos_cpu, sin_cpu)
@@ -131,9 +136,8 @@ def test_decode_qwen3_8b_32k(gpu):
     case = wl.decode_case(3, layers=1)
     dev = gpu
     sh = case.shape
-    cos, sin = _tables(dev, case.max_len)
     kc, vc = case.kc[0].to(dev), case.vc[0].to(dev)
-    q, pos = _run_prologue(dev, case, 0, cos, sin, kc, vc)
+    q, pos = _run_prologue(dev, case, 0, kc, vc)
     torch.cuda.synchronize()
     _say(f"[{sh.name} 32k decode] prologue done")
     q64 = q.float().cpu().numpy()
@@ -168,9 +172,8 @@ def test_verify_equals_sequential_decode(gpu):
     case = wl.decode_case(4, layers=1)
     dev = gpu
     sh = case.shape
-    cos, sin = _tables(dev, case.max_len)
     kc, vc = case.kc[0].to(dev), case.vc[0].to(dev)
-    q, pos = _run_prologue(dev, case, 0, cos, sin, kc, vc)
+    q, pos = _run_prologue(dev, case, 0, kc, vc)
     ws = ops.attn_workspace(5, sh.nh, sh.nkv, 32, dev)
     out = torch.empty(5, sh.nh * HD, dtype=torch.float32, device=dev)
     ops.verify_attn(q, kc, vc, pos, case.max_len, sh.scale, ws, 32, out)
@@ -192,7 +195,7 @@ def test_prologue_prefill_rows_bitexact(gpu):
     kc = torch.zeros(case.max_len, sh.nkv, HD, dtype=torch.bfloat16, device=dev)
     vc = torch.zeros_like(kc)
     q = torch.empty(case.T, sh.nh, HD, dtype=torch.bfloat16, device=dev)
-    ops.qknorm_rope_kvwrite(case.qkv[0].to(dev), case.qn_w[0].to(dev), case.kn_w[0].to(dev), wl.EPS, cos, sin,
+    ops.qknorm_rope_kvwrite(case.qkv[0].to(dev), case.qn_w[0].to(dev), case.kn_w[0].to(dev), wl.EPS, _ifr(dev),
                             None, q, kc, vc, sh.nh, sh.nkv)
     torch.cuda.synchronize()
     qx, kx, vx = exact.prologue_fixed_order(case.qkv[0].float().numpy(), case.qn_w[0].float().numpy(),
@@ -205,14 +208,13 @@ def test_prologue_prefill_rows_bitexact(gpu):
 
 def test_prologue_skips_out_of_range_positions(gpu):
     dev = gpu
-    cos, sin = _tables(dev, 64)
     kc = torch.full((64, 8, HD), 7.0, dtype=torch.bfloat16, device=dev)
     vc = kc.clone()
     qkv = torch.randn(2, 48 * HD, device=dev).to(torch.bfloat16)
     w = torch.ones(HD, dtype=torch.bfloat16, device=dev)
     q = torch.empty(2, 32, HD, dtype=torch.bfloat16, device=dev)
     pos = torch.tensor([63], dtype=torch.long, device=dev)  # token 1 lands at 64: outside the cache
-    ops.qknorm_rope_kvwrite(qkv, w, w, wl.EPS, cos, sin, pos, q, kc, vc, 32, 8)
+    ops.qknorm_rope_kvwrite(qkv, w, w, wl.EPS, _ifr(dev), pos, q, kc, vc, 32, 8)
     torch.cuda.synchronize()
     assert torch.all(kc[:63] == 7.0) and torch.all(vc[:63] == 7.0)
     assert not torch.all(kc[63] == 7.0)
@@ -268,3 +270,67 @@ def test_argmax_strided_rows(gpu):
     ops.argmax_rows(big.to(gpu)[:, 1:1000], out, ws)
     torch.cuda.synchronize()
     assert np.array_equal(out.cpu().numpy(), exact.argmax_first(x.numpy()))
+
+
+# ------------------------------------------------------------------ fused layer
+
+@pytest.mark.parametrize("index,live,n_split", [(1, 128, 4), (1, 256, 8), (1, 512, 16), (1, 1024, 32),
+                                                (1, 1024, 7), (0, None, 32), (3, None, 256), (4, None, 64)])
+def test_decode_layer_equals_prologue_then_attention(gpu, index, live, n_split):
+    """The fused launch writes the same KV bits and produces the same output bits as the two-launch path."""
+    case = wl.decode_case(index, live=live, layers=1)
+    dev = gpu
+    sh = case.shape
+    _say(f"[fused {sh.name} pos={case.pos} nq={case.nq} bound={case.bound} n_split={n_split}]")
+    ifr = _ifr(dev)
+    kc_a, vc_a = case.kc[0].to(dev), case.vc[0].to(dev)
+    kc_b, vc_b = kc_a.clone(), vc_a.clone()
+    pos = torch.tensor([case.pos], dtype=torch.long, device=dev)
+    qkv = case.qkv[0].to(dev)
+    qn, kn = case.qn_w[0].to(dev), case.kn_w[0].to(dev)
+    q = torch.empty(case.nq, sh.nh, HD, dtype=torch.bfloat16, device=dev)
+    ws = ops.attn_workspace(case.nq, sh.nh, sh.nkv, n_split, dev)
+    for dt in (torch.bfloat16, torch.float32):
+        out_a = torch.empty(case.nq, sh.nh * HD, dtype=dt, device=dev)
+        out_b = torch.empty_like(out_a)
+        ops.qknorm_rope_kvwrite(qkv, qn, kn, wl.EPS, ifr, pos, q, kc_a, vc_a, sh.nh, sh.nkv)
+        fn = ops.decode_attn if case.nq == 1 else ops.verify_attn
+        fn(q, kc_a, vc_a, pos, case.bound, sh.scale, ws, n_split, out_a)
+        ops.decode_layer(qkv, qn, kn, wl.EPS, ifr, pos, kc_b, vc_b, case.bound, sh.scale, ws, n_split, out_b,
+                         sh.nh, sh.nkv)
+        torch.cuda.synchronize()
+        assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b), "KV rows differ"
+        assert torch.equal(out_a, out_b), f"outputs differ ({dt})"
+
+
+def test_decode_layer_repeated_calls_reuse_workspace(gpu):
+    """Ten back-to-back fused launches over different layers share one workspace and each matches
+    its own single launch (the tickets are left at zero)."""
+    case = wl.decode_case(1, live=1024, layers=4)
+    dev = gpu
+    sh = case.shape
+    ifr = _ifr(dev)
+    pos = torch.tensor([case.pos], dtype=torch.long, device=dev)
+    kc, vc = case.kc.to(dev), case.vc.to(dev)
+    ws = ops.attn_workspace(1, sh.nh, sh.nkv, 32, dev)
+    outs = torch.empty(10, 1, sh.nh * HD, dtype=torch.float32, device=dev)
+    for i in range(10):
+        li = i % 4
+        ops.decode_layer(case.qkv[li].to(dev), case.qn_w[li].to(dev), case.kn_w[li].to(dev), wl.EPS, ifr, pos,
+                         kc[li], vc[li], case.bound, sh.scale, ws, 32, outs[i], sh.nh, sh.nkv)
+    torch.cuda.synchronize()
+    for i in range(4, 10):
+        assert torch.equal(outs[i], outs[i - 4])
+
+
+def test_device_rope_table_equals_torch_table(gpu):
+    """The library's cos/sin kernel reproduces torch's table (the reference's expression) bit for bit
+    for every position of the longest cache served (32768)."""
+    rows = 32768
+    cos_t, sin_t = ops.rope_tables(rows, HD, wl.THETA, gpu)
+    cos_k, sin_k = ops.rope_tables_device(_ifr(gpu), rows)
+    torch.cuda.synchronize()
+    dc = (cos_k.view(torch.int16) != cos_t.view(torch.int16)).sum().item()
+    ds = (sin_k.view(torch.int16) != sin_t.view(torch.int16)).sum().item()
+    _say(f"[rope table] differing cos {dc}, sin {ds} of {rows * 64}")
+    assert dc == 0 and ds == 0

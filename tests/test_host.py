@@ -1,0 +1,15 @@
+"""Host-side logic of the runner that needs no GPU."""
+from solort_amd.runner import DECODE_BUCKETS, PREFILL_BUCKETS, decode_splits
+
+
+def test_decode_splits_heuristic():
+    assert decode_splits(1024, 8) == 32
+    assert decode_splits(128, 8) == 4
+    assert decode_splits(32768, 8) == 256
+    assert decode_splits(16, 8) == 1
+
+
+def test_bucket_tables_follow_reference():
+    # cuda_graph_executor.py:75-77 and :83-85
+    assert DECODE_BUCKETS == (128, 256, 512, 1024, 2048, 4096)
+    assert PREFILL_BUCKETS == (16, 32, 64, 128, 256, 512, 1024)
