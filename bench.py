@@ -136,6 +136,10 @@ def main() -> int:
 
     if not args.no_sweep:
         result["extras"] = extras(torch, ops, wl, runners, dev, sh)
+        result["prefill"] = prefill_extras(torch, ops, runners, dev, sh)
+        p1024 = result["prefill"].get("1024")
+        if p1024:
+            result["prefill_tflops"] = p1024["tflops"]
 
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, live)
@@ -190,6 +194,52 @@ def extras(torch, ops, wl, runners, dev, sh) -> dict:
     for ns in (8, 16, 32, 64, 128):
         us = time_decode_kernel(torch, ops, runners, 1024, ns, sh, dev, reps=3, pos=pos)
         out["n_split_sweep_kv1024"][str(ns)] = round(us, 3)
+    return out
+
+
+def prefill_extras(torch, ops, runners, dev, sh) -> dict:
+    """Prefill attention at T in {128, 512, 1024}: the MFMA kernel alone (graph of one launch per
+    layer of every KV set, HIP events around replays) and the graphed prefill step (prologue + KV
+    write + attention, 36 layers) per layer.  Overwrites cache rows 0..T-1 of every set."""
+    out = {}
+    stream = torch.cuda.current_stream(dev)
+    gen = torch.Generator(device=dev).manual_seed(1002)
+    for T in (128, 512, 1024):
+        for r in runners:
+            r.prefill((torch.randn(sh.layers, T, sh.qkv_width, generator=gen, device=dev)).to(torch.bfloat16))
+        torch.cuda.synchronize()
+        outs = [torch.empty(T, sh.nh * 128, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+
+        def run_all():
+            for i, r in enumerate(runners):
+                for li in range(sh.layers):
+                    ops.prefill_attn(r.q_pre[:T], r.kc[li], r.vc[li], sh.scale, outs[(i + li) % 2])
+
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            run_all()
+        graph.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        reps = 3
+        e0.record(stream)
+        for _ in range(reps):
+            graph.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        kern_us = e0.elapsed_time(e1) * 1e3 / (reps * len(runners) * sh.layers)
+        # whole graphed prefill step (prologue + attention per layer)
+        e0.record(stream)
+        for i in range(reps):
+            runners[i % len(runners)]._pre_graphs[T].replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        step_us = e0.elapsed_time(e1) * 1e3 / (reps * sh.layers)
+        fl = prefill_flops(T, sh.nh)
+        tf = fl / (kern_us * 1e-6) / 1e12
+        out[str(T)] = {"kernel_us": round(kern_us, 3), "tflops": round(tf, 2),
+                       "frac_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4),
+                       "step_us_per_layer": round(step_us, 3), "flop": fl}
     return out
 
 

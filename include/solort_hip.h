@@ -146,6 +146,20 @@ int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int nq, int nh,
                         int64_t kv_head_stride, int64_t max_len, int bound, float scale, void* ws,
                         int n_split, void* out, int out_dtype, solort_stream_t stream);
 
+/*
+ * Causal grouped-query prefill attention on bf16 MFMA.
+ * Replaces cuda_graph_executor.py:124-130: SDPA(q, repeat_interleave(k, g),
+ * repeat_interleave(v, g), is_causal=True, scale) over T prompt rows at
+ * positions 0..T-1, with K/V read from cache rows 0..T-1 (written first by
+ * solort_qknorm_rope_kvwrite, as the reference writes them at :122-123).
+ * q   [T, nh, 128] bf16; out [T, nh * 128] bf16 or fp32.  T <= max_len.
+ * Query groups g = nh / nkv of 1, 2 or 4.  Probabilities enter the second
+ * matrix product rounded to bf16 (accumulation and softmax are fp32).
+ */
+int solort_prefill_attn(const void* q, int T, int nh, int nkv, int hd, const void* k_cache,
+                        const void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride,
+                        int64_t max_len, float scale, void* out, int out_dtype, solort_stream_t stream);
+
 /* Workspace bytes for solort_argmax_rows with `rows` rows. Allocate once,
  * zero-fill once, reuse; overlapping calls must not share it. */
 size_t solort_argmax_workspace_bytes(int rows);

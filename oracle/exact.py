@@ -14,6 +14,9 @@ TEST INFRASTRUCTURE ONLY (see oracle/__init__.py).
   cuda_graph_executor.py:168 and :250.
 - splitkv_combine: the split-KV partial + log-sum-exp merge the decode kernel
   performs, in fp64, to show that splitting does not change the result.
+- prefill_blockwise: the prefill kernel's own arithmetic (online softmax over
+  64-key blocks with the probabilities rounded to bf16 before the second
+  matrix product) in fp64, to pin the kernel's fp32 output tightly.
 - argmax_first: first index of the maximum, NaN counted as maximum
   (torch.argmax / numpy.argmax rule).
 """
@@ -136,6 +139,31 @@ def splitkv_combine(q: np.ndarray, keys: np.ndarray, vals: np.ndarray, scale: fl
     Lsum = sum(wi * p[1] for wi, p in zip(w, parts))
     O = sum(wi[:, None] * p[2] for wi, p in zip(w, parts))
     return O / Lsum[:, None]
+
+
+def prefill_blockwise(q: np.ndarray, keys: np.ndarray, vals: np.ndarray, scale: float, block: int = 64) -> np.ndarray:
+    """Causal attention of q [T,hd] (row t at position t) over keys/vals [T,hd] as the prefill kernel
+    evaluates it: per 64-key block, running max M (log2 units), p = bf16(2^(s - M)), l += sum of the
+    unrounded p, o = o * 2^(M_old - M) + p_bf16 @ V.  fp64 except the bf16 rounding of p."""
+    q = np.asarray(q, np.float64)
+    T = q.shape[0]
+    z = (q @ np.asarray(keys, np.float64).T) * scale * np.log2(np.e)
+    z[np.triu_indices(T, 1)] = -np.inf
+    vals = np.asarray(vals, np.float64)
+    m = np.full(T, -np.inf)
+    l = np.zeros(T)
+    o = np.zeros_like(q)
+    for k0 in range(0, T, block):
+        zb = z[:, k0:k0 + block]
+        mn = np.maximum(m, zb.max(axis=1))
+        live = np.isfinite(mn)
+        alpha = np.where(live, np.exp2(np.where(live, m - mn, 0.0)), 1.0)
+        p = np.where(live[:, None], np.exp2(zb - np.where(live, mn, 0.0)[:, None]), 0.0)
+        pb = np.asarray(bf16_round(p), np.float64)
+        l = l * alpha + p.sum(axis=1)
+        o = o * alpha[:, None] + pb @ vals[k0:k0 + block]
+        m = mn
+    return o / l[:, None]
 
 
 def argmax_first(x: np.ndarray) -> np.ndarray:

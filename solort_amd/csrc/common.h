@@ -84,18 +84,23 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v + xshfl(v, 32);
 }
 
-// RoPE cos/sin of position `pos` for 8 consecutive frequencies inv_freq[0..7]:
-// bf16(cos(float(pos) * f)), bf16(sin(...)), the reference's _cos_sin
-// (src/solort/model/cuda_graph_executor.py:95-98) with the device library's
-// fp32 cosf/sinf.  The table kernel (rope.hip) uses this same function, and a
-// test checks that table against torch's for every position served.
+// RoPE angle, cos and sin of the reference's _cos_sin
+// (src/solort/model/cuda_graph_executor.py:95-98): the fp32 product
+// float(pos) * inv_freq, then the device library's fp32 cosf/sinf rounded to
+// bf16.  Every kernel that applies RoPE evaluates them through these helpers,
+// and the table kernel (rope.hip) does too; a test checks that table against
+// torch's for every position served.
+__device__ __forceinline__ float rope_angle(int64_t pos, float inv_f) { return (float)pos * inv_f; }
+__device__ __forceinline__ float rope_cos(float ang) { return rbf(cosf(ang)); }
+__device__ __forceinline__ float rope_sin(float ang) { return rbf(sinf(ang)); }
+
+// cos/sin of position `pos` for 8 consecutive frequencies inv_freq8[0..7].
 __device__ __forceinline__ void rope_cs8(int64_t pos, const float* inv_freq8, float* c, float* s) {
-  const float p = (float)pos;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float ang = p * inv_freq8[i];
-    c[i] = rbf(cosf(ang));
-    s[i] = rbf(sinf(ang));
+    const float ang = rope_angle(pos, inv_freq8[i]);
+    c[i] = rope_cos(ang);
+    s[i] = rope_sin(ang);
   }
 }
 

@@ -104,6 +104,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   extern __shared__ __align__(16) float smem[];
   __shared__ __align__(16) float s_q[R * 128];
   __shared__ uint4 s_new[FUSED ? 2 * NQ * 16 : 1];  // fresh K rows then V rows (bf16 bits)
+  __shared__ float s_rope[FUSED ? 2 * NQ * 64 : 1];  // cos [t][64] then sin [t][64]
   __shared__ unsigned s_ticket;
 
   const int tid = threadIdx.x, j = tid & 15, slot = tid >> 4, wave = tid >> 6;
@@ -115,27 +116,25 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   const int kbeg = min(split * chunk, a.bound);
   const int kstat = min(kbeg + chunk, a.bound);
 
-  // 1. Loads for this slot's first prologue row, issued before the K/V loads:
-  //    vector loads complete in issue order, so the prologue then waits for
-  //    its own rows only.
+  // 1. Loads for this slot's first prologue row (and this thread's RoPE
+  //    frequency), issued before the K/V loads: vector loads complete in
+  //    issue order, so the prologue then waits for its own rows only.
   constexpr int NROWS = FUSED ? NQ * (G + 2) : R;
+  constexpr int NROPE = FUSED ? 2 * NQ * 64 : 0;  // (token, frequency, cos|sin) values
   uint4 raw0 = make_uint4(0u, 0u, 0u, 0u), w0 = raw0;
-  float4 f0a = make_float4(0.f, 0.f, 0.f, 0.f), f0b = f0a;
+  float fr0 = 0.f;
   if (slot < NROWS) {
     if constexpr (FUSED) {
       const int t = slot / (G + 2), c = slot % (G + 2);
       const int hs = c < G ? kvh * G + c : (c == G ? a.nh + kvh : a.nh + a.nkv + kvh);
       raw0 = *reinterpret_cast<const uint4*>(a.qkv + (int64_t)t * a.qkv_stride + hs * SOLORT_HD + j * 8);
-      if (c <= G) {
-        w0 = *reinterpret_cast<const uint4*>((c < G ? a.qn_w : a.kn_w) + j * 8);
-        f0a = *reinterpret_cast<const float4*>(a.inv_freq + (j & 7) * 8);
-        f0b = *reinterpret_cast<const float4*>(a.inv_freq + (j & 7) * 8 + 4);
-      }
+      if (c <= G) w0 = *reinterpret_cast<const uint4*>((c < G ? a.qn_w : a.kn_w) + j * 8);
     } else {
       const int t = slot / G, g = slot % G;
       raw0 = *reinterpret_cast<const uint4*>(a.q + ((int64_t)t * a.nh + kvh * G + g) * SOLORT_HD + j * 8);
     }
   }
+  if (FUSED && tid < NROPE) fr0 = a.inv_freq[(tid >> 1) & 63];
 
   // 2. First K/V loads: static addresses, independent of the position.
   const uint16_t* kp = a.kc + (int64_t)kvh * a.head_stride + j * 8;
@@ -155,12 +154,18 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
 
   const int64_t pos0 = a.pos0_dev[0];
 
-  // 3. q rows (and, fused, the new tokens' K/V rows) into LDS.
+  // 3. q rows (and, fused, the new tokens' K/V rows) into LDS.  Fused: every
+  //    thread first evaluates one (or a few) of the RoPE cos/sin values.
+  if constexpr (FUSED) {
+    for (int e = tid; e < NROPE; e += 256) {
+      const int t = e >> 7, f = (e >> 1) & 63;
+      const float ang = rope_angle(pos0 + t, e == tid ? fr0 : a.inv_freq[f]);
+      s_rope[(e & 1) * NQ * 64 + t * 64 + f] = (e & 1) ? rope_sin(ang) : rope_cos(ang);
+    }
+    __syncthreads();
+  }
   for (int row = slot; row < NROWS; row += 16) {
     uint4 raw = raw0, w8 = w0;
-    float fr[8];
-    *reinterpret_cast<float4*>(fr) = f0a;
-    *reinterpret_cast<float4*>(fr + 4) = f0b;
     if constexpr (FUSED) {
       const int t = row / (G + 2), c = row % (G + 2);
       const int64_t pos = pos0 + t;
@@ -168,11 +173,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
       if (row != slot) {  // rows past the first (verify): loaded here
         const int hs = c < G ? kvh * G + c : (c == G ? a.nh + kvh : a.nh + a.nkv + kvh);
         raw = *reinterpret_cast<const uint4*>(a.qkv + (int64_t)t * a.qkv_stride + hs * SOLORT_HD + j * 8);
-        if (c <= G) {
-          w8 = *reinterpret_cast<const uint4*>((c < G ? a.qn_w : a.kn_w) + j * 8);
-          *reinterpret_cast<float4*>(fr) = *reinterpret_cast<const float4*>(a.inv_freq + (j & 7) * 8);
-          *reinterpret_cast<float4*>(fr + 4) = *reinterpret_cast<const float4*>(a.inv_freq + (j & 7) * 8 + 4);
-        }
+        if (c <= G) w8 = *reinterpret_cast<const uint4*>((c < G ? a.qn_w : a.kn_w) + j * 8);
       }
       if (c == G + 1) {  // V row: raw
         s_new[(NQ + t) * 16 + j] = raw;
@@ -181,7 +182,11 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
         continue;
       }
       float cs[8], sn[8];
-      rope_cs8(pos, fr, cs, sn);
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        cs[i] = s_rope[t * 64 + (j & 7) * 8 + i];
+        sn[i] = s_rope[NQ * 64 + t * 64 + (j & 7) * 8 + i];
+      }
       const uint4 ov = qknorm_rope_row(raw, w8, cs, sn, a.eps, j);
       if (c < G) {
         float y[8];
@@ -715,7 +720,7 @@ static int prepare(const char* name, int nq, int nh, int nkv, int hd, void* k_ca
   if (out_dtype != SOLORT_DTYPE_BF16 && out_dtype != SOLORT_DTYPE_F32)
     return set_error(SOLORT_EINVAL, "%s: out_dtype %d", name, out_dtype);
   const int R = nq * G;
-  const size_t static_lds = (size_t)R * 128 * 4 + (size_t)2 * nq * 16 * 16 + 16;
+  const size_t static_lds = (size_t)R * 128 * 4 + (size_t)2 * nq * 16 * 16 + (size_t)2 * nq * 64 * 4 + 16;
   const size_t smem_max = decode_smem_bytes(R, n_split, true);
   const size_t comb_max = combine_floats(R, n_split, kCombineCols < R * 32 ? kCombineCols : R * 32) * 4;
   if (smem_max + static_lds > 64 * 1024 || comb_max > 64 * 1024)

@@ -198,6 +198,27 @@ def decode_layer(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps:
     _lib.check(rc, "decode_layer")
 
 
+def prefill_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, scale: float,
+                 out: torch.Tensor) -> None:
+    """Causal GQA attention of T prompt rows (q [T, nh, 128]) over cache rows 0..T-1 into
+    out [T, nh*128]; see solort_prefill_attn."""
+    _on_gpu("q", q, torch.bfloat16)
+    _need(q.dim() == 3 and q.shape[2] == HD and q.is_contiguous(), "q must be [T, nh, 128] contiguous")
+    T, nh = q.shape[0], q.shape[1]
+    nkv = k_cache.shape[1] if k_cache.dim() == 3 else -1
+    ts, hs, max_len = _cache_strides("k_cache", k_cache, nkv)
+    _on_gpu("v_cache", v_cache, torch.bfloat16)
+    _need(v_cache.shape == k_cache.shape and v_cache.stride() == k_cache.stride(),
+          "v_cache must match k_cache in shape and strides")
+    _need(out.is_cuda and out.dtype in (torch.bfloat16, torch.float32), "out must be bf16 or fp32 on the device")
+    _need(out.shape == (T, nh * HD) and out.is_contiguous() and out.data_ptr() % 16 == 0,
+          f"out must be [{T}, {nh * HD}] contiguous and 16-byte aligned")
+    dt = DTYPE_F32 if out.dtype == torch.float32 else DTYPE_BF16
+    rc = _lib.load().solort_prefill_attn(q.data_ptr(), T, nh, nkv, HD, k_cache.data_ptr(), v_cache.data_ptr(), ts,
+                                         hs, max_len, float(scale), out.data_ptr(), dt, _stream(q))
+    _lib.check(rc, "prefill_attn")
+
+
 def argmax_workspace(rows: int, device: torch.device | str) -> torch.Tensor:
     """Zero-filled workspace for argmax_rows (allocate once, reuse)."""
     nbytes = _lib.load().solort_argmax_workspace_bytes(rows)

@@ -87,6 +87,12 @@ class GraphQwen3Attention:
         self.vpos0 = torch.zeros(1, dtype=torch.long, device=self.dev)
         self.ws_ver = ops.attn_workspace(self.k1, nh, nkv, max(verify_splits(b) for b in self.buckets), self.dev)
         self._ver_graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        # prefill: padded prompt rows per layer, bucketed graphs
+        pmax = self.pre_buckets[-1]
+        self.qkv_pre = torch.zeros(layers, pmax, self.width, dtype=torch.bfloat16, device=self.dev)
+        self.q_pre = torch.zeros(pmax, nh, HD, dtype=torch.bfloat16, device=self.dev)
+        self.ctx_pre = torch.zeros(layers, pmax, nh * HD, dtype=torch.bfloat16, device=self.dev)
+        self._pre_graphs: dict[int, torch.cuda.CUDAGraph] = {}
 
     # ------------------------------------------------------------ decode
 
@@ -132,6 +138,34 @@ class GraphQwen3Attention:
         self.logits_dec.copy_(logits)
         self.decode(qkv, pos)
         return self.tok_dec
+
+    # ------------------------------------------------------------ prefill
+
+    def _prefill_forward(self, bound: int) -> None:
+        """cuda_graph_executor.py:109-130 (attention part): rows 0..bound-1 at positions 0..bound-1."""
+        for li in range(self.L):
+            ops.qknorm_rope_kvwrite(self.qkv_pre[li, :bound], self.qn_w[li], self.kn_w[li], self.eps, self.inv_freq,
+                                    None, self.q_pre[:bound], self.kc[li], self.vc[li], self.nh, self.nkv)
+            ops.prefill_attn(self.q_pre[:bound], self.kc[li], self.vc[li], self.scale, self.ctx_pre[li, :bound])
+
+    def prefill(self, qkv: torch.Tensor) -> torch.Tensor:
+        """Graphed bucketed prefill (cuda_graph_executor.py:149-161): qkv [layers, plen, width] for
+        prompt positions 0..plen-1, padded with zero rows to the first bucket >= plen.  Writes cache
+        rows 0..bucket-1 (padding rows included, as in the reference; decode never reads them) and
+        returns ctx [layers, plen, nh*128] (a view of the static buffer)."""
+        plen = int(qkv.shape[1])
+        bound = next((b for b in self.pre_buckets if b >= plen), None)
+        if bound is None or plen < 1:
+            raise RuntimeError(f"prompt length {plen} outside the prefill buckets {self.pre_buckets}")
+        self.qkv_pre[:, :plen].copy_(qkv)
+        self.qkv_pre[:, plen:bound].zero_()
+        if bound not in self._pre_graphs:
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._prefill_forward(bound)
+            self._pre_graphs[bound] = graph
+        self._pre_graphs[bound].replay()
+        return self.ctx_pre[:, :plen]
 
     # ------------------------------------------------------------ verify
 

@@ -1,0 +1,126 @@
+"""GPU parity of the MFMA causal prefill attention (with the prologue writing the cache first).
+
+Bars: bf16 output within max-abs 2e-2 / mean-abs 2e-3 of the reference's bf16
+SDPA (torch on CPU).  fp32 output against the fp64 evaluation of the kernel's
+own blockwise arithmetic (bf16 probabilities, oracle/exact.py
+prefill_blockwise): mean-abs <= 1e-5, at most 1% of the (row, head) outputs
+with an element off by more than 1e-4, max-abs <= 2e-2.  The stragglers are rare one-ulp flips in
+the bf16 rounding of a probability (the hardware exp2 is not correctly
+rounded, so fp64 cannot reproduce every rounding; one flip of p near 1 moves
+an output by up to 2^-8 * |V|); a wrong mask, scale or index shows up in the
+mean as errors of 1e-3 and more.  fp32 output against exact fp64 attention is
+reported.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import exact, ref
+from solort_amd import ops
+from solort_amd import workloads as wl
+
+pytestmark = pytest.mark.gpu
+HD = 128
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _prefill(gpu, T, shape=wl.QWEN3_4B, seed_T=None):
+    """Prologue + prefill on the GPU for a seeded prompt; returns (q, kc, vc, out_bf16, out_f32, case)."""
+    case = wl.prefill_case(T, layers=1)
+    nh, nkv = shape.nh, shape.nkv
+    qkv = case.qkv[0]
+    if shape is not wl.QWEN3_4B:  # other head counts: draw a prompt of that width
+        g = torch.Generator().manual_seed(2000 + T)
+        qkv = torch.randn(T, shape.qkv_width, generator=g).to(torch.bfloat16)
+    dev = gpu
+    kc = torch.zeros(case.max_len, nkv, HD, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    q = torch.empty(T, nh, HD, dtype=torch.bfloat16, device=dev)
+    ops.qknorm_rope_kvwrite(qkv.to(dev), case.qn_w[0].to(dev), case.kn_w[0].to(dev), wl.EPS,
+                            ops.inv_freq(HD, wl.THETA, dev), None, q, kc, vc, nh, nkv)
+    out = torch.empty(T, nh * HD, dtype=torch.bfloat16, device=dev)
+    out32 = torch.empty(T, nh * HD, dtype=torch.float32, device=dev)
+    ops.prefill_attn(q, kc, vc, shape.scale, out)
+    ops.prefill_attn(q, kc, vc, shape.scale, out32)
+    torch.cuda.synchronize()
+    return q, kc, vc, out, out32, qkv, case
+
+
+@pytest.mark.parametrize("T", [128, 512, 1024, 1, 17, 100, 1000])
+def test_prefill_qwen3_4b(gpu, T):
+    sh = wl.QWEN3_4B
+    _say(f"[prefill {sh.name} T={T}]")
+    q, kc, vc, out, out32, qkv, case = _prefill(gpu, T)
+    # reference ops on the CPU: prologue + causal SDPA with repeat_interleave, in bf16
+    cos, sin = ops.rope_tables(case.max_len, HD, wl.THETA, gpu)
+    c = torch.cat([cos.cpu()[:T]] * 2, -1)
+    s = torch.cat([sin.cpu()[:T]] * 2, -1)
+    qr, kr, vr = ref.prologue(qkv, case.qn_w[0], case.kn_w[0], wl.EPS, c, s, sh.nh, sh.nkv)
+    want = ref.prefill_attn(qr, kr, vr, sh.scale)
+    d = (out.float().cpu() - want.float()).abs()
+    _say(f"  bf16 vs reference ops: max-abs {d.max().item():.3e} mean-abs {d.mean().item():.3e}")
+    assert d.max().item() <= 2e-2 and d.mean().item() <= 2e-3
+    # fp32 output against the kernel's blockwise arithmetic and against exact attention, per head
+    qg = q.float().cpu().numpy()
+    kg = kc.float().cpu().numpy()[:T]
+    vg = vc.float().cpu().numpy()[:T]
+    o32 = out32.cpu().numpy().reshape(T, sh.nh, HD)
+    worst_blk, sum_blk, worst_exact, n_far = 0.0, 0.0, 0.0, 0
+    for h in range(sh.nh):
+        kvh = h // sh.group
+        blk = exact.prefill_blockwise(qg[:, h], kg[:, kvh], vg[:, kvh], sh.scale)
+        e = np.abs(o32[:, h] - blk)
+        worst_blk = max(worst_blk, float(e.max()))
+        sum_blk += float(e.sum())
+        n_far += int((e.max(axis=1) > 1e-4).sum())
+        if T <= 128:
+            ex = exact.causal_decode_fp64(qg[:, h][:, None, :], kg[:, kvh][:, None, :], vg[:, kvh][:, None, :], 0,
+                                          sh.scale)[:, 0]
+            worst_exact = max(worst_exact, float(np.abs(o32[:, h] - ex).max()))
+    mean_blk = sum_blk / o32.size
+    _say(f"  fp32 vs blockwise fp64: max-abs {worst_blk:.3e} mean-abs {mean_blk:.3e} rows-over-1e-4 {n_far}; "
+         f"vs exact fp64 (T<=128): {worst_exact:.3e}")
+    assert worst_blk <= 2e-2 and mean_blk <= 1e-5 and n_far <= 0.01 * T * sh.nh
+    assert torch.equal(out, out32.to(torch.bfloat16))
+
+
+def test_prefill_row0_and_last_row_pins(gpu):
+    """Row 0 attends only key 0 (output = V[0] per query group); the last row equals single-token decode
+    over the same cache at position T-1."""
+    sh = wl.QWEN3_4B
+    T = 300
+    q, kc, vc, out, out32, qkv, case = _prefill(gpu, T)
+    o = out32.reshape(T, sh.nh, HD)
+    v0 = vc[0].float().repeat_interleave(sh.group, 0)
+    assert torch.allclose(o[0], v0, atol=1e-6, rtol=0)
+    ws = ops.attn_workspace(1, sh.nh, sh.nkv, 8, gpu)
+    dec = torch.empty(1, sh.nh * HD, dtype=torch.float32, device=gpu)
+    pos = torch.tensor([T - 1], dtype=torch.long, device=gpu)
+    ops.decode_attn(q[T - 1:T].contiguous(), kc, vc, pos, 512, sh.scale, ws, 8, dec)
+    torch.cuda.synchronize()
+    # decode keeps fp32 probabilities, prefill rounds them to bf16: equal to bf16 precision
+    assert torch.allclose(o[T - 1], dec.reshape(sh.nh, HD), atol=2e-2, rtol=0)
+
+
+@pytest.mark.parametrize("shape", [wl.QWEN3_0_6B, wl.AttnShape("g1", 8, 8, 1)], ids=["g2", "g1"])
+def test_prefill_other_groups(gpu, shape):
+    T = 200
+    _say(f"[prefill {shape.name} T={T}]")
+    q, kc, vc, out, out32, qkv, case = _prefill(gpu, T, shape)
+    qg = q.float().cpu().numpy()
+    kg = kc.float().cpu().numpy()[:T]
+    vg = vc.float().cpu().numpy()[:T]
+    o32 = out32.cpu().numpy().reshape(T, shape.nh, HD)
+    for h in range(shape.nh):
+        kvh = h // shape.group
+        blk = exact.prefill_blockwise(qg[:, h], kg[:, kvh], vg[:, kvh], shape.scale)
+        e = np.abs(o32[:, h] - blk)
+        assert e.max() <= 2e-2 and e.mean() <= 1e-5 and (e.max(axis=1) > 1e-4).sum() <= max(1, 0.01 * T), h

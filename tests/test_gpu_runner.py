@@ -111,3 +111,45 @@ def test_verify_graph_replays_match_eager(gpu):
         assert torch.equal(ctx, out)
         assert torch.equal(r.tok_ver.cpu(), logits.argmax(-1))
     assert sorted(r._ver_graphs) == [128, 4096]
+
+
+def test_prefill_graph_then_decode_continues(gpu):
+    """Graphed bucketed prefill of a 300-row prompt equals eager launches; a decode step at position 300
+    then attends the prefilled rows exactly like decode over an eagerly written cache."""
+    r, g, sh = _make(gpu, layers=2, max_len=1024)
+    eager_kc, eager_vc = r.kc.clone(), r.vc.clone()
+    T = 300
+    qkv = torch.randn(r.L, T, r.width, generator=g).to(torch.bfloat16)
+    for rep in range(2):  # replays of the same bucket graph
+        ctx = r.prefill(qkv.to(gpu)).clone()
+    assert sorted(r._pre_graphs) == [512]
+    q = torch.empty(512, sh.nh, HD, dtype=torch.bfloat16, device=gpu)
+    padded = torch.zeros(r.L, 512, r.width, dtype=torch.bfloat16)
+    padded[:, :T] = qkv
+    out = torch.empty(r.L, 512, sh.nh * HD, dtype=torch.bfloat16, device=gpu)
+    for li in range(r.L):
+        ops.qknorm_rope_kvwrite(padded[li].to(gpu), r.qn_w[li], r.kn_w[li], r.eps, r.inv_freq, None, q,
+                                eager_kc[li], eager_vc[li], sh.nh, sh.nkv)
+        ops.prefill_attn(q, eager_kc[li], eager_vc[li], r.scale, out[li])
+    torch.cuda.synchronize()
+    assert torch.equal(r.kc, eager_kc) and torch.equal(r.vc, eager_vc)
+    assert torch.equal(ctx, out[:, :T])
+    # causal: rows < T do not depend on the zero padding rows
+    q2 = torch.empty(T, sh.nh, HD, dtype=torch.bfloat16, device=gpu)
+    kc2, vc2 = eager_kc.clone(), eager_vc.clone()
+    out2 = torch.empty(T, sh.nh * HD, dtype=torch.bfloat16, device=gpu)
+    ops.qknorm_rope_kvwrite(qkv[0].to(gpu), r.qn_w[0], r.kn_w[0], r.eps, r.inv_freq, None, q2, kc2[0], vc2[0],
+                            sh.nh, sh.nkv)
+    ops.prefill_attn(q2, kc2[0], vc2[0], r.scale, out2)
+    torch.cuda.synchronize()
+    assert torch.equal(out2, ctx[0])
+    # decode continues at position T over the prefilled cache
+    qd = torch.randn(r.L, 1, r.width, generator=g).to(torch.bfloat16)
+    dctx = r.decode(qd.to(gpu), T).clone()
+    ws = ops.attn_workspace(1, sh.nh, sh.nkv, 32, gpu)
+    p = torch.tensor([T], dtype=torch.long, device=gpu)
+    dout = torch.empty(1, sh.nh * HD, dtype=torch.bfloat16, device=gpu)
+    ops.decode_layer(qd[1].to(gpu), r.qn_w[1], r.kn_w[1], r.eps, r.inv_freq, p, eager_kc[1], eager_vc[1], 512,
+                     r.scale, ws, 32, dout, sh.nh, sh.nkv)
+    torch.cuda.synchronize()
+    assert torch.allclose(dctx[1].float(), dout.float(), atol=2e-3, rtol=0)

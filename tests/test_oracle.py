@@ -284,3 +284,25 @@ def test_planted_logits_answer_is_smallest_plant():
         assert len(plants) >= 2 and idx[r] == plants.min() and plants.min() < 1024
         assert plants.max() >= wl.VOCAB - 1024
     assert torch.equal(ref.argmax(x), torch.from_numpy(idx))
+
+
+def test_prefill_blockwise_equals_exact_without_rounding_and_close_with_it():
+    g = np.random.default_rng(21)
+    T = 200
+    q = g.standard_normal((T, HD))
+    k = g.standard_normal((T, HD))
+    v = g.standard_normal((T, HD))
+    want = exact.causal_decode_fp64(q[:, None, :], k[:, None, :], v[:, None, :], 0, SCALE)[:, 0]
+    # with the bf16 rounding of p removed (identity rounding) the blockwise algebra is exact attention
+    orig = exact.bf16_round
+    try:
+        exact.bf16_round = lambda x: np.asarray(x, np.float64)
+        got = exact.prefill_blockwise(q, k, v, SCALE)
+    finally:
+        exact.bf16_round = orig
+    assert np.allclose(got, want, atol=1e-12)
+    got_b = exact.prefill_blockwise(q, k, v, SCALE)
+    err = np.abs(got_b - want)
+    assert err.max() < 2e-2 and err.mean() < 2e-3
+    # row 0 sees only key 0
+    assert np.allclose(got_b[0], v[0], atol=1e-12)
