@@ -27,6 +27,10 @@ import time
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
+# HBM bytes per launch of the decode split kernel at KV 1024 (decode_kernel<1,4,2,true,false>),
+# from rocprofv3 --pmc FETCH_SIZE (x1.999: a 64 MiB copy reads 32786 KiB on it) plus
+# WRITE_SIZE (x1.000): (2140.0 * 1.999 + 524.0) KiB.  Re-measured whenever that kernel changes.
+DECODE_KERNEL_TRAFFIC = int((2140.0 * 1.999 + 524.0) * 1024)
 
 
 def decode_bytes(live: int, nh: int = 32, nkv: int = 8, hd: int = 128) -> int:
@@ -49,7 +53,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--kv-sets", type=int, default=8, help="independent KV caches rotated per step")
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
-    p.add_argument("--no-sweep", action="store_true", help="skip the per-bucket and prefill extras")
+    p.add_argument("--no-sweep", action="store_true", help="skip the per-bucket decode extras")
+    p.add_argument("--only", choices=("all", "decode", "prefill"), default="all",
+                   help="decode: the decode step and its kernel only; prefill: the prefill kernels only "
+                        "(for per-workload profiles)")
     return p.parse_args()
 
 
@@ -91,6 +98,10 @@ def main() -> int:
         runners.append(r)
     torch.cuda.synchronize()
 
+    if args.only == "prefill":
+        print(json.dumps({"prefill": prefill_extras(torch, ops, runners, dev, sh)}), flush=True)
+        return 0
+
     # ---------------------------------------------------------------- timed graph replays
     for i in range(args.warmup):
         runners[i % len(runners)]._graphs[bound].replay()
@@ -108,6 +119,11 @@ def main() -> int:
     kern_us = time_decode_kernel(torch, ops, runners, bound, ns, sh, dev, reps=4)
     kbytes = decode_bytes(live, sh.nh, sh.nkv)
     achieved = kbytes / (kern_us * 1e-6) / 1e9
+    # A plain 64 MiB device copy, outside every timed region: the reference point that scales the
+    # FETCH_SIZE / WRITE_SIZE hardware counters of a profiling run into bytes.
+    calib_src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    torch.empty_like(calib_src).copy_(calib_src)
+    torch.cuda.synchronize()
 
     result = {
         "metric": "decode-attn us/layer + HBM GB/s (Qwen3-4B, KV 1024); prefill attn TFLOP/s",
@@ -128,20 +144,22 @@ def main() -> int:
                    "n_split": ns},
         "decode_gbps": round(kbytes / (us_per_layer * 1e-6) / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4),
+                     "traffic": DECODE_KERNEL_TRAFFIC if live == 1024 else None,
                      "kernel": "solort_decode_layer = decode_kernel<1,4,2,fused> + combine_kernel<1,4>",
                      "kernel_us": round(kern_us, 3),
                      "algorithmic_bytes": kbytes},
     }
 
-    if not args.no_sweep:
+    if not args.no_sweep and args.only == "all":
         result["extras"] = extras(torch, ops, wl, runners, dev, sh)
+    if args.only == "all":
         result["prefill"] = prefill_extras(torch, ops, runners, dev, sh)
         p1024 = result["prefill"].get("1024")
         if p1024:
             result["prefill_tflops"] = p1024["tflops"]
 
-    if not args.no_cpu:
+    if not args.no_cpu and args.only == "all":
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, live)
 
     print(json.dumps(result), flush=True)
