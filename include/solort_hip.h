@@ -86,18 +86,19 @@ int solort_rope_table(const float* inv_freq, int half_dim, int64_t rows, void* c
                       solort_stream_t stream);
 
 /* Workspace bytes needed by solort_decode_attn / solort_verify_attn /
- * solort_decode_layer for `nq` query tokens and `n_split` key splits.  The
- * caller allocates it once, zero-fills it once, and reuses it: the kernels
- * leave it ready for the next call.  A workspace sized for (nq, n_split)
- * serves any call with the same nh/nkv and no larger nq or n_split.  Calls
- * that overlap in time must not share a workspace. */
+ * solort_decode_layer for `nq` query tokens and `n_split` key splits: the
+ * splits' partial results (per KV head and split: running max and sum, and
+ * the unnormalised [nq * group][128] output, fp32).  The caller allocates it
+ * once and reuses it; its contents need no initialisation.  A workspace sized
+ * for (nq, n_split) serves any call with the same nh/nkv and no larger nq or
+ * n_split.  Calls that overlap in time must not share a workspace. */
 size_t solort_attn_workspace_bytes(int nq, int nh, int nkv, int hd, int n_split);
 
 /*
  * Grouped-query attention of `nq` new tokens over the static KV cache, split
  * across `n_split` workgroups per KV head (flash-decoding), followed by the
- * log-sum-exp combine of the splits (a second launch on the same stream, or,
- * with SOLORT_DECODE_COMBINE=ticket, inside the first launch).
+ * log-sum-exp combine of the splits in a second launch on the same stream
+ * (none when n_split is 1).
  * Replaces the decode block cuda_graph_executor.py:168, :180-184 (nq = 1:
  * softmax(q K^T * scale, keys > pos masked) V over the bucket) and the verify
  * block :247-250, :261-263 (nq = K+1, query t at position pos0+t sees keys

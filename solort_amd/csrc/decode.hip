@@ -1,6 +1,6 @@
 // Split-KV (flash-decoding) grouped-query attention for 1..8 new tokens over
-// the static KV cache, with the log-sum-exp combine fused into the launch,
-// optionally fused with the QK-RMSNorm + RoPE prologue and KV write.
+// the static KV cache, optionally fused with the QK-RMSNorm + RoPE prologue
+// and KV write, followed by a small kernel that combines the splits.
 //
 // Reference semantics (src/solort/model/cuda_graph_executor.py):
 //   decode :168, :173-184  q/k norm + rope, KV write at pos, then
@@ -12,28 +12,31 @@
 // rounds scores and probabilities to bf16 between its torch ops); the output
 // is rounded once, to bf16, or left in fp32 on request.
 //
-// Grid: nkv * n_split workgroups of 256 threads.  Block b serves KV head
-// b % nkv and key split b / nkv.  The key range [0, bound) is cut into
+// Split kernel.  Grid: nkv * n_split workgroups of 256 threads; block b
+// serves KV head b % nkv and key split b / nkv (with 8 KV heads on 8 XCDs, all
+// splits of a head share one XCD's L2).  The key range [0, bound) is cut into
 // n_split static chunks, so every block issues its first K/V loads at launch,
 // before the device-side position has arrived; keys past the live length are
-// masked (and later iterations of long splits stop at the live length).
-// Inside a block, 16 row slots of 16 lanes each take one key row per step;
-// lane j of a slot loads dims [8j, 8j+8) of K and V as 16-byte vectors and
-// holds the q rows of the whole query group (nq * g rows) in registers, so a
-// KV head is read once for all of its query heads (no repeat_interleave).
-//
-// Fused variant: while the K/V loads are in flight, slots compute the q rows
-// and the new tokens' K/V rows from the fused qkv projection (qknorm_rope.h,
-// bit-identical to the standalone prologue).  Split 0 of each KV head writes
-// the new rows to the cache; every block substitutes the fresh rows for the
-// cache rows pos0..pos0+nq-1 it loaded, so no block depends on that write.
-//
-// Combine: each block merges its slots and waves, stores its partial
-// (running max in log2 units, sum, unnormalised output) to the workspace,
-// and takes a ticket (one agent-scope release per block).  The last block of
-// a KV head acquires, loads every split's partial with all loads issued
-// together, merges them and writes the output, then resets the ticket so the
-// workspace is ready for the next launch.
+// masked, and later iterations of a long split stop at the live length.
+//   - 16 row slots of 16 lanes each take U key rows per iteration; lane j of a
+//     slot loads dims [8j, 8j+8) of K and V as 16-byte vectors; q for the whole
+//     query group (nq * g rows) sits in registers, so each KV head is read once
+//     for all of its query heads (no repeat_interleave).  Dot products are
+//     reduced across the 16 lanes with DPP.
+//   - Scores and V rows of the iteration go to LDS; each thread then runs the
+//     online softmax for the output it owns (rows wave + 4i, two dims), so no
+//     per-slot state has to be merged.
+//   - Fused variant: while the K/V loads are in flight, every thread evaluates
+//     one RoPE cos/sin value into LDS and slots compute the q rows and the new
+//     tokens' K/V rows from the fused qkv projection (qknorm_rope.h, bit
+//     identical to the standalone prologue).  Split 0 of each KV head writes
+//     the new rows to the cache; every block substitutes the fresh rows for
+//     the cache rows pos0..pos0+nq-1 it loaded, so no block waits for that
+//     write.
+//   - Output: with one split the block writes the answer; otherwise its
+//     partial (running max in log2 units, sum, unnormalised output).
+// Combine kernel: merges the partials of each KV head (log-sum-exp); the
+// kernel boundary orders its reads after the split kernel's writes.
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -61,10 +64,9 @@ struct DecodeArgs {
   int64_t tok_stride;
   int64_t head_stride;
   const int64_t* pos0_dev;
-  float* ws_o;       // [nkv][n_split][R][128]
-  float* ws_ml;      // [nkv][n_split][R][2]
-  unsigned* ws_cnt;  // [nkv] tickets, zero between launches
-  void* out;         // [nq][nh][128]
+  float* ws_o;   // [nkv][n_split][R][128]
+  float* ws_ml;  // [nkv][n_split][R][2]: running max (log2 units), sum
+  void* out;     // [nq][nh][128]
   float qscale;      // softmax scale * log2(e)
   int nh, nkv, bound, n_split, out_f32;
 };
@@ -76,11 +78,6 @@ __device__ __forceinline__ float4 f4fma(float w, const float4 v, float4 acc) {
   acc.w = fmaf(w, v.w, acc.w);
   return acc;
 }
-
-template <int R, int G>
-__device__ __forceinline__ void combine_head(const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
-                                             int NS, int nh, int kvh, int c0, int c1, void* out, int out_f32,
-                                             float* smem);
 
 // Writes float4 column col of KV head kvh's [R][128] output block.
 __device__ __forceinline__ void store_out(void* out, int out_f32, int nh, int kvh, int G, int col, float4 O) {
@@ -97,17 +94,29 @@ __device__ __forceinline__ void store_out(void* out, int out_f32, int nh, int kv
   }
 }
 
-template <int NQ, int G, int U, bool FUSED, bool COMBINE>
-__global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
-  constexpr int R = NQ * G;  // query rows sharing one KV head
-  constexpr int C = R * 32;  // float4 columns of an [R][128] block
-  extern __shared__ __align__(16) float smem[];
-  __shared__ __align__(16) float s_q[R * 128];
-  __shared__ uint4 s_new[FUSED ? 2 * NQ * 16 : 1];  // fresh K rows then V rows (bf16 bits)
-  __shared__ float s_rope[FUSED ? 2 * NQ * 64 : 1];  // cos [t][64] then sin [t][64]
-  __shared__ unsigned s_ticket;
+// Writes dims d, d+1 of output row r (query t = r / G, head kvh*G + r % G).
+__device__ __forceinline__ void store_out2(void* out, int out_f32, int nh, int kvh, int G, int r, int d, float o0,
+                                           float o1) {
+  const int t = r / G, g = r % G;
+  const int64_t oi = ((int64_t)t * nh + kvh * G + g) * SOLORT_HD + d;
+  if (out_f32)
+    *reinterpret_cast<float2*>(reinterpret_cast<float*>(out) + oi) = make_float2(o0, o1);
+  else
+    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(out) + oi) = f2bf(o0) | (f2bf(o1) << 16);
+}
 
-  const int tid = threadIdx.x, j = tid & 15, slot = tid >> 4, wave = tid >> 6;
+template <int NQ, int G, int U, bool FUSED>
+__global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
+  constexpr int R = NQ * G;            // query rows sharing one KV head
+  constexpr int KPI = 16 * U;          // keys per iteration (16 slots x U)
+  constexpr int RPW = (R + 3) / 4;     // output rows per wavefront
+  __shared__ __align__(16) float s_q[R * 128];
+  __shared__ uint4 s_new[FUSED ? 2 * NQ * 16 : 1];   // fresh K rows then V rows (bf16 bits)
+  __shared__ float s_rope[FUSED ? 2 * NQ * 64 : 1];  // cos [t][64] then sin [t][64]
+  __shared__ __align__(16) uint4 s_v[KPI * 16];      // the iteration's V rows [key][16 x 16 B]
+  __shared__ float s_s[KPI * R];                     // its masked scores [key][row], log2 units
+
+  const int tid = threadIdx.x, j = tid & 15, slot = tid >> 4, wave = tid >> 6, lane = tid & 63;
   const int kvh = blockIdx.x % a.nkv;
   const int split = blockIdx.x / a.nkv;
   const int NS = a.n_split;
@@ -215,23 +224,26 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) qf[r][i] = s_q[r * 128 + j * 8 + i];
 
-  // 4. Online softmax over this split's live keys.
+  // 4. Per iteration: the 16 slots score U keys each (16-lane dot products
+  //    reduced with DPP) and stage the scores and V rows in LDS; then every
+  //    thread runs the online softmax for the output it owns - rows
+  //    wave + 4i, dims 2*lane and 2*lane+1 - so no per-slot state is merged.
   int64_t live64 = pos0 + NQ;
   live64 = live64 < 0 ? 0 : (live64 > a.bound ? a.bound : live64);
   const int kend = min(kstat, (int)live64);
-  float m[R], l[R], acc[R][8];
+  float M[RPW], L[RPW], O[RPW][2];
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    m[r] = -INFINITY;
-    l[r] = 0.f;
-#pragma unroll
-    for (int i = 0; i < 8; ++i) acc[r][i] = 0.f;
+  for (int i = 0; i < RPW; ++i) {
+    M[i] = -INFINITY;
+    L[i] = 0.f;
+    O[i][0] = O[i][1] = 0.f;
   }
-  for (int k0 = kbeg; k0 < kend; k0 += 16 * U) {
+  const uint32_t* s_v32 = reinterpret_cast<const uint32_t*>(s_v);
+  for (int k0 = kbeg; k0 < kend; k0 += KPI) {
     uint4 kn[U], vn[U];
-    const int k1 = k0 + 16 * U;
+    const int k1 = k0 + KPI;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {  // prefetch the next step of a long split
+    for (int u = 0; u < U; ++u) {  // prefetch the next iteration of a long split
       const int kid = k1 + u * 16 + slot;
       if (kid < kend) {
         kn[u] = *reinterpret_cast<const uint4*>(kp + (int64_t)kid * a.tok_stride);
@@ -241,68 +253,59 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
         vn[u] = make_uint4(0u, 0u, 0u, 0u);
       }
     }
-    int kid[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
-      kid[u] = k0 + u * 16 + slot;
+      const int kid = k0 + u * 16 + slot;
       if constexpr (FUSED) {
-        const int64_t off = (int64_t)kid[u] - pos0;
-        if (off >= 0 && off < NQ) {
+        const int64_t off = (int64_t)kid - pos0;
+        if (off >= 0 && off < NQ) {  // the new tokens' rows: fresh values, not the cache
           kr[u] = s_new[off * 16 + j];
           vr[u] = s_new[(NQ + off) * 16 + j];
         }
       }
-    }
-    float s[U][R];
-#pragma unroll
-    for (int u = 0; u < U; ++u) {
       float kf[8];
       unpack8(kr[u], kf);
+      const bool in = kid < kend;
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         float d = qf[r][0] * kf[0];
 #pragma unroll
         for (int i = 1; i < 8; ++i) d = fmaf(qf[r][i], kf[i], d);
-        s[u][r] = d;
+        d = row16_sum(d);
+        const int t = r / G;
+        if (!in || (int64_t)kid > pos0 + t) d = -INFINITY;
+        if (j == 0) s_s[(u * 16 + slot) * R + r] = d;
       }
+      s_v[(u * 16 + slot) * 16 + j] = vr[u];
     }
+    __syncthreads();
 #pragma unroll
-    for (int u = 0; u < U; ++u)
+    for (int i = 0; i < RPW; ++i) {
+      const int r = wave + 4 * i;
+      if (r < R) {
+        float mx = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < R; ++r) s[u][r] = row16_sum(s[u][r]);
+        for (int k = 0; k < KPI; ++k) mx = fmaxf(mx, s_s[k * R + r]);
+        const float mn = fmaxf(M[i], mx);
+        if (mn != -INFINITY) {
+          const float alpha = fast_exp2(M[i] - mn);  // M = -inf gives 0
+          float l = L[i] * alpha, o0 = O[i][0] * alpha, o1 = O[i][1] * alpha;
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      const bool in = kid[u] < kend;
-#pragma unroll
-      for (int t = 0; t < NQ; ++t)
-#pragma unroll
-        for (int g = 0; g < G; ++g)
-          if (!in || (int64_t)kid[u] > pos0 + t) s[u][t * G + g] = -INFINITY;
-    }
-    float vf[U][8];
-#pragma unroll
-    for (int u = 0; u < U; ++u) unpack8(vr[u], vf[u]);
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float mx = m[r];
-#pragma unroll
-      for (int u = 0; u < U; ++u) mx = fmaxf(mx, s[u][r]);
-      if (mx != -INFINITY) {
-        const float alpha = fast_exp2(m[r] - mx);  // m = -inf gives 0
-        float ls = l[r] * alpha;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) acc[r][i] *= alpha;
-#pragma unroll
-        for (int u = 0; u < U; ++u) {
-          const float p = fast_exp2(s[u][r] - mx);
-          ls += p;
-#pragma unroll
-          for (int i = 0; i < 8; ++i) acc[r][i] = fmaf(p, vf[u][i], acc[r][i]);
+          for (int k = 0; k < KPI; ++k) {
+            const float p = fast_exp2(s_s[k * R + r] - mn);  // masked: 0
+            const uint32_t v2 = s_v32[k * 64 + lane];
+            l += p;
+            o0 = fmaf(p, __uint_as_float(v2 << 16), o0);
+            o1 = fmaf(p, __uint_as_float(v2 & 0xffff0000u), o1);
+          }
+          L[i] = l;
+          O[i][0] = o0;
+          O[i][1] = o1;
+          M[i] = mn;
         }
-        l[r] = ls;
-        m[r] = mx;
       }
     }
+    __syncthreads();  // s_s and s_v are rewritten by the next iteration
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       kr[u] = kn[u];
@@ -310,235 +313,20 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     }
   }
 
-  // 5. Merge the 16 row slots into this split's partial (running max in
-  //    log2 units, sum, unnormalised output), as float4 columns col of the
-  //    [R][128] block: thread col < C handles dims 4*(col%32).. of row col/32.
-  float4 part_o[(C + 255) / 256];
-  float part_m[(C + 255) / 256], part_l[(C + 255) / 256];
-  if constexpr (R <= 4) {
-    // Every slot's state goes to LDS, then each column merges 16 slots.
-    float* s_acc = smem;               // [16][R][128]
-    float* s_m = smem + 16 * R * 128;  // [16][R]
-    float* s_l = s_m + 16 * R;         // [16][R]
+  // 5. One split: the answer; otherwise this split's partial (max, sum,
+  //    unnormalised output) for the combine kernel.
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float4* dst = reinterpret_cast<float4*>(s_acc + (slot * R + r) * 128 + j * 8);
-      dst[0] = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
-      dst[1] = make_float4(acc[r][4], acc[r][5], acc[r][6], acc[r][7]);
-      if (j == 0) {
-        s_m[slot * R + r] = m[r];
-        s_l[slot * R + r] = l[r];
-      }
+  for (int i = 0; i < RPW; ++i) {
+    const int r = wave + 4 * i;
+    if (r >= R) continue;
+    if (NS == 1) {
+      const float inv = L[i] > 0.f ? 1.f / L[i] : 0.f;
+      store_out2(a.out, a.out_f32, a.nh, kvh, G, r, 2 * lane, O[i][0] * inv, O[i][1] * inv);
+    } else {
+      const int64_t pr = (int64_t)(kvh * NS + split) * R + r;
+      *reinterpret_cast<float2*>(a.ws_o + pr * 128 + 2 * lane) = make_float2(O[i][0], O[i][1]);
+      if (lane == 0) *reinterpret_cast<float2*>(a.ws_ml + pr * 2) = make_float2(M[i], L[i]);
     }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < (C + 255) / 256; ++k) {
-      const int col = tid + 256 * k;
-      if (col < C) {
-        const int r = col >> 5, d = (col & 31) * 4;
-        float M = -INFINITY;
-#pragma unroll
-        for (int w = 0; w < 16; ++w) M = fmaxf(M, s_m[w * R + r]);
-        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-        float L = 0.f;
-#pragma unroll
-        for (int w = 0; w < 16; ++w) {
-          const float mw = s_m[w * R + r];
-          const float sc = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
-          O = f4fma(sc, *reinterpret_cast<const float4*>(s_acc + (w * R + r) * 128 + d), O);
-          L = fmaf(s_l[w * R + r], sc, L);
-        }
-        part_o[k] = O;
-        part_m[k] = M;
-        part_l[k] = L;
-      }
-    }
-  } else {
-    // Larger query groups: merge the 4 slots of each wavefront with lane
-    // exchanges first, then the 4 wavefronts through LDS.
-#pragma unroll
-    for (int mask = 16; mask <= 32; mask <<= 1) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const float mo = xshfl(m[r], mask), lo = xshfl(l[r], mask);
-        const float mn = fmaxf(m[r], mo);
-        const float sa = (m[r] == -INFINITY) ? 0.f : fast_exp2(m[r] - mn);
-        const float sb = (mo == -INFINITY) ? 0.f : fast_exp2(mo - mn);
-        l[r] = l[r] * sa + lo * sb;
-#pragma unroll
-        for (int i = 0; i < 8; ++i) {
-          const float ao = xshfl(acc[r][i], mask);
-          acc[r][i] = acc[r][i] * sa + ao * sb;
-        }
-        m[r] = mn;
-      }
-    }
-    float* s_acc = smem;              // [4][R][128]
-    float* s_m = smem + 4 * R * 128;  // [4][R]
-    float* s_l = s_m + 4 * R;         // [4][R]
-    if ((tid & 63) < 16) {
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        float4* dst = reinterpret_cast<float4*>(s_acc + (wave * R + r) * 128 + j * 8);
-        dst[0] = make_float4(acc[r][0], acc[r][1], acc[r][2], acc[r][3]);
-        dst[1] = make_float4(acc[r][4], acc[r][5], acc[r][6], acc[r][7]);
-        if (j == 0) {
-          s_m[wave * R + r] = m[r];
-          s_l[wave * R + r] = l[r];
-        }
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int k = 0; k < (C + 255) / 256; ++k) {
-      const int col = tid + 256 * k;
-      if (col < C) {
-        const int r = col >> 5, d = (col & 31) * 4;
-        float M = s_m[r];
-#pragma unroll
-        for (int w = 1; w < 4; ++w) M = fmaxf(M, s_m[w * R + r]);
-        float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-        float L = 0.f;
-#pragma unroll
-        for (int w = 0; w < 4; ++w) {
-          const float mw = s_m[w * R + r];
-          const float sc = (mw == -INFINITY) ? 0.f : fast_exp2(mw - M);
-          O = f4fma(sc, *reinterpret_cast<const float4*>(s_acc + (w * R + r) * 128 + d), O);
-          L = fmaf(s_l[w * R + r], sc, L);
-        }
-        part_o[k] = O;
-        part_m[k] = M;
-        part_l[k] = L;
-      }
-    }
-  }
-
-  // 6. One split: the partial is the answer.
-  if (NS == 1) {
-#pragma unroll
-    for (int k = 0; k < (C + 255) / 256; ++k) {
-      const int col = tid + 256 * k;
-      if (col < C) {
-        const float inv = part_l[k] > 0.f ? 1.f / part_l[k] : 0.f;
-        float4 O = part_o[k];
-        O.x *= inv; O.y *= inv; O.z *= inv; O.w *= inv;
-        store_out(a.out, a.out_f32, a.nh, kvh, G, col, O);
-      }
-    }
-    return;
-  }
-
-  // 7. Store the partial.
-  {
-    float4* wo = reinterpret_cast<float4*>(a.ws_o + (int64_t)(kvh * NS + split) * R * 128);
-    float* wml = a.ws_ml + (int64_t)(kvh * NS + split) * R * 2;
-#pragma unroll
-    for (int k = 0; k < (C + 255) / 256; ++k) {
-      const int col = tid + 256 * k;
-      if (col < C) {
-        wo[col] = part_o[k];
-        if ((col & 31) == 0) *reinterpret_cast<float2*>(wml + (col >> 5) * 2) = make_float2(part_m[k], part_l[k]);
-      }
-    }
-  }
-  if constexpr (!COMBINE) {
-    return;  // solort_attn_combine merges the partials in the next launch
-  } else {
-    // 8. Ticket: the last block of this KV head merges every split's partial.
-    __syncthreads();
-    if (tid == 0) {
-      fence_release_agent();
-      s_ticket = __hip_atomic_fetch_add(a.ws_cnt + kvh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    __syncthreads();
-    if (s_ticket != (unsigned)(NS - 1)) return;
-    fence_acquire_agent();
-    combine_head<R, G>(a.ws_o, a.ws_ml, NS, a.nh, kvh, 0, C, a.out, a.out_f32, smem);
-    if (tid == 0) a.ws_cnt[kvh] = 0u;
-  }
-}
-
-// Merges the n_split partials of KV head kvh for float4 columns [c0, c1) of
-// its [R][128] output block and writes them (the log-sum-exp combine).  A
-// thread's first batch of partial loads is issued before anything waits; the
-// per-row maximum and sum are wavefront reductions.
-template <int R, int G>
-__device__ __forceinline__ void combine_head(const float* __restrict__ ws_o, const float* __restrict__ ws_ml,
-                                             int NS, int nh, int kvh, int c0, int c1, void* out, int out_f32,
-                                             float* smem) {
-  constexpr int C = R * 32;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int ncol = c1 - c0;
-  const int SG = ncol >= 256 ? 1 : 256 / ncol;  // split groups sharing one column
-  constexpr int B = 16;                          // loads issued together per thread
-  const int NSR4 = (NS * R + 3) & ~3;
-  float* s_m = smem;                             // [NS][R] maxima
-  float* s_l = smem + NSR4;                      // [NS][R] sums
-  float* s_w = smem + 2 * NSR4;                  // [NS][R] combine weights
-  float4* s_red = reinterpret_cast<float4*>(smem + 3 * NSR4);  // [SG][ncol]
-  const float* wml_all = ws_ml + (int64_t)kvh * NS * R * 2;
-  const float4* wo4 = reinterpret_cast<const float4*>(ws_o + (int64_t)kvh * NS * R * 128);
-
-  const int col0 = c0 + tid % ncol, sg0 = tid / ncol;
-  const bool act0 = tid < ncol * SG;
-  float4 v[B];
-#pragma unroll
-  for (int k = 0; k < B; ++k) {
-    const int s = sg0 + k * SG;
-    v[k] = (act0 && s < NS) ? wo4[(int64_t)s * C + col0] : make_float4(0.f, 0.f, 0.f, 0.f);
-  }
-
-  // Combine weights exp2(m_s - M) / L for the rows this block writes.
-  const int r0 = c0 >> 5, r1 = (c1 - 1) >> 5;
-  for (int r = r0 + wave; r <= r1; r += 4) {
-    float mx = -INFINITY;
-    for (int s = lane; s < NS; s += 64) {
-      const float2 ml = *reinterpret_cast<const float2*>(wml_all + (s * R + r) * 2);
-      s_m[s * R + r] = ml.x;
-      s_l[s * R + r] = ml.y;
-      mx = fmaxf(mx, ml.x);
-    }
-    mx = wave_max(mx);
-    float sum = 0.f;
-    for (int s = lane; s < NS; s += 64) {
-      const float ms = s_m[s * R + r];
-      if (ms != -INFINITY) sum = fmaf(s_l[s * R + r], fast_exp2(ms - mx), sum);
-    }
-    sum = wave_sum(sum);
-    const float inv = sum > 0.f ? 1.f / sum : 0.f;
-    for (int s = lane; s < NS; s += 64) {
-      const float ms = s_m[s * R + r];
-      s_w[s * R + r] = (ms == -INFINITY) ? 0.f : fast_exp2(ms - mx) * inv;
-    }
-  }
-  __syncthreads();
-  for (int base = tid; base < ncol * SG; base += 256) {
-    const int col = c0 + base % ncol, sg = base / ncol, r = col >> 5;
-    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s0 = sg; s0 < NS; s0 += SG * B) {
-      if (!(base == tid && s0 == sg)) {
-#pragma unroll
-        for (int k = 0; k < B; ++k) {
-          const int s = s0 + k * SG;
-          v[k] = s < NS ? wo4[(int64_t)s * C + col] : make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-      }
-#pragma unroll
-      for (int k = 0; k < B; ++k) {
-        const int s = s0 + k * SG;
-        if (s < NS) O = f4fma(s_w[s * R + r], v[k], O);
-      }
-    }
-    s_red[(SG == 1 ? 0 : sg) * ncol + (col - c0)] = O;
-  }
-  __syncthreads();
-  for (int cc = tid; cc < ncol; cc += 256) {
-    float4 O = s_red[cc];
-    for (int sg = 1; sg < SG; ++sg) {
-      const float4 o2 = s_red[sg * ncol + cc];
-      O.x += o2.x; O.y += o2.y; O.z += o2.z; O.w += o2.w;
-    }
-    store_out(out, out_f32, nh, kvh, G, c0 + cc, O);
   }
 }
 
@@ -546,82 +334,114 @@ struct CombineArgs {
   const float* ws_o;
   const float* ws_ml;
   void* out;
-  int nh, nkv, n_split, out_f32, cols_per_block;
+  int nh, nkv, n_split, out_f32;
 };
 
-// Grid: nkv * ceil(C / cols_per_block) blocks; block b merges KV head b % nkv,
-// float4 columns [cb * cols_per_block, ...) with cb = b / nkv.
+// The log-sum-exp combine of the n_split partials of each KV head.  Block =
+// (KV head, 32 float4 columns of its [R][128] output); thread = (column,
+// split group sg of 8): it merges splits sg, sg+8, ... on its own (all loads
+// issued together), then the 8 split groups meet once in LDS.
 template <int NQ, int G>
 __global__ __launch_bounds__(256) void combine_kernel(const CombineArgs a) {
   constexpr int R = NQ * G;
-  constexpr int C = R * 32;
-  extern __shared__ __align__(16) float smem[];
+  constexpr int C = R * 32;  // float4 columns
+  constexpr int B = 8;       // splits per thread per batch
+  __shared__ float s_m[8][32], s_l[8][32];
+  __shared__ float4 s_o[8][32];
+  const int tid = threadIdx.x, c = tid & 31, sg = tid >> 5;
   const int kvh = blockIdx.x % a.nkv, cb = blockIdx.x / a.nkv;
-  const int c0 = cb * a.cols_per_block;
-  const int c1 = min(c0 + a.cols_per_block, C);
-  combine_head<R, G>(a.ws_o, a.ws_ml, a.n_split, a.nh, kvh, c0, c1, a.out, a.out_f32, smem);
+  const int col = cb * 32 + c;
+  const bool act = col < C;
+  const int r = col >> 5;
+  const int NS = a.n_split;
+  const float2* wml = reinterpret_cast<const float2*>(a.ws_ml) + (int64_t)kvh * NS * R;
+  const float4* wo = reinterpret_cast<const float4*>(a.ws_o) + (int64_t)kvh * NS * C;
+  float mloc = -INFINITY, lloc = 0.f;
+  float4 oloc = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int s0 = sg; s0 < NS; s0 += 8 * B) {
+    float2 ml[B];
+    float4 ov[B];
+#pragma unroll
+    for (int k = 0; k < B; ++k) {
+      const int s = s0 + 8 * k;
+      if (act && s < NS) {
+        ml[k] = wml[(int64_t)s * R + r];
+        ov[k] = wo[(int64_t)s * C + col];
+      } else {
+        ml[k] = make_float2(-INFINITY, 0.f);
+        ov[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    float mb = mloc;
+#pragma unroll
+    for (int k = 0; k < B; ++k) mb = fmaxf(mb, ml[k].x);
+    if (mb != -INFINITY) {
+      const float sc = fast_exp2(mloc - mb);  // mloc = -inf gives 0
+      lloc *= sc;
+      oloc.x *= sc; oloc.y *= sc; oloc.z *= sc; oloc.w *= sc;
+#pragma unroll
+      for (int k = 0; k < B; ++k) {
+        const float w = (ml[k].x == -INFINITY) ? 0.f : fast_exp2(ml[k].x - mb);
+        lloc = fmaf(w, ml[k].y, lloc);
+        oloc = f4fma(w, ov[k], oloc);
+      }
+      mloc = mb;
+    }
+  }
+  s_m[sg][c] = mloc;
+  s_l[sg][c] = lloc;
+  s_o[sg][c] = oloc;
+  __syncthreads();
+  if (tid < 32 && act) {
+    float Mx = -INFINITY;
+#pragma unroll
+    for (int g = 0; g < 8; ++g) Mx = fmaxf(Mx, s_m[g][c]);
+    float Ls = 0.f;
+    float4 Os = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (Mx != -INFINITY) {
+#pragma unroll
+      for (int g = 0; g < 8; ++g) {
+        const float w = (s_m[g][c] == -INFINITY) ? 0.f : fast_exp2(s_m[g][c] - Mx);
+        Ls = fmaf(w, s_l[g][c], Ls);
+        Os = f4fma(w, s_o[g][c], Os);
+      }
+    }
+    const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+    Os.x *= inv; Os.y *= inv; Os.z *= inv; Os.w *= inv;
+    store_out(a.out, a.out_f32, a.nh, kvh, G, col, Os);
+  }
 }
 
 // ---------------------------------------------------------------- host side
 
 constexpr int kMaxRows = 20;  // nq * group limit (registers and LDS)
 constexpr int kMaxSplit = 1024;
-constexpr int kCombineCols = 32;  // float4 columns per block of the combine kernel
 
 struct WsLayout {
-  size_t o_off, ml_off, cnt_off, total;
+  size_t ml_off, o_off, total;
 };
 
 static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
-// The tickets sit at offset 0 whatever the split count, so one workspace sized
-// for the largest split count can serve launches with any smaller one: every
-// launch leaves its tickets at zero, and the partials it leaves behind never
-// overlap another launch's tickets.
 static WsLayout ws_layout(int nq, int nh, int nkv, int n_split) {
   const size_t R = (size_t)nq * (nh / nkv);
   WsLayout w;
-  w.cnt_off = 0;
-  w.ml_off = align256((size_t)nkv * sizeof(unsigned));
-  w.o_off = align256(w.ml_off + (size_t)nkv * n_split * R * 2 * sizeof(float));
+  w.ml_off = 0;
+  w.o_off = align256((size_t)nkv * n_split * R * 2 * sizeof(float));
   w.total = align256(w.o_off + (size_t)nkv * n_split * R * 128 * sizeof(float));
   return w;
 }
 
-static size_t combine_floats(int R, int n_split, int ncol) {
-  const int SG = ncol >= 256 ? 1 : 256 / ncol;
-  return 3 * (((size_t)n_split * R + 3) & ~(size_t)3) + (size_t)SG * ncol * 4;
-}
-
-static size_t decode_smem_bytes(int R, int n_split, bool combine_in_kernel) {
-  const size_t main_f = R <= 4 ? (size_t)16 * R * 128 + 32 * R : (size_t)4 * R * 128 + 8 * R;
-  const size_t comb_f = combine_in_kernel ? combine_floats(R, n_split, R * 32) : 0;
-  return (main_f > comb_f ? main_f : comb_f) * sizeof(float);
-}
-
-// How the split partials are merged: 0 = a separate combine launch (the
-// kernel boundary orders the partials; the default), 1 = the last block of
-// each KV head merges them inside the same launch (agent-scope release and
-// acquire around an atomic ticket).  SOLORT_DECODE_COMBINE=ticket selects 1.
-static int combine_mode() {
-  static int mode = -1;
-  if (mode < 0) {
-    const char* e = getenv("SOLORT_DECODE_COMBINE");
-    mode = (e && strcmp(e, "ticket") == 0) ? 1 : 0;
-  }
-  return mode;
-}
-
-template <int NQ, int G, bool FUSED, bool COMBINE>
-static bool launch_u(int U, const DecodeArgs& a, int blocks, size_t smem, hipStream_t s) {
+template <int NQ, int G, bool FUSED>
+static bool launch_u(int U, const DecodeArgs& a, int blocks, hipStream_t s) {
   if constexpr (NQ * G <= kMaxRows) {
     if constexpr (NQ == 1) {
       if (U == 4) {
-        hipLaunchKernelGGL((decode_kernel<NQ, G, 4, FUSED, COMBINE>), dim3(blocks), dim3(256), smem, s, a);
+        hipLaunchKernelGGL((decode_kernel<NQ, G, 4, FUSED>), dim3(blocks), dim3(256), 0, s, a);
         return true;
       }
     }
-    hipLaunchKernelGGL((decode_kernel<NQ, G, 2, FUSED, COMBINE>), dim3(blocks), dim3(256), smem, s, a);
+    hipLaunchKernelGGL((decode_kernel<NQ, G, 2, FUSED>), dim3(blocks), dim3(256), 0, s, a);
     return true;
   } else {
     return false;
@@ -629,67 +449,60 @@ static bool launch_u(int U, const DecodeArgs& a, int blocks, size_t smem, hipStr
 }
 
 template <int NQ, int G>
-static bool launch_combine(const CombineArgs& c, int blocks, size_t smem, hipStream_t s) {
+static bool launch_combine(const CombineArgs& c, int blocks, hipStream_t s) {
   if constexpr (NQ * G <= kMaxRows) {
-    hipLaunchKernelGGL((combine_kernel<NQ, G>), dim3(blocks), dim3(256), smem, s, c);
+    hipLaunchKernelGGL((combine_kernel<NQ, G>), dim3(blocks), dim3(256), 0, s, c);
     return true;
   } else {
     return false;
   }
 }
 
-// Dispatches on (nq, G) to fn<NQ, G>(args...).
-#define SOLORT_DISPATCH_NQ(G, FN, ...)                       \
-  switch (nq) {                                              \
-    case 1: return FN<1, G>(__VA_ARGS__);                    \
-    case 2: return FN<2, G>(__VA_ARGS__);                    \
-    case 3: return FN<3, G>(__VA_ARGS__);                    \
-    case 4: return FN<4, G>(__VA_ARGS__);                    \
-    case 5: return FN<5, G>(__VA_ARGS__);                    \
-    case 6: return FN<6, G>(__VA_ARGS__);                    \
-    case 7: return FN<7, G>(__VA_ARGS__);                    \
-    case 8: return FN<8, G>(__VA_ARGS__);                    \
-  }                                                          \
+// Dispatches on nq to FN<NQ, G>(args...).
+#define SOLORT_DISPATCH_NQ(G, FN, ...)    \
+  switch (nq) {                           \
+    case 1: return FN<1, G>(__VA_ARGS__); \
+    case 2: return FN<2, G>(__VA_ARGS__); \
+    case 3: return FN<3, G>(__VA_ARGS__); \
+    case 4: return FN<4, G>(__VA_ARGS__); \
+    case 5: return FN<5, G>(__VA_ARGS__); \
+    case 6: return FN<6, G>(__VA_ARGS__); \
+    case 7: return FN<7, G>(__VA_ARGS__); \
+    case 8: return FN<8, G>(__VA_ARGS__); \
+  }                                       \
   return false;
 
 template <int NQ, int G>
-static bool launch_attn(bool fused, bool combine, int U, const DecodeArgs& a, int blocks, size_t smem,
-                        hipStream_t s) {
-  if (fused)
-    return combine ? launch_u<NQ, G, true, true>(U, a, blocks, smem, s)
-                   : launch_u<NQ, G, true, false>(U, a, blocks, smem, s);
-  return combine ? launch_u<NQ, G, false, true>(U, a, blocks, smem, s)
-                 : launch_u<NQ, G, false, false>(U, a, blocks, smem, s);
+static bool launch_attn(bool fused, int U, const DecodeArgs& a, int blocks, hipStream_t s) {
+  return fused ? launch_u<NQ, G, true>(U, a, blocks, s) : launch_u<NQ, G, false>(U, a, blocks, s);
 }
 
 template <int G>
-static bool attn_nq(int nq, bool fused, bool combine, int U, const DecodeArgs& a, int blocks, size_t smem,
-                    hipStream_t s) {
-  SOLORT_DISPATCH_NQ(G, launch_attn, fused, combine, U, a, blocks, smem, s)
+static bool attn_nq(int nq, bool fused, int U, const DecodeArgs& a, int blocks, hipStream_t s) {
+  SOLORT_DISPATCH_NQ(G, launch_attn, fused, U, a, blocks, s)
 }
 
 template <int G>
-static bool combine_nq(int nq, const CombineArgs& c, int blocks, size_t smem, hipStream_t s) {
-  SOLORT_DISPATCH_NQ(G, launch_combine, c, blocks, smem, s)
+static bool combine_nq(int nq, const CombineArgs& c, int blocks, hipStream_t s) {
+  SOLORT_DISPATCH_NQ(G, launch_combine, c, blocks, s)
 }
 
-static bool dispatch_attn(int G, int nq, bool fused, bool combine, int U, const DecodeArgs& a, int blocks,
-                          size_t smem, hipStream_t s) {
+static bool dispatch_attn(int G, int nq, bool fused, int U, const DecodeArgs& a, int blocks, hipStream_t s) {
   switch (G) {
-    case 1: return attn_nq<1>(nq, fused, combine, U, a, blocks, smem, s);
-    case 2: return attn_nq<2>(nq, fused, combine, U, a, blocks, smem, s);
-    case 4: return attn_nq<4>(nq, fused, combine, U, a, blocks, smem, s);
-    case 8: return attn_nq<8>(nq, fused, combine, U, a, blocks, smem, s);
+    case 1: return attn_nq<1>(nq, fused, U, a, blocks, s);
+    case 2: return attn_nq<2>(nq, fused, U, a, blocks, s);
+    case 4: return attn_nq<4>(nq, fused, U, a, blocks, s);
+    case 8: return attn_nq<8>(nq, fused, U, a, blocks, s);
   }
   return false;
 }
 
-static bool dispatch_combine(int G, int nq, const CombineArgs& c, int blocks, size_t smem, hipStream_t s) {
+static bool dispatch_combine(int G, int nq, const CombineArgs& c, int blocks, hipStream_t s) {
   switch (G) {
-    case 1: return combine_nq<1>(nq, c, blocks, smem, s);
-    case 2: return combine_nq<2>(nq, c, blocks, smem, s);
-    case 4: return combine_nq<4>(nq, c, blocks, smem, s);
-    case 8: return combine_nq<8>(nq, c, blocks, smem, s);
+    case 1: return combine_nq<1>(nq, c, blocks, s);
+    case 2: return combine_nq<2>(nq, c, blocks, s);
+    case 4: return combine_nq<4>(nq, c, blocks, s);
+    case 8: return combine_nq<8>(nq, c, blocks, s);
   }
   return false;
 }
@@ -719,12 +532,6 @@ static int prepare(const char* name, int nq, int nh, int nkv, int hd, void* k_ca
     return set_error(SOLORT_EINVAL, "%s: n_split %d outside [1, %d]", name, n_split, kMaxSplit);
   if (out_dtype != SOLORT_DTYPE_BF16 && out_dtype != SOLORT_DTYPE_F32)
     return set_error(SOLORT_EINVAL, "%s: out_dtype %d", name, out_dtype);
-  const int R = nq * G;
-  const size_t static_lds = (size_t)R * 128 * 4 + (size_t)2 * nq * 16 * 16 + (size_t)2 * nq * 64 * 4 + 16;
-  const size_t smem_max = decode_smem_bytes(R, n_split, true);
-  const size_t comb_max = combine_floats(R, n_split, kCombineCols < R * 32 ? kCombineCols : R * 32) * 4;
-  if (smem_max + static_lds > 64 * 1024 || comb_max > 64 * 1024)
-    return set_error(SOLORT_EINVAL, "%s: n_split %d too large for %d query rows", name, n_split, R);
   const WsLayout w = ws_layout(nq, nh, nkv, n_split);
   a.kc = (uint16_t*)k_cache;
   a.vc = (uint16_t*)v_cache;
@@ -733,7 +540,6 @@ static int prepare(const char* name, int nq, int nh, int nkv, int hd, void* k_ca
   a.pos0_dev = pos0_dev;
   a.ws_o = (float*)((char*)ws + w.o_off);
   a.ws_ml = (float*)((char*)ws + w.ml_off);
-  a.ws_cnt = (unsigned*)((char*)ws + w.cnt_off);
   a.out = out;
   a.qscale = scale * 1.4426950408889634f;
   a.nh = nh;
@@ -746,15 +552,13 @@ static int prepare(const char* name, int nq, int nh, int nkv, int hd, void* k_ca
   return 0;
 }
 
-// Launches the split kernel and, in the default mode, the combine kernel.
+// Launches the split kernel, then (more than one split) the combine kernel.
 static int launch_all(const char* name, bool fused, int nq, const DecodeArgs& a, int U, hipStream_t s) {
-  const int G = a.nh / a.nkv, R = nq * G, C = R * 32;
-  const bool in_kernel = a.n_split > 1 && combine_mode() == 1;
-  const size_t smem = decode_smem_bytes(R, a.n_split, in_kernel);
-  if (!dispatch_attn(G, nq, fused, in_kernel, U, a, a.n_split * a.nkv, smem, s))
+  const int G = a.nh / a.nkv, C = nq * G * 32;
+  if (!dispatch_attn(G, nq, fused, U, a, a.n_split * a.nkv, s))
     return set_error(SOLORT_EINVAL, "%s: no kernel for nq=%d group=%d", name, nq, G);
   int rc = check_launch(name);
-  if (rc || a.n_split == 1 || in_kernel) return rc;
+  if (rc || a.n_split == 1) return rc;
   CombineArgs c;
   c.ws_o = a.ws_o;
   c.ws_ml = a.ws_ml;
@@ -763,10 +567,7 @@ static int launch_all(const char* name, bool fused, int nq, const DecodeArgs& a,
   c.nkv = a.nkv;
   c.n_split = a.n_split;
   c.out_f32 = a.out_f32;
-  c.cols_per_block = kCombineCols < C ? kCombineCols : C;
-  const int cb = (C + c.cols_per_block - 1) / c.cols_per_block;
-  const size_t csmem = combine_floats(R, a.n_split, c.cols_per_block) * sizeof(float);
-  if (!dispatch_combine(G, nq, c, cb * a.nkv, csmem, s))
+  if (!dispatch_combine(G, nq, c, ((C + 31) / 32) * a.nkv, s))
     return set_error(SOLORT_EINVAL, "%s: no combine kernel for nq=%d group=%d", name, nq, G);
   return check_launch(name);
 }

@@ -81,21 +81,27 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
   const int kend = min(a.T, q0 + RW);
   const int kg = tid >> 4, dg = tid & 15;  // V^T staging: 4 keys x 8 dims per thread
 
-  for (int k0 = 0; k0 < kend; k0 += kKeys) {
-    // Stage K [64][128] and V^T [128][64]; rows at or past T are zero.
-    uint4 kv[4], vv[4];
+  // Global loads of a block's K rows (4 chunks of 16 B per thread) and V rows
+  // (4 keys x 8 dims per thread); rows at or past T read as zero.
+  uint4 kv[4], vv[4];
+  auto fetch = [&](int kb) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int c = tid + 256 * i, r = c >> 4, ch = c & 15;
-      kv[i] = (k0 + r < a.T) ? *reinterpret_cast<const uint4*>(kbase + (int64_t)(k0 + r) * a.tok_stride + ch * 8)
+      kv[i] = (kb + r < a.T) ? *reinterpret_cast<const uint4*>(kbase + (int64_t)(kb + r) * a.tok_stride + ch * 8)
                              : make_uint4(0u, 0u, 0u, 0u);
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int r = 4 * kg + i;
-      vv[i] = (k0 + r < a.T) ? *reinterpret_cast<const uint4*>(vbase + (int64_t)(k0 + r) * a.tok_stride + dg * 8)
+      vv[i] = (kb + r < a.T) ? *reinterpret_cast<const uint4*>(vbase + (int64_t)(kb + r) * a.tok_stride + dg * 8)
                              : make_uint4(0u, 0u, 0u, 0u);
     }
+  };
+  fetch(0);
+
+  for (int k0 = 0; k0 < kend; k0 += kKeys) {
+    // Stage the fetched block: K [64][128] row-major, V^T [128][64].
     __syncthreads();  // the previous block's tiles are no longer read
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -117,6 +123,8 @@ __global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
       }
     }
     __syncthreads();
+    // The next block's global loads fly while this block is computed.
+    if (k0 + kKeys < kend) fetch(k0 + kKeys);
 
     // S^T = K Q^T for the block's 64 keys.
     f32x4 s[4];

@@ -6,10 +6,11 @@
 // The row arithmetic (and its fixed summation order) lives in qknorm_rope.h,
 // shared with the fused decode kernel.
 //
-// Mapping: one 16-lane group per (token, head) row of the fused qkv output;
-// lane j of the group holds dims [8j, 8j+8) as one 16-byte vector.  Rows are
-// the nh q heads, then nkv k heads (normed + roped, written to k_cache), then
-// nkv v heads (copied raw to v_cache).
+// Mapping: one block per token; its cos/sin are evaluated once into LDS; one
+// 16-lane group per (token, head) row of the fused qkv output, lane j holding
+// dims [8j, 8j+8) as one 16-byte vector.  Rows are the nh q heads, then nkv k
+// heads (normed + roped, written to k_cache), then nkv v heads (copied raw to
+// v_cache).
 #include "common.h"
 #include "capi_internal.h"
 #include "qknorm_rope.h"
@@ -22,31 +23,40 @@ __global__ __launch_bounds__(256) void qknorm_rope_kvwrite_kernel(
     const float* __restrict__ inv_freq, int64_t pos_limit, const int64_t* __restrict__ pos0_dev,
     uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int64_t tok_stride,
     int64_t head_stride) {
-  const int j = threadIdx.x & 15;
+  // Block = one token: its 128 cos/sin values are evaluated once (one per
+  // thread) into LDS, then the 16 slots of 16 lanes take its head rows.
+  __shared__ float s_cs[64], s_sn[64];
+  const int tid = threadIdx.x, j = tid & 15, slot = tid >> 4;
+  const int t = blockIdx.x;
   const int heads = nh + 2 * nkv;
-  const int64_t row = (int64_t)blockIdx.x * 16 + (threadIdx.x >> 4);
-  if (row >= (int64_t)T * heads) return;  // whole 16-lane groups retire together
-  const int t = (int)(row / heads);
-  const int hs = (int)(row % heads);
   const int64_t pos = (pos0_dev ? pos0_dev[0] : 0) + t;
   const bool pos_ok = pos >= 0 && pos < pos_limit;
-
-  const uint4 raw = *reinterpret_cast<const uint4*>(qkv + (int64_t)t * qkv_stride + hs * SOLORT_HD + j * 8);
-  if (hs >= nh + nkv) {  // V rows: raw copy (V is neither normed nor roped)
-    if (pos_ok)
-      *reinterpret_cast<uint4*>(vc + pos * tok_stride + (int64_t)(hs - nh - nkv) * head_stride + j * 8) = raw;
-    return;
+  if (tid < 128) {
+    const float ang = rope_angle(pos, inv_freq[tid >> 1]);
+    if (tid & 1) s_sn[tid >> 1] = rope_sin(ang);
+    else s_cs[tid >> 1] = rope_cos(ang);
   }
-  const uint16_t* w = (hs < nh) ? qn_w : kn_w;
-  float fr[8], c[8], s[8];
-  *reinterpret_cast<float4*>(fr) = *reinterpret_cast<const float4*>(inv_freq + (j & 7) * 8);
-  *reinterpret_cast<float4*>(fr + 4) = *reinterpret_cast<const float4*>(inv_freq + (j & 7) * 8 + 4);
-  rope_cs8(pos, fr, c, s);
-  const uint4 ov = qknorm_rope_row(raw, *reinterpret_cast<const uint4*>(w + j * 8), c, s, eps, j);
-  if (hs < nh) {
-    *reinterpret_cast<uint4*>(q_out + ((int64_t)t * nh + hs) * SOLORT_HD + j * 8) = ov;
-  } else if (pos_ok) {
-    *reinterpret_cast<uint4*>(kc + pos * tok_stride + (int64_t)(hs - nh) * head_stride + j * 8) = ov;
+  __syncthreads();
+  float c[8], s[8];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    c[i] = s_cs[(j & 7) * 8 + i];
+    s[i] = s_sn[(j & 7) * 8 + i];
+  }
+  for (int hs = slot; hs < heads; hs += 16) {  // whole 16-lane groups take a row
+    const uint4 raw = *reinterpret_cast<const uint4*>(qkv + (int64_t)t * qkv_stride + hs * SOLORT_HD + j * 8);
+    if (hs >= nh + nkv) {  // V rows: raw copy (V is neither normed nor roped)
+      if (pos_ok)
+        *reinterpret_cast<uint4*>(vc + pos * tok_stride + (int64_t)(hs - nh - nkv) * head_stride + j * 8) = raw;
+      continue;
+    }
+    const uint16_t* w = (hs < nh) ? qn_w : kn_w;
+    const uint4 ov = qknorm_rope_row(raw, *reinterpret_cast<const uint4*>(w + j * 8), c, s, eps, j);
+    if (hs < nh) {
+      *reinterpret_cast<uint4*>(q_out + ((int64_t)t * nh + hs) * SOLORT_HD + j * 8) = ov;
+    } else if (pos_ok) {
+      *reinterpret_cast<uint4*>(kc + pos * tok_stride + (int64_t)(hs - nh) * head_stride + j * 8) = ov;
+    }
   }
 }
 
@@ -73,10 +83,8 @@ extern "C" int solort_qknorm_rope_kvwrite(const void* qkv, int64_t qkv_row_strid
     return set_error(SOLORT_EINVAL, "qknorm_rope_kvwrite: KV strides must be positive multiples of 8");
   if (max_len <= 0) return set_error(SOLORT_EINVAL, "qknorm_rope_kvwrite: max_len must be positive");
   if (T == 0) return 0;
-  const int64_t rows = (int64_t)T * (nh + 2 * nkv);
-  const int64_t blocks = (rows + 15) / 16;
-  if (blocks > 0x7fffffff) return set_error(SOLORT_EINVAL, "qknorm_rope_kvwrite: too many rows");
-  hipLaunchKernelGGL(qknorm_rope_kvwrite_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+  if (T > 0x7fffffff) return set_error(SOLORT_EINVAL, "qknorm_rope_kvwrite: too many rows");
+  hipLaunchKernelGGL(qknorm_rope_kvwrite_kernel, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)qkv, qkv_row_stride, T, nh, nkv, (const uint16_t*)qn_w,
                      (const uint16_t*)kn_w, eps, inv_freq, max_len, pos0_dev, (uint16_t*)q_out,
                      (uint16_t*)k_cache, (uint16_t*)v_cache, kv_tok_stride, kv_head_stride);

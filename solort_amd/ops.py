@@ -119,7 +119,8 @@ def qknorm_rope_kvwrite(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tenso
 
 
 def attn_workspace(nq: int, nh: int, nkv: int, n_split: int, device: torch.device | str) -> torch.Tensor:
-    """Zero-filled workspace for decode_attn/verify_attn (allocate once, reuse)."""
+    """Workspace for decode_attn / verify_attn / decode_layer (the splits' partials; allocate once,
+    reuse for any call with no larger nq or n_split)."""
     nbytes = _lib.load().solort_attn_workspace_bytes(nq, nh, nkv, HD, n_split)
     _need(nbytes > 0, f"bad workspace request nq={nq} nh={nh} nkv={nkv} n_split={n_split}")
     return torch.zeros(nbytes, dtype=torch.uint8, device=device)
