@@ -1,7 +1,7 @@
 // Shared device helpers for the gfx950 attention kernels.
 //
 // bf16 is carried as raw uint16_t bits so that every rounding step is explicit
-// and matches torch's c10::BFloat16 (round-to-nearest-even, NaN -> 0x7FC0).
+// and matches torch's c10::BFloat16 (round-to-nearest-even).
 #pragma once
 #include <hip/hip_runtime.h>
 #include <stdint.h>
@@ -13,12 +13,19 @@ namespace solort {
 
 __device__ __forceinline__ float bf2f(uint32_t h) { return __uint_as_float(h << 16); }
 
-// float -> bf16 bits, round to nearest even; NaN becomes the canonical 0x7FC0.
-__device__ __forceinline__ uint32_t f2bf(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return 0x7fc0u;
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return u >> 16;
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+
+// float -> bf16 bits, round to nearest even, by gfx950's v_cvt_pk_bf16_f32.
+// For every non-NaN input this is bit-identical to torch's c10::BFloat16
+// rounding (checked over all 2^32 fp32 patterns, denormals and infinities
+// included); a NaN stays a NaN.
+__device__ __forceinline__ uint32_t f2bf(float f) { return __builtin_bit_cast(unsigned short, (__bf16)f); }
+
+// Two values, one instruction: bits of bf16(lo) | bf16(hi) << 16.
+__device__ __forceinline__ uint32_t pack2(float lo, float hi) {
+  const f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_t));
 }
 
 // bf16 round trip of an fp32 value (the per-op rounding torch applies to bf16 tensors).
@@ -34,11 +41,17 @@ __device__ __forceinline__ void unpack8(const uint4& v, float* x) {
 
 __device__ __forceinline__ uint4 pack8(const float* x) {
   uint4 v;
-  v.x = f2bf(x[0]) | (f2bf(x[1]) << 16);
-  v.y = f2bf(x[2]) | (f2bf(x[3]) << 16);
-  v.z = f2bf(x[4]) | (f2bf(x[5]) << 16);
-  v.w = f2bf(x[6]) | (f2bf(x[7]) << 16);
+  v.x = pack2(x[0], x[1]);
+  v.y = pack2(x[2], x[3]);
+  v.z = pack2(x[4], x[5]);
+  v.w = pack2(x[6], x[7]);
   return v;
+}
+
+// fp32 dot product of two bf16 pairs plus an accumulator (v_dot2c_f32_bf16);
+// the bf16 products are exact in fp32.
+__device__ __forceinline__ float dot2bf(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, a), __builtin_bit_cast(bf16x2_t, b), c, false);
 }
 
 // Lane exchange within a wavefront (64 lanes); xor masks < 64.
@@ -69,19 +82,38 @@ __device__ __forceinline__ float row16_sum(float v) {
 // The value held by lane i^8 of the same 16-lane row.
 __device__ __forceinline__ float row16_swap8(float v) { return dpp<0x128>(v); }
 
+// The value of lane i ^ 16 (i ^ 32) combined with this lane's by OP, using
+// gfx950's row-swap instructions: after swapping rows, each lane holds its own
+// value in one result and its partner's in the other.  (The elements are read
+// with __uint_as_float: __builtin_bit_cast of a vector element reads element 0.)
+template <typename OP>
+__device__ __forceinline__ float xor16_combine(float v, OP op) {
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return op(__uint_as_float(r0), __uint_as_float(r1));
+}
+template <typename OP>
+__device__ __forceinline__ float xor32_combine(float v, OP op) {
+  const uint32_t u = __float_as_uint(v);
+  const auto r = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  const uint32_t r0 = r[0], r1 = r[1];
+  return op(__uint_as_float(r0), __uint_as_float(r1));
+}
+
 // Maximum / sum over all 64 lanes of a wavefront, the same value in every lane.
 __device__ __forceinline__ float wave_max(float v) {
   v = fmaxf(v, dpp<0xB1>(v));
   v = fmaxf(v, dpp<0x4E>(v));
   v = fmaxf(v, dpp<0x141>(v));
   v = fmaxf(v, dpp<0x140>(v));
-  v = fmaxf(v, xshfl(v, 16));
-  return fmaxf(v, xshfl(v, 32));
+  v = xor16_combine(v, [](float x, float y) { return fmaxf(x, y); });
+  return xor32_combine(v, [](float x, float y) { return fmaxf(x, y); });
 }
 __device__ __forceinline__ float wave_sum(float v) {
   v = row16_sum(v);
-  v = v + xshfl(v, 16);
-  return v + xshfl(v, 32);
+  v = xor16_combine(v, [](float x, float y) { return x + y; });
+  return xor32_combine(v, [](float x, float y) { return x + y; });
 }
 
 // RoPE angle, cos and sin of the reference's _cos_sin
@@ -104,9 +136,14 @@ __device__ __forceinline__ void rope_cs8(int64_t pos, const float* inv_freq8, fl
   }
 }
 
-// Device-scope (agent) fences used by the last-workgroup-combines pattern.
-__device__ __forceinline__ void fence_release_agent() { __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent"); }
-__device__ __forceinline__ void fence_acquire_agent() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+// Workgroup barrier that orders LDS accesses only.  __syncthreads() also waits
+// for every global load the wave has in flight, which would stall a kernel
+// that issues its HBM loads early and synchronises on LDS before using them.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 

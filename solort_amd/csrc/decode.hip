@@ -110,11 +110,11 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   constexpr int R = NQ * G;            // query rows sharing one KV head
   constexpr int KPI = 16 * U;          // keys per iteration (16 slots x U)
   constexpr int RPW = (R + 3) / 4;     // output rows per wavefront
-  __shared__ __align__(16) float s_q[R * 128];
+  __shared__ __align__(16) uint4 s_q[R * 16];         // q rows, bf16 bits [row][16 x 16 B]
   __shared__ uint4 s_new[FUSED ? 2 * NQ * 16 : 1];   // fresh K rows then V rows (bf16 bits)
   __shared__ float s_rope[FUSED ? 2 * NQ * 64 : 1];  // cos [t][64] then sin [t][64]
   __shared__ __align__(16) uint4 s_v[KPI * 16];      // the iteration's V rows [key][16 x 16 B]
-  __shared__ float s_s[KPI * R];                     // its masked scores [key][row], log2 units
+  __shared__ __align__(16) float s_s[R * KPI];       // its masked scores [row][key] (log2 units), then p
 
   const int tid = threadIdx.x, j = tid & 15, slot = tid >> 4, wave = tid >> 6, lane = tid & 63;
   const int kvh = blockIdx.x % a.nkv;
@@ -125,40 +125,42 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   const int kbeg = min(split * chunk, a.bound);
   const int kstat = min(kbeg + chunk, a.bound);
 
-  // 1. Loads for this slot's first prologue row (and this thread's RoPE
-  //    frequency), issued before the K/V loads: vector loads complete in
-  //    issue order, so the prologue then waits for its own rows only.
+  // 1. Loads for this slot's first prologue row, issued before the K/V loads:
+  //    vector loads complete in issue order, so the prologue then waits for
+  //    its own rows only.  Every load of phases 1 and 2 is unconditional
+  //    (idle lanes load a valid row they ignore): a load skipped on some path
+  //    would make the compiler wait for all of them before the first use.
   constexpr int NROWS = FUSED ? NQ * (G + 2) : R;
-  constexpr int NROPE = FUSED ? 2 * NQ * 64 : 0;  // (token, frequency, cos|sin) values
-  uint4 raw0 = make_uint4(0u, 0u, 0u, 0u), w0 = raw0;
-  float fr0 = 0.f;
-  if (slot < NROWS) {
+  constexpr int NROPE = FUSED ? 2 * NQ * 64 : 0;  // (token, cos|sin, frequency) values
+  uint4 raw0, wq0 = make_uint4(0u, 0u, 0u, 0u), wk0 = wq0;
+  {
+    const int row = min(slot, NROWS - 1);
     if constexpr (FUSED) {
-      const int t = slot / (G + 2), c = slot % (G + 2);
+      const int t = row / (G + 2), c = row % (G + 2);
       const int hs = c < G ? kvh * G + c : (c == G ? a.nh + kvh : a.nh + a.nkv + kvh);
       raw0 = *reinterpret_cast<const uint4*>(a.qkv + (int64_t)t * a.qkv_stride + hs * SOLORT_HD + j * 8);
-      if (c <= G) w0 = *reinterpret_cast<const uint4*>((c < G ? a.qn_w : a.kn_w) + j * 8);
+      wq0 = *reinterpret_cast<const uint4*>(a.qn_w + j * 8);
+      wk0 = *reinterpret_cast<const uint4*>(a.kn_w + j * 8);
     } else {
-      const int t = slot / G, g = slot % G;
+      const int t = row / G, g = row % G;
       raw0 = *reinterpret_cast<const uint4*>(a.q + ((int64_t)t * a.nh + kvh * G + g) * SOLORT_HD + j * 8);
     }
   }
-  if (FUSED && tid < NROPE) fr0 = a.inv_freq[(tid >> 1) & 63];
+  const float fr = FUSED ? a.inv_freq[lane] : 0.f;  // RoPE frequency `lane`
+  __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the K/V loads
 
-  // 2. First K/V loads: static addresses, independent of the position.
+  // 2. First K/V loads: static addresses, independent of the position.  Rows
+  //    past this split's chunk re-read its last row (an empty chunk: row 0)
+  //    and are masked below.
   const uint16_t* kp = a.kc + (int64_t)kvh * a.head_stride + j * 8;
   const uint16_t* vp = a.vc + (int64_t)kvh * a.head_stride + j * 8;
+  const int kclamp = kstat > kbeg ? kstat - 1 : 0;
   uint4 kr[U], vr[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
-    const int kid = kbeg + u * 16 + slot;
-    if (kid < kstat) {
-      kr[u] = *reinterpret_cast<const uint4*>(kp + (int64_t)kid * a.tok_stride);
-      vr[u] = *reinterpret_cast<const uint4*>(vp + (int64_t)kid * a.tok_stride);
-    } else {
-      kr[u] = make_uint4(0u, 0u, 0u, 0u);
-      vr[u] = make_uint4(0u, 0u, 0u, 0u);
-    }
+    const int kid = min(kbeg + u * 16 + slot, kclamp);
+    kr[u] = *reinterpret_cast<const uint4*>(kp + (int64_t)kid * a.tok_stride);
+    vr[u] = *reinterpret_cast<const uint4*>(vp + (int64_t)kid * a.tok_stride);
   }
 
   const int64_t pos0 = a.pos0_dev[0];
@@ -166,17 +168,21 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   // 3. q rows (and, fused, the new tokens' K/V rows) into LDS.  Fused: every
   //    thread first evaluates one (or a few) of the RoPE cos/sin values.
   if constexpr (FUSED) {
-    for (int e = tid; e < NROPE; e += 256) {
-      const int t = e >> 7, f = (e >> 1) & 63;
-      const float ang = rope_angle(pos0 + t, e == tid ? fr0 : a.inv_freq[f]);
-      s_rope[(e & 1) * NQ * 64 + t * 64 + f] = (e & 1) ? rope_sin(ang) : rope_cos(ang);
+    // e = (token, cos|sin, frequency = lane); every thread evaluates, so the
+    // frequency load stays where it was issued.
+    for (int e = tid; e < max(NROPE, 256); e += 256) {
+      const int t = e >> 7, sn = (e >> 6) & 1;
+      const float ang = rope_angle(pos0 + t, fr);
+      const float v = sn ? rope_sin(ang) : rope_cos(ang);
+      if (e < NROPE) s_rope[sn * NQ * 64 + t * 64 + lane] = v;
     }
-    __syncthreads();
+    lds_barrier();
   }
   for (int row = slot; row < NROWS; row += 16) {
-    uint4 raw = raw0, w8 = w0;
+    uint4 raw = raw0, w8;
     if constexpr (FUSED) {
       const int t = row / (G + 2), c = row % (G + 2);
+      w8 = c < G ? wq0 : wk0;
       const int64_t pos = pos0 + t;
       const bool pos_ok = pos >= 0 && pos < a.pos_limit;
       if (row != slot) {  // rows past the first (verify): loaded here
@@ -198,10 +204,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
       }
       const uint4 ov = qknorm_rope_row(raw, w8, cs, sn, a.eps, j);
       if (c < G) {
-        float y[8];
-        unpack8(ov, y);
-#pragma unroll
-        for (int i = 0; i < 8; ++i) s_q[(t * G + c) * 128 + j * 8 + i] = y[i] * a.qscale;
+        s_q[(t * G + c) * 16 + j] = ov;
       } else {
         s_new[t * 16 + j] = ov;
         if (split == 0 && pos_ok)
@@ -211,46 +214,40 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
       const int t = row / G, g = row % G;
       if (row != slot)
         raw = *reinterpret_cast<const uint4*>(a.q + ((int64_t)t * a.nh + kvh * G + g) * SOLORT_HD + j * 8);
-      float x[8];
-      unpack8(raw, x);
-#pragma unroll
-      for (int i = 0; i < 8; ++i) s_q[row * 128 + j * 8 + i] = x[i] * a.qscale;
+      s_q[row * 16 + j] = raw;
     }
   }
-  __syncthreads();
-  float qf[R][8];
+  lds_barrier();
+  uint4 qb[R];  // this lane's 8 dims of every q row, bf16 pairs
 #pragma unroll
-  for (int r = 0; r < R; ++r)
-#pragma unroll
-    for (int i = 0; i < 8; ++i) qf[r][i] = s_q[r * 128 + j * 8 + i];
+  for (int r = 0; r < R; ++r) qb[r] = s_q[r * 16 + j];
 
-  // 4. Per iteration: the 16 slots score U keys each (16-lane dot products
-  //    reduced with DPP) and stage the scores and V rows in LDS; then every
-  //    thread runs the online softmax for the output it owns - rows
-  //    wave + 4i, dims 2*lane and 2*lane+1 - so no per-slot state is merged.
+  // 4. Per iteration: the 16 slots score U keys each (bf16 pair dot products
+  //    over the slot's 16 lanes, reduced with DPP) and stage the scores and V
+  //    rows in LDS.  Then each wavefront takes the rows it owns (wave + 4i):
+  //    lane k evaluates p for key k, the wavefront's p go through its own LDS
+  //    row, and each lane accumulates dims 2*lane, 2*lane+1 of the output, so
+  //    no per-slot state is merged.
   int64_t live64 = pos0 + NQ;
   live64 = live64 < 0 ? 0 : (live64 > a.bound ? a.bound : live64);
   const int kend = min(kstat, (int)live64);
-  float M[RPW], L[RPW], O[RPW][2];
+  float M[RPW], Lk[RPW], O[RPW][2];  // Lk: this lane's share of the sum (its keys)
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
     M[i] = -INFINITY;
-    L[i] = 0.f;
+    Lk[i] = 0.f;
     O[i][0] = O[i][1] = 0.f;
   }
   const uint32_t* s_v32 = reinterpret_cast<const uint32_t*>(s_v);
   for (int k0 = kbeg; k0 < kend; k0 += KPI) {
-    uint4 kn[U], vn[U];
     const int k1 = k0 + KPI;
+    uint4 kn[U], vn[U];
+    if (k1 < kend) {  // prefetch the next iteration of a long split (block-uniform)
 #pragma unroll
-    for (int u = 0; u < U; ++u) {  // prefetch the next iteration of a long split
-      const int kid = k1 + u * 16 + slot;
-      if (kid < kend) {
+      for (int u = 0; u < U; ++u) {
+        const int kid = min(k1 + u * 16 + slot, kend - 1);
         kn[u] = *reinterpret_cast<const uint4*>(kp + (int64_t)kid * a.tok_stride);
         vn[u] = *reinterpret_cast<const uint4*>(vp + (int64_t)kid * a.tok_stride);
-      } else {
-        kn[u] = make_uint4(0u, 0u, 0u, 0u);
-        vn[u] = make_uint4(0u, 0u, 0u, 0u);
       }
     }
 #pragma unroll
@@ -263,53 +260,74 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
           vr[u] = s_new[(NQ + off) * 16 + j];
         }
       }
-      float kf[8];
-      unpack8(kr[u], kf);
       const bool in = kid < kend;
+      if (!in) vr[u] = make_uint4(0u, 0u, 0u, 0u);  // p = 0 must not meet a non-finite value
 #pragma unroll
       for (int r = 0; r < R; ++r) {
-        float d = qf[r][0] * kf[0];
-#pragma unroll
-        for (int i = 1; i < 8; ++i) d = fmaf(qf[r][i], kf[i], d);
-        d = row16_sum(d);
+        float d = dot2bf(kr[u].x, qb[r].x, 0.f);
+        d = dot2bf(kr[u].y, qb[r].y, d);
+        d = dot2bf(kr[u].z, qb[r].z, d);
+        d = dot2bf(kr[u].w, qb[r].w, d);
+        d = row16_sum(d) * a.qscale;
         const int t = r / G;
         if (!in || (int64_t)kid > pos0 + t) d = -INFINITY;
-        if (j == 0) s_s[(u * 16 + slot) * R + r] = d;
+        if (j == 0) s_s[r * KPI + u * 16 + slot] = d;
       }
       s_v[(u * 16 + slot) * 16 + j] = vr[u];
     }
-    __syncthreads();
+    lds_barrier();
+    // Dims 2*lane, 2*lane+1 of every key of the iteration, held in registers
+    // when the wave owns one row (re-read from LDS per row otherwise).
+    constexpr bool kHoistV = RPW == 1;
+    uint32_t v2[kHoistV ? KPI : 1];
+    if constexpr (kHoistV) {
+#pragma unroll
+      for (int k = 0; k < KPI; ++k) v2[k] = s_v32[k * 64 + lane];
+    }
 #pragma unroll
     for (int i = 0; i < RPW; ++i) {
       const int r = wave + 4 * i;
-      if (r < R) {
-        float mx = -INFINITY;
+      if (r < R) {  // wave-uniform
+        float* srow = s_s + r * KPI;
+        float sk = -INFINITY;
 #pragma unroll
-        for (int k = 0; k < KPI; ++k) mx = fmaxf(mx, s_s[k * R + r]);
-        const float mn = fmaxf(M[i], mx);
-        if (mn != -INFINITY) {
-          const float alpha = fast_exp2(M[i] - mn);  // M = -inf gives 0
-          float l = L[i] * alpha, o0 = O[i][0] * alpha, o1 = O[i][1] * alpha;
+        for (int h = 0; h < KPI; h += 64)
+          if (h + lane < KPI) sk = srow[h + lane];  // KPI <= 64: one key per lane
+        const float mx = fmaxf(M[i], wave_max(sk));
+        if (mx != -INFINITY) {  // wave-uniform
+          const float alpha = fast_exp2(M[i] - mx);  // M = -inf gives 0
+          const float pk = fast_exp2(sk - mx);       // masked or idle lane: 0
+          Lk[i] = Lk[i] * alpha + pk;
+          if (lane < KPI) srow[lane] = pk;
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+          const float4* p4 = reinterpret_cast<const float4*>(srow);
+          float o0 = O[i][0] * alpha, o1 = O[i][1] * alpha;
 #pragma unroll
-          for (int k = 0; k < KPI; ++k) {
-            const float p = fast_exp2(s_s[k * R + r] - mn);  // masked: 0
-            const uint32_t v2 = s_v32[k * 64 + lane];
-            l += p;
-            o0 = fmaf(p, __uint_as_float(v2 << 16), o0);
-            o1 = fmaf(p, __uint_as_float(v2 & 0xffff0000u), o1);
+          for (int k4 = 0; k4 < KPI / 4; ++k4) {
+            const float4 p = p4[k4];
+            const float pp[4] = {p.x, p.y, p.z, p.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              const int k = 4 * k4 + e;
+              const uint32_t vk = kHoistV ? v2[kHoistV ? k : 0] : s_v32[k * 64 + lane];
+              o0 = fmaf(pp[e], __uint_as_float(vk << 16), o0);
+              o1 = fmaf(pp[e], __uint_as_float(vk & 0xffff0000u), o1);
+            }
           }
-          L[i] = l;
           O[i][0] = o0;
           O[i][1] = o1;
-          M[i] = mn;
+          M[i] = mx;
         }
       }
     }
-    __syncthreads();  // s_s and s_v are rewritten by the next iteration
+    lds_barrier();  // s_s and s_v are rewritten by the next iteration
+    if (k1 < kend) {
 #pragma unroll
-    for (int u = 0; u < U; ++u) {
-      kr[u] = kn[u];
-      vr[u] = vn[u];
+      for (int u = 0; u < U; ++u) {
+        kr[u] = kn[u];
+        vr[u] = vn[u];
+      }
     }
   }
 
@@ -319,13 +337,14 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   for (int i = 0; i < RPW; ++i) {
     const int r = wave + 4 * i;
     if (r >= R) continue;
+    const float Ls = wave_sum(Lk[i]);
     if (NS == 1) {
-      const float inv = L[i] > 0.f ? 1.f / L[i] : 0.f;
+      const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
       store_out2(a.out, a.out_f32, a.nh, kvh, G, r, 2 * lane, O[i][0] * inv, O[i][1] * inv);
     } else {
       const int64_t pr = (int64_t)(kvh * NS + split) * R + r;
       *reinterpret_cast<float2*>(a.ws_o + pr * 128 + 2 * lane) = make_float2(O[i][0], O[i][1]);
-      if (lane == 0) *reinterpret_cast<float2*>(a.ws_ml + pr * 2) = make_float2(M[i], L[i]);
+      if (lane == 0) *reinterpret_cast<float2*>(a.ws_ml + pr * 2) = make_float2(M[i], Ls);
     }
   }
 }
