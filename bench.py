@@ -175,10 +175,11 @@ def time_decode_kernel(torch, ops, runners, bound, ns, sh, dev, reps=3, pos=None
     ws = ops.attn_workspace(1, sh.nh, sh.nkv, ns, dev)
     out = torch.empty(1, sh.nh * 128, dtype=torch.bfloat16, device=dev)
     order = [(r, li) for r in runners for li in range(sh.layers)]
+    cs = {id(r): ops.rope_rows(r.inv_freq, r.pos_buf if pos is None else pos, 1) for r in runners}
 
     def run_all():
         for r, li in order:
-            ops.decode_layer(r.qkv_dec[li], r.qn_w[li], r.kn_w[li], r.eps, r.inv_freq,
+            ops.decode_layer(r.qkv_dec[li], r.qn_w[li], r.kn_w[li], r.eps, cs[id(r)],
                              r.pos_buf if pos is None else pos, r.kc[li], r.vc[li], bound, sh.scale, ws, ns, out,
                              sh.nh, sh.nkv)
 

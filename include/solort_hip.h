@@ -85,6 +85,17 @@ int solort_qknorm_rope_kvwrite(const void* qkv, int64_t qkv_row_stride, int T, i
 int solort_rope_table(const float* inv_freq, int half_dim, int64_t rows, void* cos_out, void* sin_out,
                       solort_stream_t stream);
 
+/*
+ * cos/sin rows of the positions of one decode or verify step, computed once
+ * per step and read by every layer's solort_decode_layer, as the reference
+ * computes cos, sin = _cos_sin(pos) once per step (cuda_graph_executor.py:164,
+ * :248) and every layer applies them.
+ * cs_out [2, n, half_dim] bf16: cos rows of positions *pos0_dev + t
+ *        (t < n), then the sin rows; values as in solort_rope_table.
+ */
+int solort_rope_rows(const float* inv_freq, int half_dim, const int64_t* pos0_dev, int n, void* cs_out,
+                     solort_stream_t stream);
+
 /* Workspace bytes needed by solort_decode_attn / solort_verify_attn /
  * solort_decode_layer for `nq` query tokens and `n_split` key splits: the
  * splits' partial results (per KV head and split: running max and sum, and
@@ -137,12 +148,14 @@ int solort_verify_attn(const void* q, int nq, int nh, int nkv, int hd, const voi
  * cuda_graph_executor.py:173-184 (decode, nq = 1) and :254-263 (verify,
  * nq = K+1); results equal solort_qknorm_rope_kvwrite followed by
  * solort_decode_attn on the same inputs (the KV rows bit for bit).
- * Arguments as in those two functions; the workspace is sized by
+ * rope_cs  [2, nq, 64] bf16 from solort_rope_rows(inv_freq, 64, pos0_dev, nq)
+ *          of this step (16-byte aligned).
+ * Other arguments as in those two functions; the workspace is sized by
  * solort_attn_workspace_bytes(nq, nh, nkv, hd, n_split).  q is not
  * materialised.
  */
 int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int nq, int nh, int nkv, int hd,
-                        const void* qn_w, const void* kn_w, float eps, const float* inv_freq,
+                        const void* qn_w, const void* kn_w, float eps, const void* rope_cs,
                         const int64_t* pos0_dev, void* k_cache, void* v_cache, int64_t kv_tok_stride,
                         int64_t kv_head_stride, int64_t max_len, int bound, float scale, void* ws,
                         int n_split, void* out, int out_dtype, solort_stream_t stream);

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before ours)
 
 LIB_PATH = Path(__file__).resolve().parent / "libsolort_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 # name -> (restype, argtypes); mirrors include/solort_hip.h
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -27,6 +27,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p],
     ),
     "solort_rope_table": (c_int, [c_void_p, c_int, c_int64, c_void_p, c_void_p, c_void_p]),
+    "solort_rope_rows": (c_int, [c_void_p, c_int, c_void_p, c_int, c_void_p, c_void_p]),
     "solort_attn_workspace_bytes": (c_size_t, [c_int, c_int, c_int, c_int, c_int]),
     "solort_decode_attn": (
         c_int,

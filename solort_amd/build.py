@@ -28,6 +28,9 @@ HIPCC_FLAGS = [
     "-Wno-unused-function",
     # Packed fp32 instructions are disabled for all device code.
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # Leading scalar/pointer kernel arguments arrive preloaded in SGPRs, so a
+    # kernel's first loads do not wait for the kernel-argument fetch.
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

@@ -82,6 +82,32 @@ __device__ __forceinline__ float row16_sum(float v) {
 // The value held by lane i^8 of the same 16-lane row.
 __device__ __forceinline__ float row16_swap8(float v) { return dpp<0x128>(v); }
 
+// Reduce-scatter over a 16-lane row: each of v[0..7] is summed over the row's
+// 16 lanes, and lane j returns the total of value j >> 1 (lanes j and j ^ 1
+// hold the same one).  Each step pairs lanes that differ in one more bit
+// (bit 3 via row_ror:8, bit 2 via half mirror, bit 1, then bit 0); the lane
+// with that bit set keeps the upper half of its list, its partner the lower
+// half, and each adds the half the other hands over.  22 VALU operations
+// instead of 32 for eight separate row sums, and the eight totals end in
+// different lanes.
+__device__ __forceinline__ float row16_reduce8(const float (&v)[8], int j) {
+  const bool h3 = j & 8, h2 = j & 4, h1 = j & 2;
+  float a[4], b[2];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const float keep = h3 ? v[i + 4] : v[i], give = h3 ? v[i] : v[i + 4];
+    a[i] = keep + dpp<0x128>(give);
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const float keep = h2 ? a[i + 2] : a[i], give = h2 ? a[i] : a[i + 2];
+    b[i] = keep + dpp<0x141>(give);
+  }
+  const float keep = h1 ? b[1] : b[0], give = h1 ? b[0] : b[1];
+  const float c = keep + dpp<0x4E>(give);
+  return c + dpp<0xB1>(c);
+}
+
 // The value of lane i ^ 16 (i ^ 32) combined with this lane's by OP, using
 // gfx950's row-swap instructions: after swapping rows, each lane holds its own
 // value in one result and its partner's in the other.  (The elements are read

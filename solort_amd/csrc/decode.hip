@@ -19,20 +19,22 @@
 // before the device-side position has arrived; keys past the live length are
 // masked, and later iterations of a long split stop at the live length.
 //   - 16 row slots of 16 lanes each take U key rows per iteration; lane j of a
-//     slot loads dims [8j, 8j+8) of K and V as 16-byte vectors; q for the whole
-//     query group (nq * g rows) sits in registers, so each KV head is read once
-//     for all of its query heads (no repeat_interleave).  Dot products are
-//     reduced across the 16 lanes with DPP.
-//   - Scores and V rows of the iteration go to LDS; each thread then runs the
-//     online softmax for the output it owns (rows wave + 4i, two dims), so no
-//     per-slot state has to be merged.
-//   - Fused variant: while the K/V loads are in flight, every thread evaluates
-//     one RoPE cos/sin value into LDS and slots compute the q rows and the new
-//     tokens' K/V rows from the fused qkv projection (qknorm_rope.h, bit
-//     identical to the standalone prologue).  Split 0 of each KV head writes
-//     the new rows to the cache; every block substitutes the fresh rows for
-//     the cache rows pos0..pos0+nq-1 it loaded, so no block waits for that
-//     write.
+//     slot loads dims [8j, 8j+8) of K and V as 16-byte vectors.  The query
+//     group (nq * g rows) sits in registers as bf16 pairs, so each KV head is
+//     read once for all of its query heads (no repeat_interleave); a score is
+//     four bf16 pair dot products per lane, reduced over the slot with DPP.
+//   - Scores and V rows of the iteration go to LDS.  Each wavefront then takes
+//     the rows it owns: lane k evaluates p for key k, the p values go through
+//     the wavefront's own LDS row, and every lane accumulates two output dims,
+//     so no per-slot state is merged.
+//   - Fused variant: while the K/V loads are in flight, slots compute the q
+//     rows and the new tokens' K/V rows from the fused qkv projection and the
+//     step's cos/sin rows (qknorm_rope.h, bit identical to the standalone
+//     prologue).  Split 0 of each KV head writes the new rows to the cache;
+//     every block substitutes the fresh rows for the cache rows
+//     pos0..pos0+nq-1 it loaded, so no block waits for that write.
+//   - Barriers order LDS only (lds_barrier): the K/V loads stay in flight
+//     across them.
 //   - Output: with one split the block writes the answer; otherwise its
 //     partial (running max in log2 units, sum, unnormalised output).
 // Combine kernel: merges the partials of each KV head (log-sum-exp); the
@@ -47,28 +49,21 @@
 
 namespace solort {
 
-struct DecodeArgs {
-  // fused prologue inputs
-  const uint16_t* qkv;
-  int64_t qkv_stride;
-  const uint16_t* qn_w;
+// The kernel's leading arguments are the ones its first loads need; the
+// compiler preloads the leading kernel arguments into SGPRs (14 dwords, see
+// -amdgpu-kernarg-preload-count in the build), so those loads issue without
+// waiting for the kernel-argument fetch.  The rest travel in DecodeTail.
+struct DecodeTail {
   const uint16_t* kn_w;
-  const float* inv_freq;  // [64] RoPE frequencies
-  int64_t pos_limit;      // positions >= pos_limit are not written
-  float eps;
-  // unfused: q rows [nq][nh][128]
-  const uint16_t* q;
-  // cache and attention
-  uint16_t* kc;
-  uint16_t* vc;
-  int64_t tok_stride;
-  int64_t head_stride;
+  const uint16_t* rope_cs;  // [2][nq][64] bf16: cos rows, then sin rows, of this step
   const int64_t* pos0_dev;
   float* ws_o;   // [nkv][n_split][R][128]
   float* ws_ml;  // [nkv][n_split][R][2]: running max (log2 units), sum
   void* out;     // [nq][nh][128]
-  float qscale;      // softmax scale * log2(e)
-  int nh, nkv, bound, n_split, out_f32;
+  float qscale;  // softmax scale * log2(e)
+  float eps;
+  int pos_limit;  // positions >= pos_limit are not written
+  int out_f32;
 };
 
 __device__ __forceinline__ float4 f4fma(float w, const float4 v, float4 acc) {
@@ -105,115 +100,101 @@ __device__ __forceinline__ void store_out2(void* out, int out_f32, int nh, int k
     *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(out) + oi) = f2bf(o0) | (f2bf(o1) << 16);
 }
 
+// Grid (nkv, n_split): block (kvh, split).  qsrc: fused, the qkv rows (row
+// stride qsrc_stride); unfused, the q rows [nq][nh][128] (qsrc_stride = nh*128).
 template <int NQ, int G, int U, bool FUSED>
-__global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
+__global__ __launch_bounds__(256) void decode_kernel(uint16_t* kc, uint16_t* vc, int tok_stride, int head_stride,
+                                                     int chunk, int bound, const uint16_t* qsrc, int qsrc_stride,
+                                                     int nh, const uint16_t* qn_w, const DecodeTail a) {
   constexpr int R = NQ * G;            // query rows sharing one KV head
   constexpr int KPI = 16 * U;          // keys per iteration (16 slots x U)
   constexpr int RPW = (R + 3) / 4;     // output rows per wavefront
   __shared__ __align__(16) uint4 s_q[R * 16];         // q rows, bf16 bits [row][16 x 16 B]
   __shared__ uint4 s_new[FUSED ? 2 * NQ * 16 : 1];   // fresh K rows then V rows (bf16 bits)
-  __shared__ float s_rope[FUSED ? 2 * NQ * 64 : 1];  // cos [t][64] then sin [t][64]
   __shared__ __align__(16) uint4 s_v[KPI * 16];      // the iteration's V rows [key][16 x 16 B]
   __shared__ __align__(16) float s_s[R * KPI];       // its masked scores [row][key] (log2 units), then p
 
   const int tid = threadIdx.x, j = tid & 15, slot = tid >> 4, wave = tid >> 6, lane = tid & 63;
-  const int kvh = blockIdx.x % a.nkv;
-  const int split = blockIdx.x / a.nkv;
-  const int NS = a.n_split;
-  int chunk = (a.bound + NS - 1) / NS;
-  chunk = (chunk + 15) & ~15;
-  const int kbeg = min(split * chunk, a.bound);
-  const int kstat = min(kbeg + chunk, a.bound);
+  const int kvh = blockIdx.x, split = blockIdx.y, nkv = gridDim.x, NS = gridDim.y;
+  const int kbeg = min(split * chunk, bound);
+  const int kstat = min(kbeg + chunk, bound);
 
-  // 1. Loads for this slot's first prologue row, issued before the K/V loads:
-  //    vector loads complete in issue order, so the prologue then waits for
-  //    its own rows only.  Every load of phases 1 and 2 is unconditional
-  //    (idle lanes load a valid row they ignore): a load skipped on some path
-  //    would make the compiler wait for all of them before the first use.
+  // 1. Loads for this slot's first prologue row (fused: with its norm
+  //    weights and its token's cos/sin), issued before the K/V loads: vector
+  //    loads complete in issue order, so the prologue then waits for its own
+  //    rows only.  Every load of phases 1 and 2 is unconditional (idle lanes
+  //    load a valid row they ignore): a load skipped on some path would make
+  //    the compiler wait for all of them before the first use.
   constexpr int NROWS = FUSED ? NQ * (G + 2) : R;
-  constexpr int NROPE = FUSED ? 2 * NQ * 64 : 0;  // (token, cos|sin, frequency) values
-  uint4 raw0, wq0 = make_uint4(0u, 0u, 0u, 0u), wk0 = wq0;
+  uint4 raw0, wq0 = make_uint4(0u, 0u, 0u, 0u), wk0 = wq0, c0 = wq0, s0 = wq0;
   {
     const int row = min(slot, NROWS - 1);
     if constexpr (FUSED) {
       const int t = row / (G + 2), c = row % (G + 2);
-      const int hs = c < G ? kvh * G + c : (c == G ? a.nh + kvh : a.nh + a.nkv + kvh);
-      raw0 = *reinterpret_cast<const uint4*>(a.qkv + (int64_t)t * a.qkv_stride + hs * SOLORT_HD + j * 8);
-      wq0 = *reinterpret_cast<const uint4*>(a.qn_w + j * 8);
+      const int hs = c < G ? kvh * G + c : (c == G ? nh + kvh : nh + nkv + kvh);
+      raw0 = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + hs * SOLORT_HD + j * 8);
+      wq0 = *reinterpret_cast<const uint4*>(qn_w + j * 8);
       wk0 = *reinterpret_cast<const uint4*>(a.kn_w + j * 8);
+      c0 = *reinterpret_cast<const uint4*>(a.rope_cs + t * 64 + (j & 7) * 8);
+      s0 = *reinterpret_cast<const uint4*>(a.rope_cs + (NQ + t) * 64 + (j & 7) * 8);
     } else {
       const int t = row / G, g = row % G;
-      raw0 = *reinterpret_cast<const uint4*>(a.q + ((int64_t)t * a.nh + kvh * G + g) * SOLORT_HD + j * 8);
+      raw0 = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + (kvh * G + g) * SOLORT_HD + j * 8);
     }
   }
-  const float fr = FUSED ? a.inv_freq[lane] : 0.f;  // RoPE frequency `lane`
   __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the K/V loads
 
   // 2. First K/V loads: static addresses, independent of the position.  Rows
   //    past this split's chunk re-read its last row (an empty chunk: row 0)
   //    and are masked below.
-  const uint16_t* kp = a.kc + (int64_t)kvh * a.head_stride + j * 8;
-  const uint16_t* vp = a.vc + (int64_t)kvh * a.head_stride + j * 8;
+  const uint16_t* kp = kc + (int64_t)kvh * head_stride + j * 8;
+  const uint16_t* vp = vc + (int64_t)kvh * head_stride + j * 8;
   const int kclamp = kstat > kbeg ? kstat - 1 : 0;
   uint4 kr[U], vr[U];
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int kid = min(kbeg + u * 16 + slot, kclamp);
-    kr[u] = *reinterpret_cast<const uint4*>(kp + (int64_t)kid * a.tok_stride);
-    vr[u] = *reinterpret_cast<const uint4*>(vp + (int64_t)kid * a.tok_stride);
+    kr[u] = *reinterpret_cast<const uint4*>(kp + (int64_t)kid * tok_stride);
+    vr[u] = *reinterpret_cast<const uint4*>(vp + (int64_t)kid * tok_stride);
   }
 
   const int64_t pos0 = a.pos0_dev[0];
 
-  // 3. q rows (and, fused, the new tokens' K/V rows) into LDS.  Fused: every
-  //    thread first evaluates one (or a few) of the RoPE cos/sin values.
-  if constexpr (FUSED) {
-    // e = (token, cos|sin, frequency = lane); every thread evaluates, so the
-    // frequency load stays where it was issued.
-    for (int e = tid; e < max(NROPE, 256); e += 256) {
-      const int t = e >> 7, sn = (e >> 6) & 1;
-      const float ang = rope_angle(pos0 + t, fr);
-      const float v = sn ? rope_sin(ang) : rope_cos(ang);
-      if (e < NROPE) s_rope[sn * NQ * 64 + t * 64 + lane] = v;
-    }
-    lds_barrier();
-  }
+  // 3. q rows (and, fused, the new tokens' K/V rows) into LDS.
   for (int row = slot; row < NROWS; row += 16) {
-    uint4 raw = raw0, w8;
+    uint4 raw = raw0, w8, c8 = c0, s8 = s0;
     if constexpr (FUSED) {
       const int t = row / (G + 2), c = row % (G + 2);
       w8 = c < G ? wq0 : wk0;
       const int64_t pos = pos0 + t;
       const bool pos_ok = pos >= 0 && pos < a.pos_limit;
       if (row != slot) {  // rows past the first (verify): loaded here
-        const int hs = c < G ? kvh * G + c : (c == G ? a.nh + kvh : a.nh + a.nkv + kvh);
-        raw = *reinterpret_cast<const uint4*>(a.qkv + (int64_t)t * a.qkv_stride + hs * SOLORT_HD + j * 8);
-        if (c <= G) w8 = *reinterpret_cast<const uint4*>((c < G ? a.qn_w : a.kn_w) + j * 8);
+        const int hs = c < G ? kvh * G + c : (c == G ? nh + kvh : nh + nkv + kvh);
+        raw = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + hs * SOLORT_HD + j * 8);
+        c8 = *reinterpret_cast<const uint4*>(a.rope_cs + t * 64 + (j & 7) * 8);
+        s8 = *reinterpret_cast<const uint4*>(a.rope_cs + (NQ + t) * 64 + (j & 7) * 8);
       }
       if (c == G + 1) {  // V row: raw
         s_new[(NQ + t) * 16 + j] = raw;
         if (split == 0 && pos_ok)
-          *reinterpret_cast<uint4*>(a.vc + pos * a.tok_stride + (int64_t)kvh * a.head_stride + j * 8) = raw;
+          *reinterpret_cast<uint4*>(vc + pos * tok_stride + (int64_t)kvh * head_stride + j * 8) = raw;
         continue;
       }
       float cs[8], sn[8];
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        cs[i] = s_rope[t * 64 + (j & 7) * 8 + i];
-        sn[i] = s_rope[NQ * 64 + t * 64 + (j & 7) * 8 + i];
-      }
+      unpack8(c8, cs);
+      unpack8(s8, sn);
       const uint4 ov = qknorm_rope_row(raw, w8, cs, sn, a.eps, j);
       if (c < G) {
         s_q[(t * G + c) * 16 + j] = ov;
       } else {
         s_new[t * 16 + j] = ov;
         if (split == 0 && pos_ok)
-          *reinterpret_cast<uint4*>(a.kc + pos * a.tok_stride + (int64_t)kvh * a.head_stride + j * 8) = ov;
+          *reinterpret_cast<uint4*>(kc + pos * tok_stride + (int64_t)kvh * head_stride + j * 8) = ov;
       }
     } else {
       const int t = row / G, g = row % G;
       if (row != slot)
-        raw = *reinterpret_cast<const uint4*>(a.q + ((int64_t)t * a.nh + kvh * G + g) * SOLORT_HD + j * 8);
+        raw = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + (kvh * G + g) * SOLORT_HD + j * 8);
       s_q[row * 16 + j] = raw;
     }
   }
@@ -229,7 +210,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   //    row, and each lane accumulates dims 2*lane, 2*lane+1 of the output, so
   //    no per-slot state is merged.
   int64_t live64 = pos0 + NQ;
-  live64 = live64 < 0 ? 0 : (live64 > a.bound ? a.bound : live64);
+  live64 = live64 < 0 ? 0 : (live64 > bound ? bound : live64);
   const int kend = min(kstat, (int)live64);
   float M[RPW], Lk[RPW], O[RPW][2];  // Lk: this lane's share of the sum (its keys)
 #pragma unroll
@@ -246,10 +227,11 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int kid = min(k1 + u * 16 + slot, kend - 1);
-        kn[u] = *reinterpret_cast<const uint4*>(kp + (int64_t)kid * a.tok_stride);
-        vn[u] = *reinterpret_cast<const uint4*>(vp + (int64_t)kid * a.tok_stride);
+        kn[u] = *reinterpret_cast<const uint4*>(kp + (int64_t)kid * tok_stride);
+        vn[u] = *reinterpret_cast<const uint4*>(vp + (int64_t)kid * tok_stride);
       }
     }
+    float part[U * R];  // this lane's share of each score, index u * R + r
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int kid = k0 + u * 16 + slot;
@@ -260,20 +242,30 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
           vr[u] = s_new[(NQ + off) * 16 + j];
         }
       }
-      const bool in = kid < kend;
-      if (!in) vr[u] = make_uint4(0u, 0u, 0u, 0u);  // p = 0 must not meet a non-finite value
+      if (kid >= kend) vr[u] = make_uint4(0u, 0u, 0u, 0u);  // p = 0 must not meet a non-finite value
+      s_v[(u * 16 + slot) * 16 + j] = vr[u];
 #pragma unroll
       for (int r = 0; r < R; ++r) {
         float d = dot2bf(kr[u].x, qb[r].x, 0.f);
         d = dot2bf(kr[u].y, qb[r].y, d);
         d = dot2bf(kr[u].z, qb[r].z, d);
-        d = dot2bf(kr[u].w, qb[r].w, d);
-        d = row16_sum(d) * a.qscale;
-        const int t = r / G;
-        if (!in || (int64_t)kid > pos0 + t) d = -INFINITY;
-        if (j == 0) s_s[r * KPI + u * 16 + slot] = d;
+        part[u * R + r] = dot2bf(kr[u].w, qb[r].w, d);
       }
-      s_v[(u * 16 + slot) * 16 + j] = vr[u];
+    }
+    // Sum the shares over the slot's 16 lanes, eight scores at a time: lane j
+    // ends with score c * 8 + j / 2 and the even lanes write them.
+#pragma unroll
+    for (int c = 0; c < (U * R + 7) / 8; ++c) {
+      float v8[8];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) v8[i] = c * 8 + i < U * R ? part[c * 8 + i] : 0.f;
+      const float sum = row16_reduce8(v8, j);
+      const int idx = c * 8 + (j >> 1);
+      if ((j & 1) == 0 && idx < U * R) {
+        const int u = idx / R, r = idx % R, t = r / G;
+        const int kid = k0 + u * 16 + slot;
+        s_s[r * KPI + u * 16 + slot] = kid < kend && (int64_t)kid <= pos0 + t ? sum * a.qscale : -INFINITY;
+      }
     }
     lds_barrier();
     // Dims 2*lane, 2*lane+1 of every key of the iteration, held in registers
@@ -302,21 +294,21 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
           __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
           __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
           const float4* p4 = reinterpret_cast<const float4*>(srow);
-          float o0 = O[i][0] * alpha, o1 = O[i][1] * alpha;
+          float oa[4] = {O[i][0] * alpha, 0.f, 0.f, 0.f}, ob[4] = {O[i][1] * alpha, 0.f, 0.f, 0.f};
 #pragma unroll
-          for (int k4 = 0; k4 < KPI / 4; ++k4) {
+          for (int k4 = 0; k4 < KPI / 4; ++k4) {  // four independent accumulator chains per dim
             const float4 p = p4[k4];
             const float pp[4] = {p.x, p.y, p.z, p.w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
               const int k = 4 * k4 + e;
               const uint32_t vk = kHoistV ? v2[kHoistV ? k : 0] : s_v32[k * 64 + lane];
-              o0 = fmaf(pp[e], __uint_as_float(vk << 16), o0);
-              o1 = fmaf(pp[e], __uint_as_float(vk & 0xffff0000u), o1);
+              oa[e] = fmaf(pp[e], __uint_as_float(vk << 16), oa[e]);
+              ob[e] = fmaf(pp[e], __uint_as_float(vk & 0xffff0000u), ob[e]);
             }
           }
-          O[i][0] = o0;
-          O[i][1] = o1;
+          O[i][0] = (oa[0] + oa[1]) + (oa[2] + oa[3]);
+          O[i][1] = (ob[0] + ob[1]) + (ob[2] + ob[3]);
           M[i] = mx;
         }
       }
@@ -340,7 +332,7 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
     const float Ls = wave_sum(Lk[i]);
     if (NS == 1) {
       const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
-      store_out2(a.out, a.out_f32, a.nh, kvh, G, r, 2 * lane, O[i][0] * inv, O[i][1] * inv);
+      store_out2(a.out, a.out_f32, nh, kvh, G, r, 2 * lane, O[i][0] * inv, O[i][1] * inv);
     } else {
       const int64_t pr = (int64_t)(kvh * NS + split) * R + r;
       *reinterpret_cast<float2*>(a.ws_o + pr * 128 + 2 * lane) = make_float2(O[i][0], O[i][1]);
@@ -349,32 +341,27 @@ __global__ __launch_bounds__(256) void decode_kernel(const DecodeArgs a) {
   }
 }
 
-struct CombineArgs {
-  const float* ws_o;
-  const float* ws_ml;
-  void* out;
-  int nh, nkv, n_split, out_f32;
-};
-
-// The log-sum-exp combine of the n_split partials of each KV head.  Block =
-// (KV head, 32 float4 columns of its [R][128] output); thread = (column,
-// split group sg of 8): it merges splits sg, sg+8, ... on its own (all loads
-// issued together), then the 8 split groups meet once in LDS.
+// The log-sum-exp combine of the n_split partials of each KV head.  Grid
+// (nkv, column blocks): block = (KV head, 32 float4 columns of its [R][128]
+// output); thread = (column, split group sg of 8): it merges splits sg,
+// sg+8, ... on its own (all loads issued together), then the 8 split groups
+// meet once in LDS.  Every argument is preloaded.
 template <int NQ, int G>
-__global__ __launch_bounds__(256) void combine_kernel(const CombineArgs a) {
+__global__ __launch_bounds__(256) void combine_kernel(const float* ws_o, const float* ws_ml, void* out, int nh,
+                                                      int n_split, int out_f32) {
   constexpr int R = NQ * G;
   constexpr int C = R * 32;  // float4 columns
   constexpr int B = 8;       // splits per thread per batch
   __shared__ float s_m[8][32], s_l[8][32];
   __shared__ float4 s_o[8][32];
   const int tid = threadIdx.x, c = tid & 31, sg = tid >> 5;
-  const int kvh = blockIdx.x % a.nkv, cb = blockIdx.x / a.nkv;
+  const int kvh = blockIdx.x, cb = blockIdx.y;
   const int col = cb * 32 + c;
   const bool act = col < C;
   const int r = col >> 5;
-  const int NS = a.n_split;
-  const float2* wml = reinterpret_cast<const float2*>(a.ws_ml) + (int64_t)kvh * NS * R;
-  const float4* wo = reinterpret_cast<const float4*>(a.ws_o) + (int64_t)kvh * NS * C;
+  const int NS = n_split;
+  const float2* wml = reinterpret_cast<const float2*>(ws_ml) + (int64_t)kvh * NS * R;
+  const float4* wo = reinterpret_cast<const float4*>(ws_o) + (int64_t)kvh * NS * C;
   float mloc = -INFINITY, lloc = 0.f;
   float4 oloc = make_float4(0.f, 0.f, 0.f, 0.f);
   for (int s0 = sg; s0 < NS; s0 += 8 * B) {
@@ -427,7 +414,7 @@ __global__ __launch_bounds__(256) void combine_kernel(const CombineArgs a) {
     }
     const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
     Os.x *= inv; Os.y *= inv; Os.z *= inv; Os.w *= inv;
-    store_out(a.out, a.out_f32, a.nh, kvh, G, col, Os);
+    store_out(out, out_f32, nh, kvh, G, col, Os);
   }
 }
 
@@ -435,6 +422,17 @@ __global__ __launch_bounds__(256) void combine_kernel(const CombineArgs a) {
 
 constexpr int kMaxRows = 20;  // nq * group limit (registers and LDS)
 constexpr int kMaxSplit = 1024;
+
+// Everything a launch needs, gathered by prepare() and the entry points.
+struct DecodeArgs {
+  uint16_t* kc;
+  uint16_t* vc;
+  int tok_stride, head_stride, chunk, bound;
+  const uint16_t* qsrc;
+  int qsrc_stride, nh, nkv, n_split;
+  const uint16_t* qn_w;
+  DecodeTail tail;
+};
 
 struct WsLayout {
   size_t ml_off, o_off, total;
@@ -451,16 +449,22 @@ static WsLayout ws_layout(int nq, int nh, int nkv, int n_split) {
   return w;
 }
 
+template <int NQ, int G, int U, bool FUSED>
+static void launch_split(const DecodeArgs& a, hipStream_t s) {
+  hipLaunchKernelGGL((decode_kernel<NQ, G, U, FUSED>), dim3(a.nkv, a.n_split), dim3(256), 0, s, a.kc, a.vc,
+                     a.tok_stride, a.head_stride, a.chunk, a.bound, a.qsrc, a.qsrc_stride, a.nh, a.qn_w, a.tail);
+}
+
 template <int NQ, int G, bool FUSED>
-static bool launch_u(int U, const DecodeArgs& a, int blocks, hipStream_t s) {
+static bool launch_u(int U, const DecodeArgs& a, hipStream_t s) {
   if constexpr (NQ * G <= kMaxRows) {
     if constexpr (NQ == 1) {
       if (U == 4) {
-        hipLaunchKernelGGL((decode_kernel<NQ, G, 4, FUSED>), dim3(blocks), dim3(256), 0, s, a);
+        launch_split<NQ, G, 4, FUSED>(a, s);
         return true;
       }
     }
-    hipLaunchKernelGGL((decode_kernel<NQ, G, 2, FUSED>), dim3(blocks), dim3(256), 0, s, a);
+    launch_split<NQ, G, 2, FUSED>(a, s);
     return true;
   } else {
     return false;
@@ -468,9 +472,11 @@ static bool launch_u(int U, const DecodeArgs& a, int blocks, hipStream_t s) {
 }
 
 template <int NQ, int G>
-static bool launch_combine(const CombineArgs& c, int blocks, hipStream_t s) {
+static bool launch_combine(const DecodeArgs& a, hipStream_t s) {
   if constexpr (NQ * G <= kMaxRows) {
-    hipLaunchKernelGGL((combine_kernel<NQ, G>), dim3(blocks), dim3(256), 0, s, c);
+    constexpr int C = NQ * G * 32;  // float4 columns per KV head
+    hipLaunchKernelGGL((combine_kernel<NQ, G>), dim3(a.nkv, (C + 31) / 32), dim3(256), 0, s, a.tail.ws_o,
+                       a.tail.ws_ml, a.tail.out, a.nh, a.n_split, a.tail.out_f32);
     return true;
   } else {
     return false;
@@ -492,39 +498,41 @@ static bool launch_combine(const CombineArgs& c, int blocks, hipStream_t s) {
   return false;
 
 template <int NQ, int G>
-static bool launch_attn(bool fused, int U, const DecodeArgs& a, int blocks, hipStream_t s) {
-  return fused ? launch_u<NQ, G, true>(U, a, blocks, s) : launch_u<NQ, G, false>(U, a, blocks, s);
+static bool launch_attn(bool fused, int U, const DecodeArgs& a, hipStream_t s) {
+  return fused ? launch_u<NQ, G, true>(U, a, s) : launch_u<NQ, G, false>(U, a, s);
 }
 
 template <int G>
-static bool attn_nq(int nq, bool fused, int U, const DecodeArgs& a, int blocks, hipStream_t s) {
-  SOLORT_DISPATCH_NQ(G, launch_attn, fused, U, a, blocks, s)
+static bool attn_nq(int nq, bool fused, int U, const DecodeArgs& a, hipStream_t s) {
+  SOLORT_DISPATCH_NQ(G, launch_attn, fused, U, a, s)
 }
 
 template <int G>
-static bool combine_nq(int nq, const CombineArgs& c, int blocks, hipStream_t s) {
-  SOLORT_DISPATCH_NQ(G, launch_combine, c, blocks, s)
+static bool combine_nq(int nq, const DecodeArgs& a, hipStream_t s) {
+  SOLORT_DISPATCH_NQ(G, launch_combine, a, s)
 }
 
-static bool dispatch_attn(int G, int nq, bool fused, int U, const DecodeArgs& a, int blocks, hipStream_t s) {
+static bool dispatch_attn(int G, int nq, bool fused, int U, const DecodeArgs& a, hipStream_t s) {
   switch (G) {
-    case 1: return attn_nq<1>(nq, fused, U, a, blocks, s);
-    case 2: return attn_nq<2>(nq, fused, U, a, blocks, s);
-    case 4: return attn_nq<4>(nq, fused, U, a, blocks, s);
-    case 8: return attn_nq<8>(nq, fused, U, a, blocks, s);
+    case 1: return attn_nq<1>(nq, fused, U, a, s);
+    case 2: return attn_nq<2>(nq, fused, U, a, s);
+    case 4: return attn_nq<4>(nq, fused, U, a, s);
+    case 8: return attn_nq<8>(nq, fused, U, a, s);
   }
   return false;
 }
 
-static bool dispatch_combine(int G, int nq, const CombineArgs& c, int blocks, hipStream_t s) {
+static bool dispatch_combine(int G, int nq, const DecodeArgs& a, hipStream_t s) {
   switch (G) {
-    case 1: return combine_nq<1>(nq, c, blocks, s);
-    case 2: return combine_nq<2>(nq, c, blocks, s);
-    case 4: return combine_nq<4>(nq, c, blocks, s);
-    case 8: return combine_nq<8>(nq, c, blocks, s);
+    case 1: return combine_nq<1>(nq, a, s);
+    case 2: return combine_nq<2>(nq, a, s);
+    case 4: return combine_nq<4>(nq, a, s);
+    case 8: return combine_nq<8>(nq, a, s);
   }
   return false;
 }
+
+constexpr int64_t kMaxI32 = 0x7fffffff;
 
 // Checks shared by every attention entry point; fills the attention part of `a`.
 static int prepare(const char* name, int nq, int nh, int nkv, int hd, void* k_cache, void* v_cache,
@@ -543,8 +551,11 @@ static int prepare(const char* name, int nq, int nh, int nkv, int hd, void* k_ca
     return set_error(SOLORT_EINVAL, "%s: null pointer", name);
   if (!aligned16(k_cache) || !aligned16(v_cache) || !aligned16(ws) || !aligned16(out))
     return set_error(SOLORT_EINVAL, "%s: pointers must be 16-byte aligned", name);
-  if (kv_tok_stride <= 0 || kv_head_stride <= 0 || kv_tok_stride % 8 || kv_head_stride % 8)
-    return set_error(SOLORT_EINVAL, "%s: KV strides must be positive multiples of 8", name);
+  if (kv_tok_stride <= 0 || kv_head_stride <= 0 || kv_tok_stride % 8 || kv_head_stride % 8 ||
+      kv_tok_stride > kMaxI32 || kv_head_stride > kMaxI32)
+    return set_error(SOLORT_EINVAL, "%s: KV strides must be positive multiples of 8 below 2^31", name);
+  if (max_len < 1 || max_len > kMaxI32)
+    return set_error(SOLORT_EINVAL, "%s: max_len %lld outside [1, 2^31)", name, (long long)max_len);
   if (bound < 1 || bound > max_len || bound > (1 << 30))
     return set_error(SOLORT_EINVAL, "%s: bound %d outside [1, max_len=%lld]", name, bound, (long long)max_len);
   if (n_split < 1 || n_split > kMaxSplit)
@@ -554,39 +565,32 @@ static int prepare(const char* name, int nq, int nh, int nkv, int hd, void* k_ca
   const WsLayout w = ws_layout(nq, nh, nkv, n_split);
   a.kc = (uint16_t*)k_cache;
   a.vc = (uint16_t*)v_cache;
-  a.tok_stride = kv_tok_stride;
-  a.head_stride = kv_head_stride;
-  a.pos0_dev = pos0_dev;
-  a.ws_o = (float*)((char*)ws + w.o_off);
-  a.ws_ml = (float*)((char*)ws + w.ml_off);
-  a.out = out;
-  a.qscale = scale * 1.4426950408889634f;
+  a.tok_stride = (int)kv_tok_stride;
+  a.head_stride = (int)kv_head_stride;
+  a.chunk = ((((bound + n_split - 1) / n_split) + 15) / 16) * 16;  // static key chunk per split
+  a.bound = bound;
   a.nh = nh;
   a.nkv = nkv;
-  a.bound = bound;
   a.n_split = n_split;
-  a.out_f32 = out_dtype == SOLORT_DTYPE_F32;
-  const int per_split = (((bound + n_split - 1) / n_split) + 15) & ~15;
-  U = per_split >= 64 ? 4 : 2;
+  a.tail.pos0_dev = pos0_dev;
+  a.tail.ws_o = (float*)((char*)ws + w.o_off);
+  a.tail.ws_ml = (float*)((char*)ws + w.ml_off);
+  a.tail.out = out;
+  a.tail.qscale = scale * 1.4426950408889634f;
+  a.tail.pos_limit = (int)max_len;
+  a.tail.out_f32 = out_dtype == SOLORT_DTYPE_F32;
+  U = a.chunk >= 64 ? 4 : 2;
   return 0;
 }
 
 // Launches the split kernel, then (more than one split) the combine kernel.
 static int launch_all(const char* name, bool fused, int nq, const DecodeArgs& a, int U, hipStream_t s) {
-  const int G = a.nh / a.nkv, C = nq * G * 32;
-  if (!dispatch_attn(G, nq, fused, U, a, a.n_split * a.nkv, s))
+  const int G = a.nh / a.nkv;
+  if (!dispatch_attn(G, nq, fused, U, a, s))
     return set_error(SOLORT_EINVAL, "%s: no kernel for nq=%d group=%d", name, nq, G);
   int rc = check_launch(name);
   if (rc || a.n_split == 1) return rc;
-  CombineArgs c;
-  c.ws_o = a.ws_o;
-  c.ws_ml = a.ws_ml;
-  c.out = a.out;
-  c.nh = a.nh;
-  c.nkv = a.nkv;
-  c.n_split = a.n_split;
-  c.out_f32 = a.out_f32;
-  if (!dispatch_combine(G, nq, c, ((C + 31) / 32) * a.nkv, s))
+  if (!dispatch_combine(G, nq, a, s))
     return set_error(SOLORT_EINVAL, "%s: no combine kernel for nq=%d group=%d", name, nq, G);
   return check_launch(name);
 }
@@ -602,7 +606,8 @@ static int attn_impl(const char* name, const void* q, int nq, int nh, int nkv, i
                    max_len, pos0_dev, bound, scale, ws, n_split, out, out_dtype, a, U);
   if (rc) return rc;
   if (!q || !aligned16(q)) return set_error(SOLORT_EINVAL, "%s: q must be a 16-byte aligned pointer", name);
-  a.q = (const uint16_t*)q;
+  a.qsrc = (const uint16_t*)q;
+  a.qsrc_stride = nh * SOLORT_HD;
   return launch_all(name, false, nq, a, U, (hipStream_t)stream);
 }
 
@@ -634,7 +639,7 @@ extern "C" int solort_verify_attn(const void* q, int nq, int nh, int nkv, int hd
 }
 
 extern "C" int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int nq, int nh, int nkv, int hd,
-                                   const void* qn_w, const void* kn_w, float eps, const float* inv_freq,
+                                   const void* qn_w, const void* kn_w, float eps, const void* rope_cs,
                                    const int64_t* pos0_dev, void* k_cache, void* v_cache, int64_t kv_tok_stride,
                                    int64_t kv_head_stride, int64_t max_len, int bound, float scale, void* ws,
                                    int n_split, void* out, int out_dtype, solort_stream_t stream) {
@@ -644,17 +649,16 @@ extern "C" int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int 
   int rc = prepare(name, nq, nh, nkv, hd, k_cache, v_cache, kv_tok_stride, kv_head_stride, max_len, pos0_dev,
                    bound, scale, ws, n_split, out, out_dtype, a, U);
   if (rc) return rc;
-  if (!qkv || !qn_w || !kn_w || !inv_freq) return set_error(SOLORT_EINVAL, "%s: null pointer", name);
-  if (!aligned16(qkv) || !aligned16(qn_w) || !aligned16(kn_w) || !aligned16(inv_freq))
+  if (!qkv || !qn_w || !kn_w || !rope_cs) return set_error(SOLORT_EINVAL, "%s: null pointer", name);
+  if (!aligned16(qkv) || !aligned16(qn_w) || !aligned16(kn_w) || !aligned16(rope_cs))
     return set_error(SOLORT_EINVAL, "%s: pointers must be 16-byte aligned", name);
-  if (qkv_row_stride < (int64_t)(nh + 2 * nkv) * hd || qkv_row_stride % 8 != 0)
+  if (qkv_row_stride < (int64_t)(nh + 2 * nkv) * hd || qkv_row_stride % 8 != 0 || qkv_row_stride > kMaxI32)
     return set_error(SOLORT_EINVAL, "%s: qkv_row_stride %lld", name, (long long)qkv_row_stride);
-  a.qkv = (const uint16_t*)qkv;
-  a.qkv_stride = qkv_row_stride;
+  a.qsrc = (const uint16_t*)qkv;
+  a.qsrc_stride = (int)qkv_row_stride;
   a.qn_w = (const uint16_t*)qn_w;
-  a.kn_w = (const uint16_t*)kn_w;
-  a.inv_freq = inv_freq;
-  a.pos_limit = max_len;
-  a.eps = eps;
+  a.tail.kn_w = (const uint16_t*)kn_w;
+  a.tail.rope_cs = (const uint16_t*)rope_cs;
+  a.tail.eps = eps;
   return launch_all(name, true, nq, a, U, (hipStream_t)stream);
 }

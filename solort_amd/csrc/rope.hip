@@ -1,11 +1,16 @@
-// RoPE cos/sin table on the device: row p holds bf16(cos(float(p) * inv_freq[i]))
+// RoPE cos/sin on the device: row p holds bf16(cos(float(p) * inv_freq[i]))
 // and bf16(sin(...)) for i < half_dim, i.e. the first half of the reference's
 // _cos_sin(p) row (src/solort/model/cuda_graph_executor.py:95-98; the second
 // half of that row repeats the first).  inv_freq is the caller's fp32 vector
-// (the reference computes it at :64-66).  The values come from rope_cs8
-// (common.h), the function the prologue and fused decode kernels evaluate
-// in-kernel, so comparing this table with torch's checks those kernels' RoPE
-// inputs too.
+// (the reference computes it at :64-66).
+//   rope_table_kernel: rows 0..rows-1 (a whole table).
+//   rope_rows_kernel:  the rows of positions pos0..pos0+n-1, pos0 read on the
+//                      device; a decode or verify step computes them once and
+//                      every layer's fused kernel loads them, as the reference
+//                      computes cos, sin once per step (:164, :248).
+// Both evaluate rope_angle/rope_cos/rope_sin (common.h), the functions the
+// prefill prologue evaluates in-kernel, so comparing the table with torch's
+// checks all RoPE inputs.
 #include "common.h"
 #include "capi_internal.h"
 
@@ -31,9 +36,31 @@ __global__ __launch_bounds__(256) void rope_table_kernel(const float* __restrict
   }
 }
 
+// One thread per (row, cos|sin, frequency); cs_out = cos [n][half_dim] then sin [n][half_dim].
+__global__ __launch_bounds__(256) void rope_rows_kernel(const float* __restrict__ inv_freq, int half_dim,
+                                                        const int64_t* __restrict__ pos0_dev, int n,
+                                                        uint16_t* __restrict__ cs_out) {
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= 2 * n * half_dim) return;
+  const int f = idx % half_dim, t = (idx / half_dim) % n, sn = idx / (half_dim * n);
+  const float ang = rope_angle(pos0_dev[0] + t, inv_freq[f]);
+  cs_out[idx] = (uint16_t)f2bf(sn ? rope_sin(ang) : rope_cos(ang));
+}
+
 }  // namespace solort
 
 using namespace solort;
+
+extern "C" int solort_rope_rows(const float* inv_freq, int half_dim, const int64_t* pos0_dev, int n, void* cs_out,
+                                solort_stream_t stream) {
+  if (!inv_freq || !pos0_dev || !cs_out) return set_error(SOLORT_EINVAL, "rope_rows: null pointer");
+  if (half_dim < 1 || half_dim > 1024 || n < 1 || n > 64)
+    return set_error(SOLORT_EINVAL, "rope_rows: bad shape half_dim=%d n=%d", half_dim, n);
+  const int total = 2 * n * half_dim;
+  hipLaunchKernelGGL(rope_rows_kernel, dim3((total + 255) / 256), dim3(256), 0, (hipStream_t)stream, inv_freq,
+                     half_dim, pos0_dev, n, (uint16_t*)cs_out);
+  return check_launch("rope_rows");
+}
 
 extern "C" int solort_rope_table(const float* inv_freq, int half_dim, int64_t rows, void* cos_out,
                                  void* sin_out, solort_stream_t stream) {

@@ -79,6 +79,26 @@ def rope_tables_device(inv_freq: torch.Tensor, rows: int) -> tuple[torch.Tensor,
     return cos, sin
 
 
+def rope_rows(inv_f: torch.Tensor, pos0: torch.Tensor, n: int, out: torch.Tensor | None = None) -> torch.Tensor:
+    """cos/sin rows [2, n, 64] bf16 of positions pos0..pos0+n-1 (pos0 int64 on the device), computed once
+    per decode/verify step for every layer's decode_layer; see solort_rope_rows."""
+    _inv_freq_ok(inv_f)
+    _need(pos0.is_cuda and pos0.dtype == torch.int64 and pos0.numel() >= 1, "pos0 must be int64 on the device")
+    if out is None:
+        out = torch.empty(2, n, HD // 2, dtype=torch.bfloat16, device=inv_f.device)
+    _rope_rows_ok(out, n)
+    rc = _lib.load().solort_rope_rows(inv_f.data_ptr(), HD // 2, pos0.data_ptr(), int(n), out.data_ptr(),
+                                      _stream(inv_f))
+    _lib.check(rc, "rope_rows")
+    return out
+
+
+def _rope_rows_ok(cs: torch.Tensor, n: int) -> None:
+    _on_gpu("rope_cs", cs, torch.bfloat16)
+    _need(cs.shape == (2, n, HD // 2) and cs.is_contiguous() and cs.data_ptr() % 16 == 0,
+          f"rope_cs must be [2, {n}, {HD // 2}] contiguous and 16-byte aligned")
+
+
 def _inv_freq_ok(f: torch.Tensor) -> None:
     _on_gpu("inv_freq", f, torch.float32)
     _need(f.shape == (HD // 2,) and f.is_contiguous(), f"inv_freq must be [{HD // 2}] contiguous fp32")
@@ -163,13 +183,14 @@ def verify_attn(q, k_cache, v_cache, pos0, bound, scale, ws, n_split, out) -> No
     _attn("solort_verify_attn", q, k_cache, v_cache, pos0, bound, scale, ws, n_split, out)
 
 
-def decode_layer(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps: float, inv_f: torch.Tensor,
+def decode_layer(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps: float, rope_cs: torch.Tensor,
                  pos0: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, bound: int, scale: float,
                  ws: torch.Tensor, n_split: int, out: torch.Tensor, nh: int, nkv: int) -> None:
     """One layer's attention block: prologue + KV write of the nq new tokens (qkv [nq, (nh+2nkv)*128])
     at pos0.. and split-KV attention into out [nq, nh*128].
 
-    Equal to qknorm_rope_kvwrite followed by decode_attn; see solort_decode_layer.
+    rope_cs: this step's rope_rows(inv_f, pos0, nq).  Equal to qknorm_rope_kvwrite followed by
+    decode_attn; see solort_decode_layer.
     """
     _on_gpu("qkv", qkv, torch.bfloat16)
     _need(qkv.dim() == 2 and qkv.shape[1] == (nh + 2 * nkv) * HD and qkv.stride(1) == 1,
@@ -178,7 +199,7 @@ def decode_layer(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps:
     for name, w in (("qn_w", qn_w), ("kn_w", kn_w)):
         _on_gpu(name, w, torch.bfloat16)
         _need(w.shape == (HD,) and w.is_contiguous(), f"{name} must be [{HD}] contiguous")
-    _inv_freq_ok(inv_f)
+    _rope_rows_ok(rope_cs, nq)
     ts, hs, max_len = _cache_strides("k_cache", k_cache, nkv)
     _on_gpu("v_cache", v_cache, torch.bfloat16)
     _need(v_cache.shape == k_cache.shape and v_cache.stride() == k_cache.stride(),
@@ -194,7 +215,7 @@ def decode_layer(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps:
     dt = DTYPE_F32 if out.dtype == torch.float32 else DTYPE_BF16
     rc = lib.solort_decode_layer(
         qkv.data_ptr(), qkv.stride(0), nq, nh, nkv, HD, qn_w.data_ptr(), kn_w.data_ptr(), float(eps),
-        inv_f.data_ptr(), pos0.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), ts, hs, max_len, int(bound),
+        rope_cs.data_ptr(), pos0.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), ts, hs, max_len, int(bound),
         float(scale), ws.data_ptr(), int(n_split), out.data_ptr(), dt, _stream(qkv))
     _lib.check(rc, "decode_layer")
 

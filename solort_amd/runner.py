@@ -75,6 +75,7 @@ class GraphQwen3Attention:
         self.ctx_dec = torch.zeros(layers, 1, nh * HD, dtype=torch.bfloat16, device=self.dev)
         self.logits_dec = torch.zeros(1, self.vocab, dtype=torch.float32, device=self.dev)
         self.tok_dec = torch.zeros(1, dtype=torch.long, device=self.dev)
+        self.cs_dec = torch.zeros(2, 1, HD // 2, dtype=torch.bfloat16, device=self.dev)  # this step's cos/sin
         self.ws_dec = ops.attn_workspace(1, nh, nkv, max(decode_splits(b, nkv) for b in self.buckets), self.dev)
         self.ws_arg = ops.argmax_workspace(max(1, verify_tokens), self.dev)
         self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
@@ -85,6 +86,7 @@ class GraphQwen3Attention:
         self.logits_ver = torch.zeros(self.k1, self.vocab, dtype=torch.float32, device=self.dev)
         self.tok_ver = torch.zeros(self.k1, dtype=torch.long, device=self.dev)
         self.vpos0 = torch.zeros(1, dtype=torch.long, device=self.dev)
+        self.cs_ver = torch.zeros(2, self.k1, HD // 2, dtype=torch.bfloat16, device=self.dev)
         self.ws_ver = ops.attn_workspace(self.k1, nh, nkv, max(verify_splits(b) for b in self.buckets), self.dev)
         self._ver_graphs: dict[int, torch.cuda.CUDAGraph] = {}
         # prefill: padded prompt rows per layer, bucketed graphs
@@ -98,8 +100,9 @@ class GraphQwen3Attention:
 
     def _decode_forward(self, bound: int) -> None:
         ns = decode_splits(bound, self.nkv)
+        ops.rope_rows(self.inv_freq, self.pos_buf, 1, self.cs_dec)  # once per step (:164)
         for li in range(self.L):
-            ops.decode_layer(self.qkv_dec[li], self.qn_w[li], self.kn_w[li], self.eps, self.inv_freq, self.pos_buf,
+            ops.decode_layer(self.qkv_dec[li], self.qn_w[li], self.kn_w[li], self.eps, self.cs_dec, self.pos_buf,
                              self.kc[li], self.vc[li], bound, self.scale, self.ws_dec, ns,
                              self.ctx_dec[li], self.nh, self.nkv)
         ops.argmax_rows(self.logits_dec, self.tok_dec, self.ws_arg)
@@ -171,8 +174,9 @@ class GraphQwen3Attention:
 
     def _verify_forward(self, bound: int) -> None:
         ns = verify_splits(bound)
+        ops.rope_rows(self.inv_freq, self.vpos0, self.k1, self.cs_ver)  # once per step (:248)
         for li in range(self.L):
-            ops.decode_layer(self.qkv_ver[li], self.qn_w[li], self.kn_w[li], self.eps, self.inv_freq, self.vpos0,
+            ops.decode_layer(self.qkv_ver[li], self.qn_w[li], self.kn_w[li], self.eps, self.cs_ver, self.vpos0,
                              self.kc[li], self.vc[li], bound, self.scale, self.ws_ver, ns,
                              self.ctx_ver[li], self.nh, self.nkv)
         ops.argmax_rows(self.logits_ver, self.tok_ver, self.ws_arg)

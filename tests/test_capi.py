@@ -87,6 +87,10 @@ def test_prologue_and_argmax_reject_bad_arguments(lib):
     assert rc == EINVAL and "null" in _err(lib)
     rc = lib.solort_rope_table(p, 60, 10, p, p, None)
     assert rc == EINVAL and "half_dim" in _err(lib)
+    rc = lib.solort_rope_rows(p, 64, p, 0, p, None)
+    assert rc == EINVAL and "n=0" in _err(lib)
+    rc = lib.solort_rope_rows(p, 64, None, 1, p, None)
+    assert rc == EINVAL and "null" in _err(lib)
     rc = lib.solort_argmax_rows(p, 3, 1, 10, 10, p, p, None)
     assert rc == EINVAL and "dtype" in _err(lib)
     rc = lib.solort_argmax_rows(p, 0, 1, 10, 5, p, p, None)

@@ -296,7 +296,8 @@ def test_decode_layer_equals_prologue_then_attention(gpu, index, live, n_split):
         ops.qknorm_rope_kvwrite(qkv, qn, kn, wl.EPS, ifr, pos, q, kc_a, vc_a, sh.nh, sh.nkv)
         fn = ops.decode_attn if case.nq == 1 else ops.verify_attn
         fn(q, kc_a, vc_a, pos, case.bound, sh.scale, ws, n_split, out_a)
-        ops.decode_layer(qkv, qn, kn, wl.EPS, ifr, pos, kc_b, vc_b, case.bound, sh.scale, ws, n_split, out_b,
+        ops.decode_layer(qkv, qn, kn, wl.EPS, ops.rope_rows(ifr, pos, case.nq), pos, kc_b, vc_b, case.bound,
+                         sh.scale, ws, n_split, out_b,
                          sh.nh, sh.nkv)
         torch.cuda.synchronize()
         assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b), "KV rows differ"
@@ -305,7 +306,7 @@ def test_decode_layer_equals_prologue_then_attention(gpu, index, live, n_split):
 
 def test_decode_layer_repeated_calls_reuse_workspace(gpu):
     """Ten back-to-back fused launches over different layers share one workspace and each matches
-    its own single launch (the tickets are left at zero)."""
+    the launch four calls earlier on the same layer."""
     case = wl.decode_case(1, live=1024, layers=4)
     dev = gpu
     sh = case.shape
@@ -314,9 +315,10 @@ def test_decode_layer_repeated_calls_reuse_workspace(gpu):
     kc, vc = case.kc.to(dev), case.vc.to(dev)
     ws = ops.attn_workspace(1, sh.nh, sh.nkv, 32, dev)
     outs = torch.empty(10, 1, sh.nh * HD, dtype=torch.float32, device=dev)
+    cs = ops.rope_rows(ifr, pos, 1)
     for i in range(10):
         li = i % 4
-        ops.decode_layer(case.qkv[li].to(dev), case.qn_w[li].to(dev), case.kn_w[li].to(dev), wl.EPS, ifr, pos,
+        ops.decode_layer(case.qkv[li].to(dev), case.qn_w[li].to(dev), case.kn_w[li].to(dev), wl.EPS, cs, pos,
                          kc[li], vc[li], case.bound, sh.scale, ws, 32, outs[i], sh.nh, sh.nkv)
     torch.cuda.synchronize()
     for i in range(4, 10):

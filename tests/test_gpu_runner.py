@@ -149,7 +149,8 @@ def test_prefill_graph_then_decode_continues(gpu):
     ws = ops.attn_workspace(1, sh.nh, sh.nkv, 32, gpu)
     p = torch.tensor([T], dtype=torch.long, device=gpu)
     dout = torch.empty(1, sh.nh * HD, dtype=torch.bfloat16, device=gpu)
-    ops.decode_layer(qd[1].to(gpu), r.qn_w[1], r.kn_w[1], r.eps, r.inv_freq, p, eager_kc[1], eager_vc[1], 512,
+    ops.decode_layer(qd[1].to(gpu), r.qn_w[1], r.kn_w[1], r.eps, ops.rope_rows(r.inv_freq, p, 1), p, eager_kc[1],
+                     eager_vc[1], 512,
                      r.scale, ws, 32, dout, sh.nh, sh.nkv)
     torch.cuda.synchronize()
     assert torch.allclose(dctx[1].float(), dout.float(), atol=2e-3, rtol=0)
