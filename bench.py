@@ -153,6 +153,8 @@ def main() -> int:
 
     if not args.no_sweep and args.only == "all":
         result["extras"] = extras(torch, ops, wl, runners, dev, sh)
+        result["extras"].update(verify_extras(torch, ops, wl, runners, dev, sh))
+        result["extras"]["decode_8b_kv32768"] = long_decode_extras(torch, ops, wl, dev)
     if args.only == "all":
         result["prefill"] = prefill_extras(torch, ops, runners, dev, sh)
         p1024 = result["prefill"].get("1024")
@@ -214,6 +216,107 @@ def extras(torch, ops, wl, runners, dev, sh) -> dict:
         us = time_decode_kernel(torch, ops, runners, 1024, ns, sh, dev, reps=3, pos=pos)
         out["n_split_sweep_kv1024"][str(ns)] = round(us, 3)
     return out
+
+
+def _graph_us(torch, dev, calls, reps=3) -> float:
+    """Mean time (us) per call of `calls` (a list of closures, each one launch sequence), from HIP
+    events around replays of one graph that holds them all."""
+    stream = torch.cuda.current_stream(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for c in calls:
+            c()
+    graph.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / (reps * len(calls))
+
+
+def long_decode_extras(torch, ops, wl, dev, n_caches: int = 8) -> dict:
+    """Qwen3-8B-shape decode at KV 32768 (32 q / 8 kv heads, bucket 32768): one solort_decode_layer
+    call per distinct 134 MB layer cache, n_caches caches (1.07 GB) rotated, for several split
+    counts.  Algorithmic bytes: K and V rows 0..32767 plus q and the output."""
+    sh = wl.QWEN3_8B
+    L, pos = 32768, 32767
+    gen = torch.Generator(device=dev).manual_seed(1003)
+    kcs = [torch.randn(L, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16) for _ in range(n_caches)]
+    vcs = [torch.randn(L, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16) for _ in range(n_caches)]
+    qkv = torch.randn(n_caches, 1, sh.qkv_width, generator=gen, device=dev).to(torch.bfloat16)
+    w = (1.0 + 0.1 * torch.randn(2, 128, generator=gen, device=dev)).to(torch.bfloat16)
+    posb = torch.tensor([pos], dtype=torch.long, device=dev)
+    inv = ops.inv_freq(128, wl.THETA, dev)
+    cs = ops.rope_rows(inv, posb, 1)
+    out = torch.empty(1, sh.nh * 128, dtype=torch.bfloat16, device=dev)
+    kbytes = decode_bytes(L, sh.nh, sh.nkv)
+    res = {"workload": "Qwen3-8B decode attention, batch 1, 32q/8kv heads, KV live 32768 (bucket 32768), "
+                       f"{n_caches} rotated layer caches", "algorithmic_bytes": kbytes, "by_n_split": {}}
+    best = None
+    for ns in (128, 256, 512):
+        ws = ops.attn_workspace(1, sh.nh, sh.nkv, ns, dev)
+        calls = [(lambda i=i, ws=ws, ns=ns: ops.decode_layer(qkv[i], w[0], w[1], wl.EPS, cs, posb, kcs[i], vcs[i],
+                                                             L, sh.scale, ws, ns, out, sh.nh, sh.nkv))
+                 for i in range(n_caches)]
+        us = _graph_us(torch, dev, calls, reps=4)
+        gbs = kbytes / (us * 1e-6) / 1e9
+        res["by_n_split"][str(ns)] = {"us": round(us, 3), "gbps": round(gbs, 1),
+                                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+        if best is None or us < best[1]:
+            best = (ns, us, gbs)
+    res.update({"n_split": best[0], "us": round(best[1], 3), "gbps": round(best[2], 1),
+                "frac_hbm": round(best[2] / HBM_PEAK_GBS, 4)})
+    del kcs, vcs
+    torch.cuda.empty_cache()
+    return res
+
+
+def verify_extras(torch, ops, wl, runners, dev, sh) -> dict:
+    """Speculative verify, Qwen3-4B shape: 5 queries at 2048..2052 over the cache (bucket 4096, the
+    runner's routing), one solort_decode_layer call per layer of every KV set; then the greedy argmax
+    of [5, 151936] bf16 logits.  Uses fresh max-4096 caches (8 sets x 36 layers rotated)."""
+    from solort_amd.runner import verify_splits
+
+    pos0, K1, bound = 2048, 5, 4096
+    gen = torch.Generator(device=dev).manual_seed(1004)
+    sets = []
+    for _ in range(len(runners)):
+        kc = torch.randn(sh.layers, bound, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16)
+        vc = torch.randn(sh.layers, bound, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16)
+        sets.append((kc, vc))
+    qkv = torch.randn(sh.layers, K1, sh.qkv_width, generator=gen, device=dev).to(torch.bfloat16)
+    posb = torch.tensor([pos0], dtype=torch.long, device=dev)
+    r0 = runners[0]
+    cs = ops.rope_rows(r0.inv_freq, posb, K1)
+    ns = verify_splits(bound)
+    ws = ops.attn_workspace(K1, sh.nh, sh.nkv, ns, dev)
+    out = torch.empty(K1, sh.nh * 128, dtype=torch.bfloat16, device=dev)
+    calls = [(lambda kc=kc, vc=vc, li=li: ops.decode_layer(qkv[li], r0.qn_w[li], r0.kn_w[li], r0.eps, cs, posb,
+                                                           kc[li], vc[li], bound, sh.scale, ws, ns, out, sh.nh,
+                                                           sh.nkv))
+             for kc, vc in sets for li in range(sh.layers)]
+    us = _graph_us(torch, dev, calls, reps=3)
+    vbytes = 2 * sh.nkv * (pos0 + K1) * 128 * 2 + K1 * 2 * sh.nh * 128 * 2
+    gbs = vbytes / (us * 1e-6) / 1e9
+    del sets
+    torch.cuda.empty_cache()
+    res = {"verify": {"us_per_layer_call": round(us, 3), "gbps": round(gbs, 1),
+                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "n_split": ns, "bucket": bound,
+                      "algorithmic_bytes": vbytes}}
+    g2 = torch.Generator().manual_seed(1004)
+    logits = [wl.planted_logits(g2, K1, wl.VOCAB).to(dev) for _ in range(2)]
+    logits += [torch.randn(K1, wl.VOCAB, generator=gen, device=dev).to(torch.bfloat16) for _ in range(6)]
+    idx = torch.empty(K1, dtype=torch.long, device=dev)
+    aws = ops.argmax_workspace(K1, dev)
+    calls = [(lambda x=x: ops.argmax_rows(x, idx, aws)) for x in logits]
+    aus = _graph_us(torch, dev, calls, reps=20)
+    abytes = K1 * wl.VOCAB * 2
+    res["argmax_5x151936_bf16"] = {"us": round(aus, 3), "gbps": round(abytes / (aus * 1e-6) / 1e9, 1),
+                                   "algorithmic_bytes": abytes}
+    return res
 
 
 def prefill_extras(torch, ops, runners, dev, sh) -> dict:

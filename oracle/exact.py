@@ -141,28 +141,40 @@ def splitkv_combine(q: np.ndarray, keys: np.ndarray, vals: np.ndarray, scale: fl
     return O / Lsum[:, None]
 
 
-def prefill_blockwise(q: np.ndarray, keys: np.ndarray, vals: np.ndarray, scale: float, block: int = 64) -> np.ndarray:
+def prefill_blockwise(q: np.ndarray, keys: np.ndarray, vals: np.ndarray, scale: float, block: int = 64,
+                      splits: int = 2) -> np.ndarray:
     """Causal attention of q [T,hd] (row t at position t) over keys/vals [T,hd] as the prefill kernel
-    evaluates it: per 64-key block, running max M (log2 units), p = bf16(2^(s - M)), l += sum of the
-    unrounded p, o = o * 2^(M_old - M) + p_bf16 @ V.  fp64 except the bf16 rounding of p."""
+    evaluates it: the 64-key blocks are dealt round-robin to `splits` independent passes (block b to
+    pass b % splits); each pass keeps its own running max M (log2 units) and, per block, takes
+    p = bf16(2^(s - M)), l += sum of the unrounded p, o = o * 2^(M_old - M) + p_bf16 @ V; the passes
+    are then merged by log-sum-exp.  fp64 except the bf16 rounding of p."""
     q = np.asarray(q, np.float64)
     T = q.shape[0]
     z = (q @ np.asarray(keys, np.float64).T) * scale * np.log2(np.e)
     z[np.triu_indices(T, 1)] = -np.inf
     vals = np.asarray(vals, np.float64)
-    m = np.full(T, -np.inf)
-    l = np.zeros(T)
-    o = np.zeros_like(q)
-    for k0 in range(0, T, block):
-        zb = z[:, k0:k0 + block]
-        mn = np.maximum(m, zb.max(axis=1))
-        live = np.isfinite(mn)
-        alpha = np.where(live, np.exp2(np.where(live, m - mn, 0.0)), 1.0)
-        p = np.where(live[:, None], np.exp2(zb - np.where(live, mn, 0.0)[:, None]), 0.0)
-        pb = np.asarray(bf16_round(p), np.float64)
-        l = l * alpha + p.sum(axis=1)
-        o = o * alpha[:, None] + pb @ vals[k0:k0 + block]
-        m = mn
+    parts = []
+    for sp in range(splits):
+        m = np.full(T, -np.inf)
+        l = np.zeros(T)
+        o = np.zeros_like(q)
+        for k0 in range(sp * block, T, splits * block):
+            zb = z[:, k0:k0 + block]
+            mn = np.maximum(m, zb.max(axis=1))
+            live = np.isfinite(mn)
+            with np.errstate(invalid="ignore"):  # -inf - -inf in rows not yet live; masked by `live`
+                alpha = np.where(live, np.exp2(np.where(live, m - mn, 0.0)), 1.0)
+            p = np.where(live[:, None], np.exp2(zb - np.where(live, mn, 0.0)[:, None]), 0.0)
+            pb = np.asarray(bf16_round(p), np.float64)
+            l = l * alpha + p.sum(axis=1)
+            o = o * alpha[:, None] + pb @ vals[k0:k0 + block]
+            m = mn
+        parts.append((m, l, o))
+    mt = np.max(np.stack([m for m, _, _ in parts]), axis=0)  # finite: pass 0 holds key 0
+    l = sum(np.where(np.isfinite(m), np.exp2(np.where(np.isfinite(m), m - mt, 0.0)), 0.0) * lp
+            for m, lp, _ in parts)
+    o = sum(np.where(np.isfinite(m), np.exp2(np.where(np.isfinite(m), m - mt, 0.0)), 0.0)[:, None] * op
+            for m, _, op in parts)
     return o / l[:, None]
 
 

@@ -45,9 +45,16 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
+# Per-source extra flags.  prefill.hip: MFMA results stay in architectural
+# VGPRs, where the softmax reads and rescales them, instead of AGPRs that
+# every VALU access would first have to copy out.
+EXTRA_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
+
+
 def _compile(src: Path) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(PKG.parent / "include"), "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-I", str(PKG.parent / "include"), "-c",
+           str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")

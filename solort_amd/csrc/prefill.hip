@@ -5,24 +5,34 @@
 //        scale=hd**-0.5) over the T prompt rows, written as ctx [T, nh*128].
 // K and V are read from the cache rows 0..T-1 the prologue just wrote (the
 // reference attends the same k/v values it writes at :122-123).  No repeat:
-// the g query heads of a KV head share every K/V tile staged in LDS.
+// the query heads of a KV head share every K/V tile staged in LDS.
 //
-// Block = 4 wavefronts = (KV head, tile of 16*(4/g) query rows); wave w owns
-// query head kvh*g + w%g and 16 query rows.  Per 64-key block:
-//   S^T = K Q^T   v_mfma_f32_16x16x32_bf16, A = K tile (LDS, row-major),
-//                 B = Q^T (registers), 4 key tiles x 4 dim steps
-//   online softmax in fp32 (log2 domain), P rounded to bf16
-//   O^T += V^T P^T  A = V^T (LDS, stored transposed), B = P^T (registers),
-//                 8 dim tiles x 2 key steps
-// Operand layouts (checked on gfx950): A[m][k] lane l holds
-// A[l%16][8(l/16)+s]; B[k][n] lane l holds B[8(l/16)+s][l%16]; D[m][n] lane l
-// holds D[4(l/16)+i][l%16].  With S^T and O^T every lane keeps one query row
-// (l%16), so softmax statistics never move between lanes except for the row
-// max (two lane exchanges).  The MFMA's key index is a permutation of the
-// block's keys shared by A and B, which lets P^T be fed straight from the
-// registers that hold S^T.
-// Causal: a tile reads only key blocks up to its last row and masks keys past
-// each row; tiles are dispatched heaviest first.
+// Block = 8 wavefronts = one KV head x 32 * (4 / g) positions.  Wave w
+// belongs to key half kh = w / 4 and owns query head kvh*g + (w%4)%g at
+// positions p0 + 32*((w%4)/g) .. +31 (32 query rows).  Each iteration stages
+// 128 keys (K row-major and V transposed, in LDS, double buffered; the next
+// iteration's global loads fly during this one's math); half kh takes the
+// iteration's 64-key block kh, so two waves share each SIMD and hide each
+// other's latencies, and the two halves of every row merge through LDS at the
+// end.  Per 64-key block:
+//   S^T = K Q^T   v_mfma_f32_32x32x16_bf16, A = K (LDS, one 16-byte read per
+//                 operand), B = Q^T (registers), 2 key tiles x 8 dim steps
+//   online softmax in fp32 (max over raw scores, p = 2^(s*c - m*c) with
+//                 c = scale*log2(e)), P rounded to bf16, O rescaled only
+//                 when some row's maximum moved
+//   O^T += V^T P^T  A = V^T (LDS), B = P^T straight from the S^T registers,
+//                 4 dim tiles x 4 key steps
+// MFMA operand layouts (checked on gfx950): A[m][k] lane l holds
+// A[l%32][8(l/32)+s]; B[k][n] lane l holds B[8(l/32)+s][l%32]; D[m][n] lane
+// l, register i holds D[8(i/4)+4(l/32)+i%4][l%32].  With S^T and O^T a lane
+// keeps one query row (l%32), so softmax statistics move between lanes only
+// for the row max (one exchange with lane l^32).  The key order inside each
+// 16-key MFMA step is a permutation shared by P^T (the registers of S^T) and
+// the V^T reads, so P needs no data movement.
+// Causal: a block reads key blocks up to its last position; waves skip key
+// blocks past their own rows and mask only blocks that cross their diagonal;
+// tiles are dispatched heaviest first, with all tiles of a KV head on one
+// XCD (block index mod 8).
 #include <math.h>
 
 #include "common.h"
@@ -31,7 +41,7 @@
 namespace solort {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 struct PrefillArgs {
   const uint16_t* q;  // [T][nh][128]
@@ -43,167 +53,247 @@ struct PrefillArgs {
   int T, nh, nkv, n_qtiles, out_f32;
 };
 
-constexpr int kKeys = 64;        // keys per staged block
-constexpr int kKStride = 128 + 8;  // K tile row stride (bf16), 272 bytes
-constexpr int kVStride = 64 + 4;   // V^T tile row stride (bf16), 136 bytes
+constexpr int kThreads = 512;      // 8 wavefronts
+constexpr int kKeys = 64;          // keys per wave per iteration
+constexpr int kStage = 2 * kKeys;  // keys staged per iteration
+constexpr int kKStride = 128 + 8;      // K tile row stride (bf16): 272 B, conflict-free 16-byte reads
+constexpr int kVStride = kStage + 4;   // V^T tile row stride (bf16): 264 B, conflict-free 8-byte reads
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
+// One staged block of 128 keys in flight in registers: per thread 4 K chunks
+// (key rows r0 + 32i, dims 8ch..8ch+7) and 4 V chunks (keys 4kg..4kg+3,
+// dims 8dg..8dg+7), 16 bytes each.
+struct Staged {
+  uint4 k0, k1, k2, k3, v0, v1, v2, v3;
+};
+
+// Per-thread staging geometry: K chunk (row r0 + 32 i, 16-byte column ch),
+// V chunk (keys 4kg..4kg+3, dims 8dg..8dg+7); kg varies fastest across lanes
+// so the 16 lanes of one LDS write cycle of V^T hit distinct banks.
+struct StageMap {
+  int r0, ch, kg, dg;
+};
+
+// Global loads of the staged block starting at key kb.  Keys at or past T
+// re-read row T-1 (finite values to which the causal mask gives weight 0 in
+// every row < T); a block entirely below T takes the unclamped path.
+__device__ __forceinline__ Staged prefill_fetch(const uint16_t* kbase, const uint16_t* vbase, int64_t ts, int T,
+                                                int kb, const StageMap& mp) {
+  Staged st;
+  if (kb + kStage <= T) {  // block-uniform
+    const uint16_t* kp = kbase + (int64_t)(kb + mp.r0) * ts + mp.ch * 8;
+    const uint16_t* vp = vbase + (int64_t)(kb + 4 * mp.kg) * ts + mp.dg * 8;
+    const int64_t k32 = 32 * ts;
+    st.k0 = *reinterpret_cast<const uint4*>(kp);
+    st.k1 = *reinterpret_cast<const uint4*>(kp + k32);
+    st.k2 = *reinterpret_cast<const uint4*>(kp + 2 * k32);
+    st.k3 = *reinterpret_cast<const uint4*>(kp + 3 * k32);
+    st.v0 = *reinterpret_cast<const uint4*>(vp);
+    st.v1 = *reinterpret_cast<const uint4*>(vp + ts);
+    st.v2 = *reinterpret_cast<const uint4*>(vp + 2 * ts);
+    st.v3 = *reinterpret_cast<const uint4*>(vp + 3 * ts);
+  } else {
+    auto kld = [&](int i) {
+      return *reinterpret_cast<const uint4*>(kbase + (int64_t)min(kb + mp.r0 + 32 * i, T - 1) * ts + mp.ch * 8);
+    };
+    auto vld = [&](int i) {
+      return *reinterpret_cast<const uint4*>(vbase + (int64_t)min(kb + 4 * mp.kg + i, T - 1) * ts + mp.dg * 8);
+    };
+    st.k0 = kld(0); st.k1 = kld(1); st.k2 = kld(2); st.k3 = kld(3);
+    st.v0 = vld(0); st.v1 = vld(1); st.v2 = vld(2); st.v3 = vld(3);
+  }
+  return st;
+}
+
+// Registers -> one LDS buffer: K as [key][dim], V transposed to [dim][key]
+// (one byte permute per output word).
+__device__ __forceinline__ void prefill_stage(const Staged& st, uint16_t* sk, uint16_t* svt, const StageMap& mp) {
+  uint16_t* kd = sk + mp.r0 * kKStride + mp.ch * 8;
+  *reinterpret_cast<uint4*>(kd) = st.k0;
+  *reinterpret_cast<uint4*>(kd + 32 * kKStride) = st.k1;
+  *reinterpret_cast<uint4*>(kd + 64 * kKStride) = st.k2;
+  *reinterpret_cast<uint4*>(kd + 96 * kKStride) = st.k3;
+  const uint32_t w0[4] = {st.v0.x, st.v0.y, st.v0.z, st.v0.w};
+  const uint32_t w1[4] = {st.v1.x, st.v1.y, st.v1.z, st.v1.w};
+  const uint32_t w2[4] = {st.v2.x, st.v2.y, st.v2.z, st.v2.w};
+  const uint32_t w3[4] = {st.v3.x, st.v3.y, st.v3.z, st.v3.w};
+  uint16_t* vd = svt + (mp.dg * 8) * kVStride + 4 * mp.kg;
+#pragma unroll
+  for (int d = 0; d < 8; ++d) {
+    // dim 8dg + d of keys 4kg..4kg+3: the low (even d) or high (odd d) halves of word d/2
+    const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
+    const int wi = d >> 1;
+    uint2 pk;
+    pk.x = __builtin_amdgcn_perm(w1[wi], w0[wi], sel);
+    pk.y = __builtin_amdgcn_perm(w3[wi], w2[wi], sel);
+    *reinterpret_cast<uint2*>(vd + d * kVStride) = pk;
+  }
+}
+
 template <int G>
-__global__ __launch_bounds__(256) void prefill_kernel(const PrefillArgs a) {
-  constexpr int RW = 16 * (4 / G);  // query rows per block
-  __shared__ __align__(16) uint16_t sK[kKeys * kKStride];
-  __shared__ __align__(16) uint16_t sVt[128 * kVStride];
+__global__ __launch_bounds__(kThreads) void prefill_kernel(const PrefillArgs a) {
+  constexpr int PB = 32 * (4 / G);  // positions per block
+  __shared__ __align__(16) uint16_t sK[2][kStage * kKStride];
+  __shared__ __align__(16) uint16_t sVt[2][128 * kVStride];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int lr = lane & 15, lg = lane >> 4;  // MFMA row / lane group
+  const int kh = wave >> 2, ww = wave & 3;
+  const int l32 = lane & 31, hi = lane >> 5;
   const int kvh = blockIdx.x % a.nkv;
   const int tile = a.n_qtiles - 1 - (int)(blockIdx.x / a.nkv);  // heaviest first
-  const int q0 = tile * RW;
-  const int head = kvh * G + (wave % G);
-  const int qrow = q0 + (wave / G) * 16 + lr;  // query row of this lane's scores
+  const int p0 = tile * PB;
+  const int head = kvh * G + (ww % G);
+  const int pw = p0 + 32 * (ww / G);  // this wave's first position
+  const int qrow = pw + l32;          // the query row of this lane's scores
+  const int T = a.T;
 
-  bf16x8 qb[4];
+  // Q^T operand of the eight 16-dim steps: Q[qrow][16 kk + 8 hi .. +7].
+  bf16x8 qb[8];
+  {
+    const uint16_t* qp = a.q + ((int64_t)min(qrow, T - 1) * a.nh + head) * SOLORT_HD + 8 * hi;
 #pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    uint4 v = make_uint4(0u, 0u, 0u, 0u);
-    if (qrow < a.T)
-      v = *reinterpret_cast<const uint4*>(a.q + ((int64_t)qrow * a.nh + head) * SOLORT_HD + 32 * ks + 8 * lg);
-    qb[ks] = as_bf16x8(v);
+    for (int kk = 0; kk < 8; ++kk) qb[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 16 * kk));
   }
-  f32x4 o[8];
-#pragma unroll
-  for (int dt = 0; dt < 8; ++dt) o[dt] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m = -INFINITY, lsum = 0.f;
 
   const uint16_t* kbase = a.kc + (int64_t)kvh * a.head_stride;
   const uint16_t* vbase = a.vc + (int64_t)kvh * a.head_stride;
-  const int kend = min(a.T, q0 + RW);
-  const int kg = tid >> 4, dg = tid & 15;  // V^T staging: 4 keys x 8 dims per thread
+  const int kend = min(T, p0 + PB);    // keys the block reads
+  const int kend_w = min(T, pw + 32);  // keys this wave attends (wave-uniform)
+  const int nit = (kend + kStage - 1) / kStage;
+  const StageMap mp = {tid >> 4, tid & 15, tid & 31, tid >> 5};
 
-  // Global loads of a block's K rows (4 chunks of 16 B per thread) and V rows
-  // (4 keys x 8 dims per thread); rows at or past T read as zero.
-  uint4 kv[4], vv[4];
-  auto fetch = [&](int kb) {
+  f32x16 o[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i, r = c >> 4, ch = c & 15;
-      kv[i] = (kb + r < a.T) ? *reinterpret_cast<const uint4*>(kbase + (int64_t)(kb + r) * a.tok_stride + ch * 8)
-                             : make_uint4(0u, 0u, 0u, 0u);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int r = 4 * kg + i;
-      vv[i] = (kb + r < a.T) ? *reinterpret_cast<const uint4*>(vbase + (int64_t)(kb + r) * a.tok_stride + dg * 8)
-                             : make_uint4(0u, 0u, 0u, 0u);
-    }
-  };
-  fetch(0);
+  for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
+  float m = -INFINITY, lsum = 0.f;  // running max of raw scores; this lane's share of the row sum
+  const float qs = a.qscale;
 
-  for (int k0 = 0; k0 < kend; k0 += kKeys) {
-    // Stage the fetched block: K [64][128] row-major, V^T [128][64].
-    __syncthreads();  // the previous block's tiles are no longer read
+  // The next staged block's global loads fly while this one is computed.
+  Staged st = prefill_fetch(kbase, vbase, a.tok_stride, T, 0, mp);
+  prefill_stage(st, sK[0], sVt[0], mp);
+  __syncthreads();
+  if (nit > 1) st = prefill_fetch(kbase, vbase, a.tok_stride, T, kStage, mp);
+
+  for (int j = 0; j < nit; ++j) {
+    const int buf = j & 1;
+    const int k0 = j * kStage + kh * kKeys;  // this half's 64 keys
+    if (k0 < kend_w) {  // wave-uniform
+      // S^T for the 64 keys: s[kt][i] = score of key k0 + 32kt + 8(i/4) + 4hi + i%4.
+      f32x16 s[2] = {f32x16{}, f32x16{}};
+      const uint16_t* kr = &sK[buf][(kh * kKeys + l32) * kKStride + 8 * hi];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = tid + 256 * i, r = c >> 4, ch = c & 15;
-      *reinterpret_cast<uint4*>(sK + r * kKStride + ch * 8) = kv[i];
-    }
-    {
-      const uint32_t* w0 = reinterpret_cast<const uint32_t*>(&vv[0]);
-      const uint32_t* w1 = reinterpret_cast<const uint32_t*>(&vv[1]);
-      const uint32_t* w2 = reinterpret_cast<const uint32_t*>(&vv[2]);
-      const uint32_t* w3 = reinterpret_cast<const uint32_t*>(&vv[3]);
+      for (int kk = 0; kk < 8; ++kk)
 #pragma unroll
-      for (int d = 0; d < 8; ++d) {
-        const int sh = (d & 1) * 16, wi = d >> 1;
-        uint2 pk;
-        pk.x = ((w0[wi] >> sh) & 0xffffu) | (((w1[wi] >> sh) & 0xffffu) << 16);
-        pk.y = ((w2[wi] >> sh) & 0xffffu) | (((w3[wi] >> sh) & 0xffffu) << 16);
-        *reinterpret_cast<uint2*>(sVt + (dg * 8 + d) * kVStride + 4 * kg) = pk;
+        for (int kt = 0; kt < 2; ++kt) {  // two independent accumulation chains
+          const bf16x8 ka = as_bf16x8(*reinterpret_cast<const uint4*>(kr + kt * 32 * kKStride + 16 * kk));
+          s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qb[kk], s[kt], 0, 0, 0);
+        }
+      if (k0 + kKeys - 1 > pw) {  // the block crosses this wave's diagonal: mask keys past each row
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int key = k0 + 32 * kt + 8 * (i >> 2) + 4 * hi + (i & 3);
+            if (key > qrow) s[kt][i] = -INFINITY;
+          }
       }
+      float mx = s[0][0];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
+      mx = xor32_combine(mx, [](float x, float y) { return fmaxf(x, y); });
+      // Finite for half 0 (key 0 is visible to every row); in half 1 a row
+      // whose keys here are all masked keeps m = -inf and p = 0.
+      const float mn = fmaxf(m, mx);
+      const float mq = mn == -INFINITY ? 0.f : mn * qs;
+      const float alpha = fast_exp2(m * qs - mq);  // m = -inf gives 0
+      float ps = 0.f;
+      uint32_t pk[2][8];  // bf16 pairs of p: [kt][i / 2]
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int i = 0; i < 16; i += 2) {
+          const float e0 = fast_exp2(fmaf(s[kt][i], qs, -mq));
+          const float e1 = fast_exp2(fmaf(s[kt][i + 1], qs, -mq));
+          ps += e0 + e1;
+          pk[kt][i >> 1] = pack2(e0, e1);
+        }
+      lsum = fmaf(lsum, alpha, ps);
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // some row's maximum moved
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+      }
+      m = mn;
+      // O^T += V^T P^T: key step (kt, h) covers keys k0 + 32kt + 16h + {4hi + 0..3, 8 + 4hi + 0..3}.
+      const uint16_t* vb = &sVt[buf][l32 * kVStride + kh * kKeys + 4 * hi];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          const bf16x8 pb = as_bf16x8(make_uint4(pk[kt][4 * h], pk[kt][4 * h + 1], pk[kt][4 * h + 2],
+                                                 pk[kt][4 * h + 3]));
+#pragma unroll
+          for (int dt = 0; dt < 4; ++dt) {
+            const uint16_t* vr = vb + dt * 32 * kVStride + 32 * kt + 16 * h;
+            const uint2 lo = *reinterpret_cast<const uint2*>(vr);
+            const uint2 up = *reinterpret_cast<const uint2*>(vr + 8);
+            const bf16x8 va = as_bf16x8(make_uint4(lo.x, lo.y, up.x, up.y));
+            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, o[dt], 0, 0, 0);
+          }
+        }
     }
+    if (j + 1 < nit)  // buffer (j+1)%2 was last read before the previous barrier
+      prefill_stage(st, sK[(j + 1) & 1], sVt[(j + 1) & 1], mp);
     __syncthreads();
-    // The next block's global loads fly while this block is computed.
-    if (k0 + kKeys < kend) fetch(k0 + kKeys);
-
-    // S^T = K Q^T for the block's 64 keys.
-    f32x4 s[4];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) {
-        const bf16x8 ka = as_bf16x8(*reinterpret_cast<const uint4*>(sK + (kt * 16 + lr) * kKStride + 32 * ks + 8 * lg));
-        s[kt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[ks], s[kt], 0, 0, 0);
-      }
-    }
-    // Scale, causal mask, online softmax for row qrow.
-    float mx = -INFINITY;
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int key = k0 + kt * 16 + 4 * lg + i;
-        float v = s[kt][i] * a.qscale;
-        if (key > qrow || key >= a.T) v = -INFINITY;
-        s[kt][i] = v;
-        mx = fmaxf(mx, v);
-      }
-    mx = fmaxf(mx, xshfl(mx, 16));
-    mx = fmaxf(mx, xshfl(mx, 32));
-    const float mn = fmaxf(m, mx);
-    const bool live = mn != -INFINITY;
-    const float alpha = live ? fast_exp2(m - mn) : 1.f;
-    float ps = 0.f;
-    uint32_t pw[4][2];
-#pragma unroll
-    for (int kt = 0; kt < 4; ++kt) {
-      float p[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        p[i] = live ? fast_exp2(s[kt][i] - mn) : 0.f;
-        ps += p[i];
-      }
-      pw[kt][0] = f2bf(p[0]) | (f2bf(p[1]) << 16);
-      pw[kt][1] = f2bf(p[2]) | (f2bf(p[3]) << 16);
-    }
-    lsum = lsum * alpha + ps;
-    m = mn;
-#pragma unroll
-    for (int dt = 0; dt < 8; ++dt) o[dt] *= alpha;
-
-    // O^T += V^T P^T over the block's two 32-key halves.
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const bf16x8 pb = as_bf16x8(make_uint4(pw[2 * c][0], pw[2 * c][1], pw[2 * c + 1][0], pw[2 * c + 1][1]));
-#pragma unroll
-      for (int dt = 0; dt < 8; ++dt) {
-        const uint16_t* vrow = sVt + (dt * 16 + lr) * kVStride + 32 * c + 4 * lg;
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + 16);
-        const bf16x8 va = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-        o[dt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, o[dt], 0, 0, 0);
-      }
-    }
+    if (j + 2 < nit) st = prefill_fetch(kbase, vbase, a.tok_stride, T, (j + 2) * kStage, mp);
   }
 
-  float lt = lsum + xshfl(lsum, 16);
-  lt += xshfl(lt, 32);
-  const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  if (qrow < a.T) {
-    const int64_t base = ((int64_t)qrow * a.nh + head) * SOLORT_HD + 4 * lg;
+  // Merge the two key halves of every row: half 1 hands (m, l, O) to half 0
+  // through LDS (the staging buffers are free after the last barrier).
+  float* xf = reinterpret_cast<float*>(&sK[0][0]) + ww * (66 * 64);  // [66][64] floats per wave pair
+  if (kh == 1) {
 #pragma unroll
-    for (int dt = 0; dt < 8; ++dt) {
-      const float4 v = make_float4(o[dt][0] * inv, o[dt][1] * inv, o[dt][2] * inv, o[dt][3] * inv);
-      if (a.out_f32) {
-        *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + base + dt * 16) = v;
-      } else {
-        uint2 pk;
-        pk.x = f2bf(v.x) | (f2bf(v.y) << 16);
-        pk.y = f2bf(v.z) | (f2bf(v.w) << 16);
-        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.out) + base + dt * 16) = pk;
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) xf[(dt * 16 + i) * 64 + lane] = o[dt][i];
+    xf[64 * 64 + lane] = m;
+    xf[65 * 64 + lane] = lsum;
+  }
+  __syncthreads();
+  if (kh == 1) return;
+  {
+    const float m1 = xf[64 * 64 + lane], l1 = xf[65 * 64 + lane];
+    const float mt = fmaxf(m, m1);  // finite: half 0 saw key 0
+    const float a0 = fast_exp2((m - mt) * qs), a1 = fast_exp2((m1 - mt) * qs);  // m1 = -inf gives 0
+    lsum = fmaf(lsum, a0, l1 * a1);
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) o[dt][i] = fmaf(o[dt][i], a0, xf[(dt * 16 + i) * 64 + lane] * a1);
+  }
+
+  const float lt = xor32_combine(lsum, [](float x, float y) { return x + y; });  // both halves of the row
+  const float inv = lt > 0.f ? 1.f / lt : 0.f;
+  if (qrow < T) {
+    const int64_t base = ((int64_t)qrow * a.nh + head) * SOLORT_HD + 4 * hi;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const float4 v = make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
+                                     o[dt][4 * g + 3] * inv);
+        const int64_t oi = base + 32 * dt + 8 * g;
+        if (a.out_f32) {
+          *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + oi) = v;
+        } else {
+          uint2 pkd;
+          pkd.x = pack2(v.x, v.y);
+          pkd.y = pack2(v.z, v.w);
+          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.out) + oi) = pkd;
+        }
       }
-    }
   }
 }
 
@@ -243,15 +333,15 @@ extern "C" int solort_prefill_attn(const void* q, int T, int nh, int nkv, int hd
   a.nh = nh;
   a.nkv = nkv;
   a.out_f32 = out_dtype == SOLORT_DTYPE_F32;
-  const int rw = 16 * (4 / G);
-  a.n_qtiles = (T + rw - 1) / rw;
+  const int pb = 32 * (4 / G);  // positions per block
+  a.n_qtiles = (T + pb - 1) / pb;
   const int64_t blocks = (int64_t)a.n_qtiles * nkv;
   if (blocks > 0x7fffffff) return set_error(SOLORT_EINVAL, "%s: too many tiles", name);
   hipStream_t s = (hipStream_t)stream;
   switch (G) {
-    case 1: hipLaunchKernelGGL(prefill_kernel<1>, dim3((unsigned)blocks), dim3(256), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(prefill_kernel<2>, dim3((unsigned)blocks), dim3(256), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(prefill_kernel<4>, dim3((unsigned)blocks), dim3(256), 0, s, a); break;
+    case 1: hipLaunchKernelGGL(prefill_kernel<1>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a); break;
+    case 2: hipLaunchKernelGGL(prefill_kernel<2>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a); break;
+    case 4: hipLaunchKernelGGL(prefill_kernel<4>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a); break;
   }
   return check_launch(name);
 }
