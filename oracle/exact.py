@@ -142,12 +142,14 @@ def splitkv_combine(q: np.ndarray, keys: np.ndarray, vals: np.ndarray, scale: fl
 
 
 def prefill_blockwise(q: np.ndarray, keys: np.ndarray, vals: np.ndarray, scale: float, block: int = 64,
-                      splits: int = 2) -> np.ndarray:
+                      splits: int = 2, lazy: float = 8.0) -> np.ndarray:
     """Causal attention of q [T,hd] (row t at position t) over keys/vals [T,hd] as the prefill kernel
-    evaluates it: the 64-key blocks are dealt round-robin to `splits` independent passes (block b to
-    pass b % splits); each pass keeps its own running max M (log2 units) and, per block, takes
-    p = bf16(2^(s - M)), l += sum of the unrounded p, o = o * 2^(M_old - M) + p_bf16 @ V; the passes
-    are then merged by log-sum-exp.  fp64 except the bf16 rounding of p."""
+    evaluates it.  The 64-key blocks are dealt round-robin to `splits` independent passes (block b to
+    pass b % splits).  Each pass keeps, per row, a reference max M (log2 units) that moves to the
+    block's max only when that exceeds M by more than `lazy` (the first visible block always sets
+    it); per block p = bf16(2^(s - M)), l = l * 2^(M_old - M) + sum(p_bf16),
+    o = o * 2^(M_old - M) + p_bf16 @ V.  The passes are merged by log-sum-exp.  fp64 except the bf16
+    rounding of p."""
     q = np.asarray(q, np.float64)
     T = q.shape[0]
     z = (q @ np.asarray(keys, np.float64).T) * scale * np.log2(np.e)
@@ -160,21 +162,23 @@ def prefill_blockwise(q: np.ndarray, keys: np.ndarray, vals: np.ndarray, scale: 
         o = np.zeros_like(q)
         for k0 in range(sp * block, T, splits * block):
             zb = z[:, k0:k0 + block]
-            mn = np.maximum(m, zb.max(axis=1))
-            live = np.isfinite(mn)
-            with np.errstate(invalid="ignore"):  # -inf - -inf in rows not yet live; masked by `live`
-                alpha = np.where(live, np.exp2(np.where(live, m - mn, 0.0)), 1.0)
-            p = np.where(live[:, None], np.exp2(zb - np.where(live, mn, 0.0)[:, None]), 0.0)
+            mx = zb.max(axis=1)
+            with np.errstate(invalid="ignore"):  # -inf - -inf in rows with no visible key yet
+                bump = mx > m + lazy
+                mn = np.where(bump, mx, m)
+                live = np.isfinite(mn)
+                alpha = np.where(bump & np.isfinite(m), np.exp2(np.where(bump & np.isfinite(m), m - mn, 0.0)), 1.0)
+                p = np.where(live[:, None], np.exp2(zb - np.where(live, mn, 0.0)[:, None]), 0.0)
             pb = np.asarray(bf16_round(p), np.float64)
-            l = l * alpha + p.sum(axis=1)
+            l = l * alpha + pb.sum(axis=1)
             o = o * alpha[:, None] + pb @ vals[k0:k0 + block]
             m = mn
         parts.append((m, l, o))
     mt = np.max(np.stack([m for m, _, _ in parts]), axis=0)  # finite: pass 0 holds key 0
-    l = sum(np.where(np.isfinite(m), np.exp2(np.where(np.isfinite(m), m - mt, 0.0)), 0.0) * lp
-            for m, lp, _ in parts)
-    o = sum(np.where(np.isfinite(m), np.exp2(np.where(np.isfinite(m), m - mt, 0.0)), 0.0)[:, None] * op
-            for m, _, op in parts)
+    with np.errstate(invalid="ignore"):
+        w = [np.where(np.isfinite(m), np.exp2(np.where(np.isfinite(m), m - mt, 0.0)), 0.0) for m, _, _ in parts]
+    l = sum(wi * lp for wi, (_, lp, _) in zip(w, parts))
+    o = sum(wi[:, None] * op for wi, (_, _, op) in zip(w, parts))
     return o / l[:, None]
 
 

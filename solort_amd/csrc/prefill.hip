@@ -10,18 +10,21 @@
 // Block = 8 wavefronts = one KV head x 32 * (4 / g) positions.  Wave w
 // belongs to key half kh = w / 4 and owns query head kvh*g + (w%4)%g at
 // positions p0 + 32*((w%4)/g) .. +31 (32 query rows).  Each iteration stages
-// 128 keys (K row-major and V transposed, in LDS, double buffered; the next
-// iteration's global loads fly during this one's math); half kh takes the
-// iteration's 64-key block kh, so two waves share each SIMD and hide each
-// other's latencies, and the two halves of every row merge through LDS at the
-// end.  Per 64-key block:
+// 128 keys of K and V, both row-major, in LDS (double buffered; the next
+// iteration's buffer loads fly during this one's math and barriers order only
+// LDS); half kh takes the iteration's 64-key block kh, so two waves share each
+// SIMD, and the two halves of every row merge through LDS at the end.  Per
+// 64-key block:
 //   S^T = K Q^T   v_mfma_f32_32x32x16_bf16, A = K (LDS, one 16-byte read per
 //                 operand), B = Q^T (registers), 2 key tiles x 8 dim steps
-//   online softmax in fp32 (max over raw scores, p = 2^(s*c - m*c) with
-//                 c = scale*log2(e)), P rounded to bf16, O rescaled only
-//                 when some row's maximum moved
-//   O^T += V^T P^T  A = V^T (LDS), B = P^T straight from the S^T registers,
-//                 4 dim tiles x 4 key steps
+//   online softmax in fp32 with a lazy maximum: a row's reference max moves
+//                 only when a block's max exceeds it by more than 8 (log2
+//                 units), so p = 2^(s*c - m*c) <= 2^8 (c = scale*log2(e))
+//                 and O is rarely rescaled; P is rounded to bf16 and the row
+//                 sum adds the rounded P (v_dot2_f32_bf16)
+//   O^T += V^T P^T  A = V^T from the row-major V tile by ds_read_b64_tr_b16,
+//                 B = P^T straight from the S^T registers, 4 dim tiles x 4
+//                 key steps
 // MFMA operand layouts (checked on gfx950): A[m][k] lane l holds
 // A[l%32][8(l/32)+s]; B[k][n] lane l holds B[8(l/32)+s][l%32]; D[m][n] lane
 // l, register i holds D[8(i/4)+4(l/32)+i%4][l%32].  With S^T and O^T a lane
@@ -56,86 +59,76 @@ struct PrefillArgs {
 constexpr int kThreads = 512;      // 8 wavefronts
 constexpr int kKeys = 64;          // keys per wave per iteration
 constexpr int kStage = 2 * kKeys;  // keys staged per iteration
-constexpr int kKStride = 128 + 8;      // K tile row stride (bf16): 272 B, conflict-free 16-byte reads
-constexpr int kVStride = kStage + 4;   // V^T tile row stride (bf16): 264 B, conflict-free 8-byte reads
+constexpr int kKStride = 128 + 8;   // K tile row stride (bf16): 272 B, conflict-free 16-byte reads
+constexpr int kVStride = 128 + 16;  // V tile row stride (bf16): 288 B, conflict-free transposing reads
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
-// One staged block of 128 keys in flight in registers: per thread 4 K chunks
-// (key rows r0 + 32i, dims 8ch..8ch+7) and 4 V chunks (keys 4kg..4kg+3,
-// dims 8dg..8dg+7), 16 bytes each.
+// One staged block of 128 keys in flight in registers: per thread 4 K and 4
+// V chunks of 16 bytes, key rows r0 + 32 i, dims 8 ch .. 8 ch + 7.
 struct Staged {
   uint4 k0, k1, k2, k3, v0, v1, v2, v3;
 };
 
-// Per-thread staging geometry: K chunk (row r0 + 32 i, 16-byte column ch),
-// V chunk (keys 4kg..4kg+3, dims 8dg..8dg+7); kg varies fastest across lanes
-// so the 16 lanes of one LDS write cycle of V^T hit distinct banks.
-struct StageMap {
-  int r0, ch, kg, dg;
-};
+// Buffer resource over one KV head's rows 0..T-1 (byte offsets
+// [0, ((T-1) * tok_stride + 128) * 2)); loads past it return zeros, which is
+// what the rows at or past T must contribute (the causal mask gives them
+// weight 0 in every row < T).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t kv_rsrc(const uint16_t* base, int T, int64_t ts) {
+  const int nbytes = (int)(((int64_t)(T - 1) * ts + SOLORT_HD) * 2);
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(base), (short)0, nbytes, 0x00020000);
+}
 
-// Global loads of the staged block starting at key kb.  Keys at or past T
-// re-read row T-1 (finite values to which the causal mask gives weight 0 in
-// every row < T); a block entirely below T takes the unclamped path.
-__device__ __forceinline__ Staged prefill_fetch(const uint16_t* kbase, const uint16_t* vbase, int64_t ts, int T,
-                                                int kb, const StageMap& mp) {
+__device__ __forceinline__ uint4 bload16(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+}
+
+// Global loads of the staged block whose first key sits at byte offset soff:
+// voff[i] is this thread's byte offset of key row r0 + 32 i, dims 8ch...
+__device__ __forceinline__ Staged prefill_fetch(__amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr,
+                                                const int (&voff)[4], int soff) {
   Staged st;
-  if (kb + kStage <= T) {  // block-uniform
-    const uint16_t* kp = kbase + (int64_t)(kb + mp.r0) * ts + mp.ch * 8;
-    const uint16_t* vp = vbase + (int64_t)(kb + 4 * mp.kg) * ts + mp.dg * 8;
-    const int64_t k32 = 32 * ts;
-    st.k0 = *reinterpret_cast<const uint4*>(kp);
-    st.k1 = *reinterpret_cast<const uint4*>(kp + k32);
-    st.k2 = *reinterpret_cast<const uint4*>(kp + 2 * k32);
-    st.k3 = *reinterpret_cast<const uint4*>(kp + 3 * k32);
-    st.v0 = *reinterpret_cast<const uint4*>(vp);
-    st.v1 = *reinterpret_cast<const uint4*>(vp + ts);
-    st.v2 = *reinterpret_cast<const uint4*>(vp + 2 * ts);
-    st.v3 = *reinterpret_cast<const uint4*>(vp + 3 * ts);
-  } else {
-    auto kld = [&](int i) {
-      return *reinterpret_cast<const uint4*>(kbase + (int64_t)min(kb + mp.r0 + 32 * i, T - 1) * ts + mp.ch * 8);
-    };
-    auto vld = [&](int i) {
-      return *reinterpret_cast<const uint4*>(vbase + (int64_t)min(kb + 4 * mp.kg + i, T - 1) * ts + mp.dg * 8);
-    };
-    st.k0 = kld(0); st.k1 = kld(1); st.k2 = kld(2); st.k3 = kld(3);
-    st.v0 = vld(0); st.v1 = vld(1); st.v2 = vld(2); st.v3 = vld(3);
-  }
+  st.k0 = bload16(kr, voff[0], soff);
+  st.k1 = bload16(kr, voff[1], soff);
+  st.k2 = bload16(kr, voff[2], soff);
+  st.k3 = bload16(kr, voff[3], soff);
+  st.v0 = bload16(vr, voff[0], soff);
+  st.v1 = bload16(vr, voff[1], soff);
+  st.v2 = bload16(vr, voff[2], soff);
+  st.v3 = bload16(vr, voff[3], soff);
   return st;
 }
 
-// Registers -> one LDS buffer: K as [key][dim], V transposed to [dim][key]
-// (one byte permute per output word).
-__device__ __forceinline__ void prefill_stage(const Staged& st, uint16_t* sk, uint16_t* svt, const StageMap& mp) {
-  uint16_t* kd = sk + mp.r0 * kKStride + mp.ch * 8;
+// Registers -> one LDS buffer: K and V both as [key][dim].
+__device__ __forceinline__ void prefill_stage(const Staged& st, uint16_t* sk, uint16_t* sv, int r0, int ch) {
+  uint16_t* kd = sk + r0 * kKStride + ch * 8;
   *reinterpret_cast<uint4*>(kd) = st.k0;
   *reinterpret_cast<uint4*>(kd + 32 * kKStride) = st.k1;
   *reinterpret_cast<uint4*>(kd + 64 * kKStride) = st.k2;
   *reinterpret_cast<uint4*>(kd + 96 * kKStride) = st.k3;
-  const uint32_t w0[4] = {st.v0.x, st.v0.y, st.v0.z, st.v0.w};
-  const uint32_t w1[4] = {st.v1.x, st.v1.y, st.v1.z, st.v1.w};
-  const uint32_t w2[4] = {st.v2.x, st.v2.y, st.v2.z, st.v2.w};
-  const uint32_t w3[4] = {st.v3.x, st.v3.y, st.v3.z, st.v3.w};
-  uint16_t* vd = svt + (mp.dg * 8) * kVStride + 4 * mp.kg;
-#pragma unroll
-  for (int d = 0; d < 8; ++d) {
-    // dim 8dg + d of keys 4kg..4kg+3: the low (even d) or high (odd d) halves of word d/2
-    const uint32_t sel = (d & 1) ? 0x07060302u : 0x05040100u;
-    const int wi = d >> 1;
-    uint2 pk;
-    pk.x = __builtin_amdgcn_perm(w1[wi], w0[wi], sel);
-    pk.y = __builtin_amdgcn_perm(w3[wi], w2[wi], sel);
-    *reinterpret_cast<uint2*>(vd + d * kVStride) = pk;
-  }
+  uint16_t* vd = sv + r0 * kVStride + ch * 8;
+  *reinterpret_cast<uint4*>(vd) = st.v0;
+  *reinterpret_cast<uint4*>(vd + 32 * kVStride) = st.v1;
+  *reinterpret_cast<uint4*>(vd + 64 * kVStride) = st.v2;
+  *reinterpret_cast<uint4*>(vd + 96 * kVStride) = st.v3;
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives in slot k
+// element i % 4 of the 8 bytes addressed by lane 4k + i / 4 of the group.
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4*)(__attribute__((address_space(3))) uint16_t*)(p));
+  return __builtin_bit_cast(uint2, v);
 }
 
 template <int G>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(const PrefillArgs a) {
   constexpr int PB = 32 * (4 / G);  // positions per block
   __shared__ __align__(16) uint16_t sK[2][kStage * kKStride];
-  __shared__ __align__(16) uint16_t sVt[2][128 * kVStride];
+  __shared__ __align__(16) uint16_t sV[2][kStage * kVStride];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kh = wave >> 2, ww = wave & 3;
@@ -161,7 +154,12 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const PrefillArgs a) 
   const int kend = min(T, p0 + PB);    // keys the block reads
   const int kend_w = min(T, pw + 32);  // keys this wave attends (wave-uniform)
   const int nit = (kend + kStage - 1) / kStage;
-  const StageMap mp = {tid >> 4, tid & 15, tid & 31, tid >> 5};
+  const int r0 = tid >> 4, ch = tid & 15;  // staging: key rows r0 + 32i, dims 8ch..8ch+7
+  const __amdgpu_buffer_rsrc_t krs = kv_rsrc(kbase, T, a.tok_stride), vrs = kv_rsrc(vbase, T, a.tok_stride);
+  const int ts2 = (int)a.tok_stride * 2;  // bytes per key row
+  int voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) voff[i] = (r0 + 32 * i) * ts2 + ch * 16;
 
   f32x16 o[4];
 #pragma unroll
@@ -169,11 +167,17 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const PrefillArgs a) 
   float m = -INFINITY, lsum = 0.f;  // running max of raw scores; this lane's share of the row sum
   const float qs = a.qscale;
 
-  // The next staged block's global loads fly while this one is computed.
-  Staged st = prefill_fetch(kbase, vbase, a.tok_stride, T, 0, mp);
-  prefill_stage(st, sK[0], sVt[0], mp);
-  __syncthreads();
-  if (nit > 1) st = prefill_fetch(kbase, vbase, a.tok_stride, T, kStage, mp);
+  // The next staged block's loads fly while this one is computed.  Fetches
+  // past the last block are issued anyway (buffer loads beyond the head's
+  // rows return zeros), so every fetch and stage is unconditional and each
+  // stage waits only for the loads it consumes.
+  Staged st = prefill_fetch(krs, vrs, voff, 0);
+  prefill_stage(st, sK[0], sV[0], r0, ch);
+  // Every load issued so far (q and block 0) is complete past this point, so
+  // the loop's waits count only the staged block in flight.
+  __builtin_amdgcn_s_waitcnt(0);
+  lds_barrier();
+  st = prefill_fetch(krs, vrs, voff, kStage * ts2);
 
   for (int j = 0; j < nit; ++j) {
     const int buf = j & 1;
@@ -204,50 +208,60 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const PrefillArgs a) 
 #pragma unroll
         for (int i = 0; i < 16; ++i) mx = fmaxf(mx, s[kt][i]);
       mx = xor32_combine(mx, [](float x, float y) { return fmaxf(x, y); });
-      // Finite for half 0 (key 0 is visible to every row); in half 1 a row
-      // whose keys here are all masked keeps m = -inf and p = 0.
-      const float mn = fmaxf(m, mx);
+      // Lazy maximum: a row keeps the reference max m it last rescaled to
+      // until a block's max exceeds it by more than 8 (log2 units), so p <= 2^8
+      // and O is rescaled only on those rare steps.  Before its first visible
+      // key a row has m = -inf and O = 0, l = 0, so it takes the block's max
+      // without rescaling.  A block whose keys are all masked for a row
+      // (mx = -inf) changes nothing.
+      const bool bump = mx * qs > m * qs + 8.f;
+      const float mn = bump ? mx : m;
       const float mq = mn == -INFINITY ? 0.f : mn * qs;
-      const float alpha = fast_exp2(m * qs - mq);  // m = -inf gives 0
+      const float alpha = (bump && m != -INFINITY) ? fast_exp2(m * qs - mq) : 1.f;
+      // p in bf16 pairs; the row sum adds the rounded p that weigh V.
       float ps = 0.f;
       uint32_t pk[2][8];  // bf16 pairs of p: [kt][i / 2]
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int i = 0; i < 16; i += 2) {
-          const float e0 = fast_exp2(fmaf(s[kt][i], qs, -mq));
-          const float e1 = fast_exp2(fmaf(s[kt][i + 1], qs, -mq));
-          ps += e0 + e1;
-          pk[kt][i >> 1] = pack2(e0, e1);
+          const uint32_t pr = pack2(fast_exp2(fmaf(s[kt][i], qs, -mq)), fast_exp2(fmaf(s[kt][i + 1], qs, -mq)));
+          pk[kt][i >> 1] = pr;
+          ps = dot2bf(pr, 0x3f803f80u, ps);  // + p_lo + p_hi
         }
       lsum = fmaf(lsum, alpha, ps);
-      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // some row's maximum moved
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // some row's reference max moved
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
       }
       m = mn;
-      // O^T += V^T P^T: key step (kt, h) covers keys k0 + 32kt + 16h + {4hi + 0..3, 8 + 4hi + 0..3}.
-      const uint16_t* vb = &sVt[buf][l32 * kVStride + kh * kKeys + 4 * hi];
+    // O^T += V^T P^T: key step (kt, h) covers keys k0 + 32kt + 16h + {4hi + 0..3, 8 + 4hi + 0..3}.
+    // The V^T operand comes from the row-major V tile by transposing reads:
+    // lane 16G + jj addresses key row 4(G/2) + jj/4 (+8 for the upper four
+    // keys) at dims 16(G%2) + 4(jj%4), so lane l receives dim l%32 of the
+    // four keys its P^T slots hold.
+    const uint16_t* vb = &sV[buf][(kh * kKeys + 4 * hi + ((lane & 15) >> 2)) * kVStride +
+                                  16 * ((lane >> 4) & 1) + 4 * (lane & 3)];
 #pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
+    for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-          const bf16x8 pb = as_bf16x8(make_uint4(pk[kt][4 * h], pk[kt][4 * h + 1], pk[kt][4 * h + 2],
-                                                 pk[kt][4 * h + 3]));
+      for (int h = 0; h < 2; ++h) {
+        const bf16x8 pb = as_bf16x8(make_uint4(pk[kt][4 * h], pk[kt][4 * h + 1], pk[kt][4 * h + 2],
+                                               pk[kt][4 * h + 3]));
 #pragma unroll
-          for (int dt = 0; dt < 4; ++dt) {
-            const uint16_t* vr = vb + dt * 32 * kVStride + 32 * kt + 16 * h;
-            const uint2 lo = *reinterpret_cast<const uint2*>(vr);
-            const uint2 up = *reinterpret_cast<const uint2*>(vr + 8);
-            const bf16x8 va = as_bf16x8(make_uint4(lo.x, lo.y, up.x, up.y));
-            o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, o[dt], 0, 0, 0);
-          }
+        for (int dt = 0; dt < 4; ++dt) {
+          const uint16_t* vr = vb + (32 * kt + 16 * h) * kVStride + 32 * dt;
+          const uint2 lo = lds_read_tr16(vr);
+          const uint2 up = lds_read_tr16(vr + 8 * kVStride);
+          const bf16x8 va = as_bf16x8(make_uint4(lo.x, lo.y, up.x, up.y));
+          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, o[dt], 0, 0, 0);
         }
-    }
-    if (j + 1 < nit)  // buffer (j+1)%2 was last read before the previous barrier
-      prefill_stage(st, sK[(j + 1) & 1], sVt[(j + 1) & 1], mp);
-    __syncthreads();
-    if (j + 2 < nit) st = prefill_fetch(kbase, vbase, a.tok_stride, T, (j + 2) * kStage, mp);
+      }
+  }
+    // buffer (j+1)%2 was last read before the previous barrier
+    prefill_stage(st, sK[(j + 1) & 1], sV[(j + 1) & 1], r0, ch);
+    lds_barrier();  // orders the LDS tiles only: the loads below stay in flight
+    st = prefill_fetch(krs, vrs, voff, (j + 2) * kStage * ts2);
   }
 
   // Merge the two key halves of every row: half 1 hands (m, l, O) to half 0
@@ -321,6 +335,11 @@ extern "C" int solort_prefill_attn(const void* q, int T, int nh, int nkv, int hd
   if (out_dtype != SOLORT_DTYPE_BF16 && out_dtype != SOLORT_DTYPE_F32)
     return set_error(SOLORT_EINVAL, "%s: out_dtype %d", name, out_dtype);
   if (T == 0) return 0;
+  // K/V rows are addressed with 32-bit byte offsets from the head's row 0, up
+  // to two staged blocks past T.
+  if (((int64_t)T + 4 * kStage) * kv_tok_stride * 2 >= ((int64_t)1 << 31))
+    return set_error(SOLORT_EINVAL, "%s: T=%d rows of stride %lld exceed 32-bit byte offsets", name, T,
+                     (long long)kv_tok_stride);
   PrefillArgs a;
   a.q = (const uint16_t*)q;
   a.kc = (const uint16_t*)k_cache;

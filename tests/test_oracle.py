@@ -297,11 +297,17 @@ def test_prefill_blockwise_equals_exact_without_rounding_and_close_with_it():
     orig = exact.bf16_round
     try:
         exact.bf16_round = lambda x: np.asarray(x, np.float64)
-        got = [exact.prefill_blockwise(q, k, v, SCALE, splits=sp) for sp in (1, 2, 3)]
+        got = [exact.prefill_blockwise(q, k, v, SCALE, splits=sp, lazy=lz) for sp in (1, 2, 3) for lz in (0.0, 8.0)]
+        # keys x8 (scores far above the lazy threshold) still merge back to exact attention
+        k8 = k.copy()
+        k8[::7] *= 8.0
+        want8 = exact.causal_decode_fp64(q[:, None, :], k8[:, None, :], v[:, None, :], 0, SCALE)[:, 0]
+        got8 = exact.prefill_blockwise(q, k8, v, SCALE)
     finally:
         exact.bf16_round = orig
-    for g_sp in got:  # any number of interleaved passes merges back to exact attention
+    for g_sp in got:  # any number of interleaved passes and any lazy threshold give exact attention
         assert np.allclose(g_sp, want, atol=1e-12)
+    assert np.allclose(got8, want8, atol=1e-10)
     got_b = exact.prefill_blockwise(q, k, v, SCALE)
     err = np.abs(got_b - want)
     assert err.max() < 2e-2 and err.mean() < 2e-3
