@@ -256,7 +256,7 @@ def long_decode_extras(torch, ops, wl, dev, n_caches: int = 8) -> dict:
     res = {"workload": "Qwen3-8B decode attention, batch 1, 32q/8kv heads, KV live 32768 (bucket 32768), "
                        f"{n_caches} rotated layer caches", "algorithmic_bytes": kbytes, "by_n_split": {}}
     best = None
-    for ns in (128, 256, 512):
+    for ns in (32, 64, 128, 256):
         ws = ops.attn_workspace(1, sh.nh, sh.nkv, ns, dev)
         calls = [(lambda i=i, ws=ws, ns=ns: ops.decode_layer(qkv[i], w[0], w[1], wl.EPS, cs, posb, kcs[i], vcs[i],
                                                              L, sh.scale, ws, ns, out, sh.nh, sh.nkv))
@@ -292,20 +292,25 @@ def verify_extras(torch, ops, wl, runners, dev, sh) -> dict:
     r0 = runners[0]
     cs = ops.rope_rows(r0.inv_freq, posb, K1)
     ns = verify_splits(bound)
-    ws = ops.attn_workspace(K1, sh.nh, sh.nkv, ns, dev)
     out = torch.empty(K1, sh.nh * 128, dtype=torch.bfloat16, device=dev)
-    calls = [(lambda kc=kc, vc=vc, li=li: ops.decode_layer(qkv[li], r0.qn_w[li], r0.kn_w[li], r0.eps, cs, posb,
-                                                           kc[li], vc[li], bound, sh.scale, ws, ns, out, sh.nh,
-                                                           sh.nkv))
-             for kc, vc in sets for li in range(sh.layers)]
-    us = _graph_us(torch, dev, calls, reps=3)
     vbytes = 2 * sh.nkv * (pos0 + K1) * 128 * 2 + K1 * 2 * sh.nh * 128 * 2
+
+    def time_splits(n):
+        ws = ops.attn_workspace(K1, sh.nh, sh.nkv, n, dev)
+        calls = [(lambda kc=kc, vc=vc, li=li: ops.decode_layer(qkv[li], r0.qn_w[li], r0.kn_w[li], r0.eps, cs, posb,
+                                                               kc[li], vc[li], bound, sh.scale, ws, n, out, sh.nh,
+                                                               sh.nkv))
+                 for kc, vc in sets for li in range(sh.layers)]
+        return _graph_us(torch, dev, calls, reps=3)
+
+    us = time_splits(ns)
+    sweep = {str(n): round(time_splits(n), 3) for n in (16, 32, 64, 128)}
     gbs = vbytes / (us * 1e-6) / 1e9
     del sets
     torch.cuda.empty_cache()
     res = {"verify": {"us_per_layer_call": round(us, 3), "gbps": round(gbs, 1),
                       "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "n_split": ns, "bucket": bound,
-                      "algorithmic_bytes": vbytes}}
+                      "algorithmic_bytes": vbytes, "n_split_sweep": sweep}}
     g2 = torch.Generator().manual_seed(1004)
     logits = [wl.planted_logits(g2, K1, wl.VOCAB).to(dev) for _ in range(2)]
     logits += [torch.randn(K1, wl.VOCAB, generator=gen, device=dev).to(torch.bfloat16) for _ in range(6)]

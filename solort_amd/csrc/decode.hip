@@ -12,33 +12,34 @@
 // rounds scores and probabilities to bf16 between its torch ops); the output
 // is rounded once, to bf16, or left in fp32 on request.
 //
-// Split kernel.  Grid: nkv * n_split workgroups of 256 threads; block b
-// serves KV head b % nkv and key split b / nkv (with 8 KV heads on 8 XCDs, all
-// splits of a head share one XCD's L2).  The key range [0, bound) is cut into
-// n_split static chunks, so every block issues its first K/V loads at launch,
-// before the device-side position has arrived; keys past the live length are
-// masked, and later iterations of a long split stop at the live length.
-//   - 16 row slots of 16 lanes each take U key rows per iteration; lane j of a
-//     slot loads dims [8j, 8j+8) of K and V as 16-byte vectors.  The query
-//     group (nq * g rows) sits in registers as bf16 pairs, so each KV head is
-//     read once for all of its query heads (no repeat_interleave); a score is
-//     four bf16 pair dot products per lane, reduced over the slot with DPP.
-//   - Scores and V rows of the iteration go to LDS.  Each wavefront then takes
-//     the rows it owns: lane k evaluates p for key k, the p values go through
-//     the wavefront's own LDS row, and every lane accumulates two output dims,
-//     so no per-slot state is merged.
-//   - Fused variant: while the K/V loads are in flight, slots compute the q
-//     rows and the new tokens' K/V rows from the fused qkv projection and the
-//     step's cos/sin rows (qknorm_rope.h, bit identical to the standalone
-//     prologue).  Split 0 of each KV head writes the new rows to the cache;
-//     every block substitutes the fresh rows for the cache rows
-//     pos0..pos0+nq-1 it loaded, so no block waits for that write.
-//   - Barriers order LDS only (lds_barrier): the K/V loads stay in flight
-//     across them.
-//   - Output: with one split the block writes the answer; otherwise its
-//     partial (running max in log2 units, sum, unnormalised output).
-// Combine kernel: merges the partials of each KV head (log-sum-exp); the
-// kernel boundary orders its reads after the split kernel's writes.
+// Grid: nkv * n_split workgroups of 256 threads; block (kvh, split) serves
+// KV head kvh and a static key chunk of [0, bound) (with 8 KV heads on 8
+// XCDs, all splits of a head share one XCD's L2).  Every block issues its
+// first K/V loads at launch, before the device-side position has arrived;
+// keys past the live length are masked.  Fused variant: while those loads
+// are in flight, 16-lane slots compute the q rows and the new tokens' K/V
+// rows from the fused qkv projection and the step's cos/sin rows
+// (qknorm_rope.h, bit identical to the standalone prologue).  Split 0 of
+// each KV head writes the new rows to the cache; every block substitutes the
+// fresh rows for the cache rows pos0..pos0+nq-1 it loaded, so no block waits
+// for that write.  Two split kernels share this structure:
+//   - decode_lanes_kernel, for short chunks of one new token (latency-bound):
+//     16 row slots of 16 lanes take U key rows per step (lane j: dims
+//     8j..8j+7); the query group sits in registers as bf16 pairs, a score is
+//     four bf16 pair dot products reduced over the slot with DPP, and scores
+//     and V rows go through LDS so that each wavefront accumulates its own
+//     query row (two output dims per lane).
+//   - decode_mfma_kernel, for long chunks and several new tokens: each
+//     wavefront takes 32-key tiles (kbeg + 32w + 128i), stages K and V
+//     through its LDS tile with whole-row loads, and computes S^T = K q^T and
+//     O^T += V^T P^T on v_mfma_f32_32x32x16_bf16 with the query rows (at most
+//     32) as the N dimension; V^T comes from transposing LDS reads and P
+//     enters as bf16 high and low parts (~16 bits), with a lazily moved
+//     softmax maximum.  The wavefronts merge in LDS at the end.
+// Output: with one split the block writes the answer; otherwise its partial
+// (running max in log2 units, sum, unnormalised output).  Combine kernel:
+// merges the partials of each KV head (log-sum-exp); the kernel boundary
+// orders its reads after the split kernel's writes.
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -100,10 +101,12 @@ __device__ __forceinline__ void store_out2(void* out, int out_f32, int nh, int k
     *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(out) + oi) = f2bf(o0) | (f2bf(o1) << 16);
 }
 
-// Grid (nkv, n_split): block (kvh, split).  qsrc: fused, the qkv rows (row
-// stride qsrc_stride); unfused, the q rows [nq][nh][128] (qsrc_stride = nh*128).
+// Lane-parallel split kernel, for short key chunks (latency-bound: one to a
+// few key rows per slot).  Grid (nkv, n_split): block (kvh, split).  qsrc:
+// fused, the qkv rows (row stride qsrc_stride); unfused, the q rows
+// [nq][nh][128] (qsrc_stride = nh*128).
 template <int NQ, int G, int U, bool FUSED>
-__global__ __launch_bounds__(256) void decode_kernel(uint16_t* kc, uint16_t* vc, int tok_stride, int head_stride,
+__global__ __launch_bounds__(256) void decode_lanes_kernel(uint16_t* kc, uint16_t* vc, int tok_stride, int head_stride,
                                                      int chunk, int bound, const uint16_t* qsrc, int qsrc_stride,
                                                      int nh, const uint16_t* qn_w, const DecodeTail a) {
   constexpr int R = NQ * G;            // query rows sharing one KV head
@@ -341,6 +344,356 @@ __global__ __launch_bounds__(256) void decode_kernel(uint16_t* kc, uint16_t* vc,
   }
 }
 
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+constexpr int kTile = 32;           // keys per wave per step (one MFMA tile)
+constexpr int kQStride = 128 + 8;   // q rows in LDS (bf16): 272 B, conflict-free 16-byte reads
+constexpr int kVStride = 128 + 16;  // V tile rows in LDS (bf16): 288 B, conflict-free transposing reads
+constexpr int kMergeFloats = 66 * 64;  // one wave's (O, m, l) handed over at the end
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// ds_read_b64_tr_b16: within each 16-lane group, lane i receives in slot k
+// element i % 4 of the 8 bytes addressed by lane 4k + i / 4 of the group.
+__device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (lds_i16x4*)(__attribute__((address_space(3))) uint16_t*)(p));
+  return __builtin_bit_cast(uint2, v);
+}
+
+// One key tile in flight: lane l holds 16-byte column l%16 of K and V rows
+// k0 + l/16 + 4i, i < 8.
+struct KVTile {
+  uint4 k0, k1, k2, k3, k4, k5, k6, k7, v0, v1, v2, v3, v4, v5, v6, v7;
+};
+
+// Loads of the tile at key k0 (k0 past the split: its first rows again, which
+// are cached).  Rows are clamped to kclamp, a row the split may read.
+__device__ __forceinline__ KVTile fetch_tile(const uint16_t* kp, const uint16_t* vp, int tok_stride, int k0, int kbeg,
+                                             int kstat, int kclamp, int lrow) {
+  const int base = k0 < kstat ? k0 : kbeg;
+  const bool whole = base + kTile - 1 <= kclamp;  // wave-uniform: no row needs clamping
+  const int64_t off0 = (int64_t)(base + lrow) * tok_stride, step = (int64_t)4 * tok_stride;
+  KVTile t;
+  auto ld = [&](int i, uint4& kd, uint4& vd) {
+    const int64_t off = whole ? off0 + i * step : (int64_t)min(base + lrow + 4 * i, kclamp) * tok_stride;
+    kd = *reinterpret_cast<const uint4*>(kp + off);
+    vd = *reinterpret_cast<const uint4*>(vp + off);
+  };
+  ld(0, t.k0, t.v0); ld(1, t.k1, t.v1); ld(2, t.k2, t.v2); ld(3, t.k3, t.v3);
+  ld(4, t.k4, t.v4); ld(5, t.k5, t.v5); ld(6, t.k6, t.v6); ld(7, t.k7, t.v7);
+  return t;
+}
+
+// Grid (nkv, n_split): block (kvh, split), 4 wavefronts.  qsrc: fused, the
+// qkv rows (row stride qsrc_stride); unfused, the q rows [nq][nh][128]
+// (qsrc_stride = nh*128).
+template <int NQ, int G, bool FUSED>
+__global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint16_t* vc, int tok_stride, int head_stride,
+                                                        int chunk, int bound, const uint16_t* qsrc, int qsrc_stride,
+                                                        int nh, const uint16_t* qn_w, const DecodeTail a) {
+  constexpr int R = NQ * G;  // query rows sharing one KV head (<= 32)
+  constexpr int NROWS = FUSED ? NQ * (G + 2) : R;
+  static_assert(R <= 32, "at most 32 query rows per KV head");
+  __shared__ __align__(16) uint16_t s_new[FUSED ? 2 * NQ * 128 : 8];  // fresh K rows, then V rows
+  // One region, three uses in turn: the q tile (rows zero past R) until every
+  // wave holds its q operand; then each wave's K and V tiles; at the end the
+  // waves' (O, m, l) handed over for the merge.
+  constexpr int kTileBytes = kTile * (kQStride + kVStride) * 2;  // one wave's K + V tiles
+  constexpr int kXBytes = 4 * kMergeFloats * 4 > 4 * kTileBytes ? 4 * kMergeFloats * 4 : 4 * kTileBytes;
+  __shared__ __align__(16) uint8_t s_x[kXBytes];
+  uint16_t* s_q = reinterpret_cast<uint16_t*>(s_x);
+
+  const int tid = threadIdx.x, j = tid & 15, slot = tid >> 4, wave = tid >> 6, lane = tid & 63;
+  const int l32 = lane & 31, hi = lane >> 5;
+  const int kvh = blockIdx.x, split = blockIdx.y, nkv = gridDim.x, NS = gridDim.y;
+  const int kbeg = min(split * chunk, bound);
+  const int kstat = min(kbeg + chunk, bound);
+  const int kclamp = kstat > kbeg ? kstat - 1 : (kbeg > 0 ? kbeg - 1 : 0);  // a row this split may read
+
+  // 1. Loads for this slot's first prologue row (fused: with its norm
+  //    weights and its token's cos/sin), issued before the K/V loads: vector
+  //    loads complete in issue order, so the prologue then waits for its own
+  //    rows only.  Every load of phases 1 and 2 is unconditional (idle lanes
+  //    load a valid row they ignore): a load skipped on some path would make
+  //    the compiler wait for all of them before the first use.
+  uint4 raw0, wq0 = make_uint4(0u, 0u, 0u, 0u), wk0 = wq0, c0 = wq0, s0 = wq0;
+  {
+    const int row = min(slot, NROWS - 1);
+    if constexpr (FUSED) {
+      const int t = row / (G + 2), c = row % (G + 2);
+      const int hs = c < G ? kvh * G + c : (c == G ? nh + kvh : nh + nkv + kvh);
+      raw0 = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + hs * SOLORT_HD + j * 8);
+      wq0 = *reinterpret_cast<const uint4*>(qn_w + j * 8);
+      wk0 = *reinterpret_cast<const uint4*>(a.kn_w + j * 8);
+      c0 = *reinterpret_cast<const uint4*>(a.rope_cs + t * 64 + (j & 7) * 8);
+      s0 = *reinterpret_cast<const uint4*>(a.rope_cs + (NQ + t) * 64 + (j & 7) * 8);
+    } else {
+      const int t = row / G, g = row % G;
+      raw0 = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + (kvh * G + g) * SOLORT_HD + j * 8);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the K/V loads
+
+  // 2. This wave's first key tile, at static addresses (before the device-side
+  //    position arrives): lane l loads 16-byte column l%16 of key rows
+  //    k0 + l/16 + 4i (i < 8) of K and of V, so each load instruction reads
+  //    four whole 256-byte rows.  Rows past the split re-read a row of it; a
+  //    wave without a tile re-reads the split's first rows (wave 0's, so no
+  //    extra traffic reaches HBM).
+  const uint16_t* kp = kc + (int64_t)kvh * head_stride + 8 * j;
+  const uint16_t* vp = vc + (int64_t)kvh * head_stride + 8 * j;
+  const int lrow = lane >> 4;  // this lane's first row of the tile; rows lrow + 4i
+  KVTile kv = fetch_tile(kp, vp, tok_stride, kbeg + kTile * wave, kbeg, kstat, kclamp, lrow);
+
+  const int64_t pos0 = a.pos0_dev[0];
+
+  // 3. q rows (and, fused, the new tokens' K/V rows) into LDS; rows R..31 of
+  //    the q tile are zero.
+  for (int row = slot; row < NROWS; row += 16) {
+    uint4 raw = raw0, w8, c8 = c0, s8 = s0;
+    if constexpr (FUSED) {
+      const int t = row / (G + 2), c = row % (G + 2);
+      w8 = c < G ? wq0 : wk0;
+      const int64_t pos = pos0 + t;
+      const bool pos_ok = pos >= 0 && pos < a.pos_limit;
+      if (row != slot) {  // rows past the first (verify): loaded here
+        const int hs = c < G ? kvh * G + c : (c == G ? nh + kvh : nh + nkv + kvh);
+        raw = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + hs * SOLORT_HD + j * 8);
+        c8 = *reinterpret_cast<const uint4*>(a.rope_cs + t * 64 + (j & 7) * 8);
+        s8 = *reinterpret_cast<const uint4*>(a.rope_cs + (NQ + t) * 64 + (j & 7) * 8);
+      }
+      if (c == G + 1) {  // V row: raw
+        *reinterpret_cast<uint4*>(&s_new[(NQ + t) * 128 + j * 8]) = raw;
+        if (split == 0 && pos_ok)
+          *reinterpret_cast<uint4*>(vc + pos * tok_stride + (int64_t)kvh * head_stride + j * 8) = raw;
+        continue;
+      }
+      float cs[8], sn[8];
+      unpack8(c8, cs);
+      unpack8(s8, sn);
+      const uint4 ov = qknorm_rope_row(raw, w8, cs, sn, a.eps, j);
+      if (c < G) {
+        *reinterpret_cast<uint4*>(&s_q[(t * G + c) * kQStride + j * 8]) = ov;
+      } else {
+        *reinterpret_cast<uint4*>(&s_new[t * 128 + j * 8]) = ov;
+        if (split == 0 && pos_ok)
+          *reinterpret_cast<uint4*>(kc + pos * tok_stride + (int64_t)kvh * head_stride + j * 8) = ov;
+      }
+    } else {
+      const int t = row / G, g = row % G;
+      if (row != slot)
+        raw = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + (kvh * G + g) * SOLORT_HD + j * 8);
+      *reinterpret_cast<uint4*>(&s_q[row * kQStride + j * 8]) = raw;
+    }
+  }
+  for (int i = tid; i < (32 - R) * 16; i += 256)
+    *reinterpret_cast<uint4*>(&s_q[(R + (i >> 4)) * kQStride + (i & 15) * 8]) = make_uint4(0u, 0u, 0u, 0u);
+  lds_barrier();
+
+  // q^T operand of the eight 16-dim steps: lane l holds row l%32, dims 16kk + 8(l/32) .. +7.
+  bf16x8 qb[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+    qb[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(&s_q[l32 * kQStride + 16 * kk + 8 * hi]));
+  lds_barrier();  // the q tile's space becomes the waves' K/V tiles
+
+  // 4. Key tiles k0 = kbeg + 32 wave + 128 i.  Per tile: V into this wave's
+  //    LDS tile, S^T = K q^T (8 MFMAs), the next tile's loads, softmax with a
+  //    lazy maximum, then O^T += V^T P^T with P split into bf16 high and low
+  //    parts (16 MFMAs), which keeps P to ~16 bits.
+  int64_t live64 = pos0 + NQ;
+  live64 = live64 < 0 ? 0 : (live64 > bound ? bound : live64);
+  const int kend = min(kstat, (int)live64);
+  const int64_t rowpos = pos0 + (l32 < R ? l32 / G : NQ - 1);  // this lane's query position
+  const float qs = a.qscale;
+  uint16_t* sk = reinterpret_cast<uint16_t*>(s_x + wave * kTileBytes);  // [32][kQStride] K tile
+  uint16_t* sv = sk + kTile * kQStride;                                  // [32][kVStride] V tile
+  f32x16 o[4];
+#pragma unroll
+  for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
+  float m = -INFINITY, lsum = 0.f;  // reference max (raw score units); this lane's share of the row sum
+  for (int k0 = kbeg + kTile * wave; k0 < kend; k0 += 4 * kTile) {
+    // Wave-uniform: does the tile hold the new tokens' rows, or rows past the
+    // live length, or keys past some query's position?
+    const bool has_new = FUSED && (int64_t)k0 <= pos0 + NQ - 1 && (int64_t)(k0 + kTile) > pos0;
+    const bool tail = k0 + kTile > kend;
+    const bool edge = tail || (int64_t)(k0 + kTile - 1) > pos0;
+    auto stage_row = [&](int i, uint4 kd, uint4 vd) {
+      const int key = k0 + lrow + 4 * i;
+      if (has_new) {  // the new tokens' rows: fresh values, not the cache
+        const int64_t off = (int64_t)key - pos0;
+        if (off >= 0 && off < NQ) {
+          kd = *reinterpret_cast<const uint4*>(&s_new[off * 128 + 8 * j]);
+          vd = *reinterpret_cast<const uint4*>(&s_new[(NQ + off) * 128 + 8 * j]);
+        }
+      }
+      if (tail && key >= kend) vd = make_uint4(0u, 0u, 0u, 0u);  // p = 0 must not meet a non-finite value
+      *reinterpret_cast<uint4*>(&sk[(lrow + 4 * i) * kQStride + 8 * j]) = kd;
+      *reinterpret_cast<uint4*>(&sv[(lrow + 4 * i) * kVStride + 8 * j]) = vd;
+    };
+    stage_row(0, kv.k0, kv.v0); stage_row(1, kv.k1, kv.v1); stage_row(2, kv.k2, kv.v2); stage_row(3, kv.k3, kv.v3);
+    stage_row(4, kv.k4, kv.v4); stage_row(5, kv.k5, kv.v5); stage_row(6, kv.k6, kv.v6); stage_row(7, kv.k7, kv.v7);
+    // next tile (past the end: a re-read of cached rows)
+    kv = fetch_tile(kp, vp, tok_stride, k0 + 4 * kTile, kbeg, kstat, kclamp, lrow);
+    f32x16 s = f32x16{};
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk) {
+      const uint4 ka = *reinterpret_cast<const uint4*>(&sk[l32 * kQStride + 16 * kk + 8 * hi]);
+      s = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(ka), qb[kk], s, 0, 0, 0);
+    }
+
+    // s[i] is the score of key k0 + 8(i/4) + 4hi + i%4 for query row l%32.
+    if (edge) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int key = k0 + 8 * (i >> 2) + 4 * hi + (i & 3);
+        if (key >= kend || (int64_t)key > rowpos) s[i] = -INFINITY;
+      }
+    }
+    float mx = s[0];
+#pragma unroll
+    for (int i = 1; i < 16; ++i) mx = fmaxf(mx, s[i]);
+    mx = xor32_combine(mx, [](float x, float y) { return fmaxf(x, y); });
+    // Lazy maximum: the reference max moves only when a tile's max exceeds it
+    // by more than 8 (log2 units), so p <= 2^8; before a row's first visible
+    // key m = -inf and O = 0, l = 0, so it takes the tile's max without a rescale.
+    const bool bump = mx * qs > m * qs + 8.f;
+    const float mn = bump ? mx : m;
+    const float mq = mn == -INFINITY ? 0.f : mn * qs;
+    const float alpha = (bump && m != -INFINITY) ? fast_exp2(m * qs - mq) : 1.f;
+    float ps = 0.f;
+    uint32_t ph[8], pl[8];  // p as bf16 pairs: high parts and the low remainders
+#pragma unroll
+    for (int i = 0; i < 16; i += 2) {
+      const float e0 = fast_exp2(fmaf(s[i], qs, -mq)), e1 = fast_exp2(fmaf(s[i + 1], qs, -mq));
+      ps += e0 + e1;
+      const uint32_t h2 = pack2(e0, e1);
+      ph[i >> 1] = h2;
+      pl[i >> 1] = pack2(e0 - __uint_as_float(h2 << 16), e1 - __uint_as_float(h2 & 0xffff0000u));
+    }
+    lsum = fmaf(lsum, alpha, ps);
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // some row's reference max moved
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) o[dt] *= alpha;
+    }
+    m = mn;
+    // O^T += V^T P^T; key step h covers keys k0 + 16h + {4hi + 0..3, 8 + 4hi + 0..3}.  The V^T
+    // operand comes from the row-major tile by transposing reads: lane 16G + jj addresses key
+    // row 4(G/2) + jj/4 (+8 for the upper four keys) at dims 16(G%2) + 4(jj%4), so lane l
+    // receives dim l%32 of the four keys its P^T slots hold.
+    const uint16_t* vb = sv + (4 * hi + ((lane & 15) >> 2)) * kVStride + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      const bf16x8 pbh = as_bf16x8(make_uint4(ph[4 * h], ph[4 * h + 1], ph[4 * h + 2], ph[4 * h + 3]));
+      const bf16x8 pbl = as_bf16x8(make_uint4(pl[4 * h], pl[4 * h + 1], pl[4 * h + 2], pl[4 * h + 3]));
+#pragma unroll
+      for (int dt = 0; dt < 4; ++dt) {
+        const uint16_t* vr8 = vb + 16 * h * kVStride + 32 * dt;
+        const uint2 lo = lds_read_tr16(vr8);
+        const uint2 up = lds_read_tr16(vr8 + 8 * kVStride);
+        const bf16x8 va = as_bf16x8(make_uint4(lo.x, lo.y, up.x, up.y));
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pbh, o[dt], 0, 0, 0);
+        o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pbl, o[dt], 0, 0, 0);
+      }
+    }
+  }
+
+  // 5. Merge the wavefronts that saw keys (log-sum-exp) and write this
+  //    split's partial (max in log2 units, sum, unnormalised output) or, with
+  //    one split, the answer.  O^T: lane l, register i of o[dt] holds dim
+  //    32dt + 8(i/4) + 4(l/32) + i%4 of row l%32.  With one active wave it
+  //    writes directly; otherwise every wave hands (O, m, l) over through LDS
+  //    and wave w merges and writes dims 32w .. 32w + 31.
+  lsum = xor32_combine(lsum, [](float x, float y) { return x + y; });  // both halves of the row
+  const int nact = kend > kbeg ? min(4, (kend - kbeg + kTile - 1) / kTile) : 1;  // block-uniform
+  f32x16 om;  // the output dims this wave writes: o[wave] (merged) or, alone, all four in turn
+  if (nact > 1) {
+    __syncthreads();  // every wave is done with its V tile
+    float* xf = reinterpret_cast<float*>(s_x);
+    float* xw = xf + wave * kMergeFloats;
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        *reinterpret_cast<float4*>(&xw[(dt * 4 + q4) * 256 + 4 * lane]) =
+            make_float4(o[dt][4 * q4], o[dt][4 * q4 + 1], o[dt][4 * q4 + 2], o[dt][4 * q4 + 3]);
+    xw[64 * 64 + lane] = m;
+    xw[65 * 64 + lane] = lsum;
+    __syncthreads();
+    float mw[4], lw[4], mt = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      mw[w] = w < nact ? xf[w * kMergeFloats + 64 * 64 + lane] : -INFINITY;
+      lw[w] = w < nact ? xf[w * kMergeFloats + 65 * 64 + lane] : 0.f;
+      mt = fmaxf(mt, mw[w]);
+    }
+    om = f32x16{};
+    lsum = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) {
+      if (w >= nact) break;  // block-uniform
+      const float aw = mt == -INFINITY ? 0.f : fast_exp2((mw[w] - mt) * qs);  // -inf gives 0
+      lsum = fmaf(lw[w], aw, lsum);
+      const float* src = xf + w * kMergeFloats + (wave * 4) * 256 + 4 * lane;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const float4 v = *reinterpret_cast<const float4*>(src + q4 * 256);
+        om[4 * q4] = fmaf(v.x, aw, om[4 * q4]);
+        om[4 * q4 + 1] = fmaf(v.y, aw, om[4 * q4 + 1]);
+        om[4 * q4 + 2] = fmaf(v.z, aw, om[4 * q4 + 2]);
+        om[4 * q4 + 3] = fmaf(v.w, aw, om[4 * q4 + 3]);
+      }
+    }
+    m = mt;
+  } else if (wave > 0) {
+    return;
+  }
+  if (l32 >= R) return;
+  const int r = l32;
+  // Writes dims 32dt .. 32dt + 31 of row r (this lane's 16 of them) from od.
+  auto write_dims = [&](const f32x16& od, int dt) {
+    if (NS == 1) {
+      const float inv = lsum > 0.f ? 1.f / lsum : 0.f;
+      const int t = r / G, g = r % G;
+      const int64_t ob = ((int64_t)t * nh + kvh * G + g) * SOLORT_HD + 4 * hi + 32 * dt;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const float4 v = make_float4(od[4 * q4] * inv, od[4 * q4 + 1] * inv, od[4 * q4 + 2] * inv,
+                                     od[4 * q4 + 3] * inv);
+        if (a.out_f32) {
+          *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + ob + 8 * q4) = v;
+        } else {
+          uint2 pk;
+          pk.x = pack2(v.x, v.y);
+          pk.y = pack2(v.z, v.w);
+          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.out) + ob + 8 * q4) = pk;
+        }
+      }
+    } else {
+      float* dst = a.ws_o + ((int64_t)(kvh * NS + split) * R + r) * 128 + 32 * dt + 4 * hi;
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4)
+        *reinterpret_cast<float4*>(dst + 8 * q4) = make_float4(od[4 * q4], od[4 * q4 + 1], od[4 * q4 + 2],
+                                                               od[4 * q4 + 3]);
+    }
+  };
+  if (nact > 1) {
+    write_dims(om, wave);
+  } else {
+    write_dims(o[0], 0);
+    write_dims(o[1], 1);
+    write_dims(o[2], 2);
+    write_dims(o[3], 3);
+  }
+  if (NS > 1 && hi == 0 && (nact == 1 || wave == 0))
+    *reinterpret_cast<float2*>(a.ws_ml + ((int64_t)(kvh * NS + split) * R + r) * 2) =
+        make_float2(m == -INFINITY ? m : m * qs, lsum);
+}
+
 // The log-sum-exp combine of the n_split partials of each KV head.  Grid
 // (nkv, column blocks): block = (KV head, 32 float4 columns of its [R][128]
 // output); thread = (column, split group sg of 8): it merges splits sg,
@@ -420,7 +773,9 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* ws_o, const f
 
 // ---------------------------------------------------------------- host side
 
-constexpr int kMaxRows = 20;  // nq * group limit (registers and LDS)
+constexpr int kMaxRows = 32;       // nq * group limit: one MFMA tile of query rows
+constexpr int kLanesMaxGroup = 8;  // the lane-parallel kernel serves one token of up to 8 query heads
+constexpr int kLanesMaxChunk = 64;  // ... and key chunks of at most 64 rows (4 per slot)
 constexpr int kMaxSplit = 1024;
 
 // Everything a launch needs, gathered by prepare() and the entry points.
@@ -431,6 +786,8 @@ struct DecodeArgs {
   const uint16_t* qsrc;
   int qsrc_stride, nh, nkv, n_split;
   const uint16_t* qn_w;
+  bool lanes;  // the lane-parallel kernel (short chunks, one new token), else the MFMA kernel
+  int U;       // key rows per slot per step of the lane-parallel kernel
   DecodeTail tail;
 };
 
@@ -449,22 +806,23 @@ static WsLayout ws_layout(int nq, int nh, int nkv, int n_split) {
   return w;
 }
 
-template <int NQ, int G, int U, bool FUSED>
-static void launch_split(const DecodeArgs& a, hipStream_t s) {
-  hipLaunchKernelGGL((decode_kernel<NQ, G, U, FUSED>), dim3(a.nkv, a.n_split), dim3(256), 0, s, a.kc, a.vc,
-                     a.tok_stride, a.head_stride, a.chunk, a.bound, a.qsrc, a.qsrc_stride, a.nh, a.qn_w, a.tail);
-}
-
 template <int NQ, int G, bool FUSED>
-static bool launch_u(int U, const DecodeArgs& a, hipStream_t s) {
+static bool launch_split(const DecodeArgs& a, hipStream_t s) {
   if constexpr (NQ * G <= kMaxRows) {
-    if constexpr (NQ == 1) {
-      if (U == 4) {
-        launch_split<NQ, G, 4, FUSED>(a, s);
+    const dim3 grid(a.nkv, a.n_split);
+    if constexpr (NQ == 1 && G <= kLanesMaxGroup) {
+      if (a.lanes) {
+        if (a.U == 4)
+          hipLaunchKernelGGL((decode_lanes_kernel<NQ, G, 4, FUSED>), grid, dim3(256), 0, s, a.kc, a.vc, a.tok_stride,
+                             a.head_stride, a.chunk, a.bound, a.qsrc, a.qsrc_stride, a.nh, a.qn_w, a.tail);
+        else
+          hipLaunchKernelGGL((decode_lanes_kernel<NQ, G, 2, FUSED>), grid, dim3(256), 0, s, a.kc, a.vc, a.tok_stride,
+                             a.head_stride, a.chunk, a.bound, a.qsrc, a.qsrc_stride, a.nh, a.qn_w, a.tail);
         return true;
       }
     }
-    launch_split<NQ, G, 2, FUSED>(a, s);
+    hipLaunchKernelGGL((decode_mfma_kernel<NQ, G, FUSED>), grid, dim3(256), 0, s, a.kc, a.vc, a.tok_stride,
+                       a.head_stride, a.chunk, a.bound, a.qsrc, a.qsrc_stride, a.nh, a.qn_w, a.tail);
     return true;
   } else {
     return false;
@@ -498,13 +856,13 @@ static bool launch_combine(const DecodeArgs& a, hipStream_t s) {
   return false;
 
 template <int NQ, int G>
-static bool launch_attn(bool fused, int U, const DecodeArgs& a, hipStream_t s) {
-  return fused ? launch_u<NQ, G, true>(U, a, s) : launch_u<NQ, G, false>(U, a, s);
+static bool launch_attn(bool fused, const DecodeArgs& a, hipStream_t s) {
+  return fused ? launch_split<NQ, G, true>(a, s) : launch_split<NQ, G, false>(a, s);
 }
 
 template <int G>
-static bool attn_nq(int nq, bool fused, int U, const DecodeArgs& a, hipStream_t s) {
-  SOLORT_DISPATCH_NQ(G, launch_attn, fused, U, a, s)
+static bool attn_nq(int nq, bool fused, const DecodeArgs& a, hipStream_t s) {
+  SOLORT_DISPATCH_NQ(G, launch_attn, fused, a, s)
 }
 
 template <int G>
@@ -512,12 +870,12 @@ static bool combine_nq(int nq, const DecodeArgs& a, hipStream_t s) {
   SOLORT_DISPATCH_NQ(G, launch_combine, a, s)
 }
 
-static bool dispatch_attn(int G, int nq, bool fused, int U, const DecodeArgs& a, hipStream_t s) {
+static bool dispatch_attn(int G, int nq, bool fused, const DecodeArgs& a, hipStream_t s) {
   switch (G) {
-    case 1: return attn_nq<1>(nq, fused, U, a, s);
-    case 2: return attn_nq<2>(nq, fused, U, a, s);
-    case 4: return attn_nq<4>(nq, fused, U, a, s);
-    case 8: return attn_nq<8>(nq, fused, U, a, s);
+    case 1: return attn_nq<1>(nq, fused, a, s);
+    case 2: return attn_nq<2>(nq, fused, a, s);
+    case 4: return attn_nq<4>(nq, fused, a, s);
+    case 8: return attn_nq<8>(nq, fused, a, s);
   }
   return false;
 }
@@ -538,7 +896,7 @@ constexpr int64_t kMaxI32 = 0x7fffffff;
 static int prepare(const char* name, int nq, int nh, int nkv, int hd, void* k_cache, void* v_cache,
                    int64_t kv_tok_stride, int64_t kv_head_stride, int64_t max_len,
                    const int64_t* pos0_dev, int bound, float scale, void* ws, int n_split, void* out,
-                   int out_dtype, DecodeArgs& a, int& U) {
+                   int out_dtype, DecodeArgs& a) {
   if (hd != SOLORT_HD) return set_error(SOLORT_EINVAL, "%s: head_dim %d != 128", name, hd);
   if (nh <= 0 || nkv <= 0 || nh % nkv != 0)
     return set_error(SOLORT_EINVAL, "%s: nh=%d must be a positive multiple of nkv=%d", name, nh, nkv);
@@ -567,7 +925,14 @@ static int prepare(const char* name, int nq, int nh, int nkv, int hd, void* k_ca
   a.vc = (uint16_t*)v_cache;
   a.tok_stride = (int)kv_tok_stride;
   a.head_stride = (int)kv_head_stride;
-  a.chunk = ((((bound + n_split - 1) / n_split) + 15) / 16) * 16;  // static key chunk per split
+  // Short chunks of one new token are latency-bound: the lane-parallel kernel
+  // (chunk a multiple of 16 keys).  Longer chunks and several new tokens: the
+  // MFMA kernel (chunk a multiple of its 32-key tile).
+  const int raw_chunk = (bound + n_split - 1) / n_split;
+  a.lanes = nq == 1 && G <= kLanesMaxGroup && raw_chunk <= kLanesMaxChunk;
+  const int gran = a.lanes ? 16 : kTile;
+  a.chunk = ((raw_chunk + gran - 1) / gran) * gran;  // static key chunk per split
+  a.U = a.chunk >= 64 ? 4 : 2;
   a.bound = bound;
   a.nh = nh;
   a.nkv = nkv;
@@ -579,14 +944,13 @@ static int prepare(const char* name, int nq, int nh, int nkv, int hd, void* k_ca
   a.tail.qscale = scale * 1.4426950408889634f;
   a.tail.pos_limit = (int)max_len;
   a.tail.out_f32 = out_dtype == SOLORT_DTYPE_F32;
-  U = a.chunk >= 64 ? 4 : 2;
   return 0;
 }
 
 // Launches the split kernel, then (more than one split) the combine kernel.
-static int launch_all(const char* name, bool fused, int nq, const DecodeArgs& a, int U, hipStream_t s) {
+static int launch_all(const char* name, bool fused, int nq, const DecodeArgs& a, hipStream_t s) {
   const int G = a.nh / a.nkv;
-  if (!dispatch_attn(G, nq, fused, U, a, s))
+  if (!dispatch_attn(G, nq, fused, a, s))
     return set_error(SOLORT_EINVAL, "%s: no kernel for nq=%d group=%d", name, nq, G);
   int rc = check_launch(name);
   if (rc || a.n_split == 1) return rc;
@@ -601,14 +965,13 @@ static int attn_impl(const char* name, const void* q, int nq, int nh, int nkv, i
                      float scale, void* ws, int n_split, void* out, int out_dtype,
                      solort_stream_t stream) {
   DecodeArgs a = {};
-  int U = 2;
   int rc = prepare(name, nq, nh, nkv, hd, (void*)k_cache, (void*)v_cache, kv_tok_stride, kv_head_stride,
-                   max_len, pos0_dev, bound, scale, ws, n_split, out, out_dtype, a, U);
+                   max_len, pos0_dev, bound, scale, ws, n_split, out, out_dtype, a);
   if (rc) return rc;
   if (!q || !aligned16(q)) return set_error(SOLORT_EINVAL, "%s: q must be a 16-byte aligned pointer", name);
   a.qsrc = (const uint16_t*)q;
   a.qsrc_stride = nh * SOLORT_HD;
-  return launch_all(name, false, nq, a, U, (hipStream_t)stream);
+  return launch_all(name, false, nq, a, (hipStream_t)stream);
 }
 
 }  // namespace solort
@@ -645,9 +1008,8 @@ extern "C" int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int 
                                    int n_split, void* out, int out_dtype, solort_stream_t stream) {
   const char* name = "decode_layer";
   DecodeArgs a = {};
-  int U = 2;
   int rc = prepare(name, nq, nh, nkv, hd, k_cache, v_cache, kv_tok_stride, kv_head_stride, max_len, pos0_dev,
-                   bound, scale, ws, n_split, out, out_dtype, a, U);
+                   bound, scale, ws, n_split, out, out_dtype, a);
   if (rc) return rc;
   if (!qkv || !qn_w || !kn_w || !rope_cs) return set_error(SOLORT_EINVAL, "%s: null pointer", name);
   if (!aligned16(qkv) || !aligned16(qn_w) || !aligned16(kn_w) || !aligned16(rope_cs))
@@ -660,5 +1022,5 @@ extern "C" int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int 
   a.tail.kn_w = (const uint16_t*)kn_w;
   a.tail.rope_cs = (const uint16_t*)rope_cs;
   a.tail.eps = eps;
-  return launch_all(name, true, nq, a, U, (hipStream_t)stream);
+  return launch_all(name, true, nq, a, (hipStream_t)stream);
 }

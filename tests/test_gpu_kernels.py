@@ -146,7 +146,7 @@ def test_decode_qwen3_8b_32k(gpu):
     ctx_ref = ref.decode_attn(q.cpu().transpose(0, 1), kc.cpu(), vc.cpu(), case.pos, case.bound, sh.scale)
     ref_err = np.abs(ctx_ref.float().numpy() - want64)
     _say(f"  reference bf16 ops vs fp64: max-abs {ref_err.max():.3e} mean-abs {ref_err.mean():.3e}")
-    for ns in (64, 128, 256):
+    for ns in (32, 64, 256, 1024):  # 1024 splits: 32-key chunks (lane-parallel kernel); others MFMA
         ws = ops.attn_workspace(1, sh.nh, sh.nkv, ns, dev)
         out = torch.empty(1, sh.nh * HD, dtype=torch.bfloat16, device=dev)
         out32 = torch.empty(1, sh.nh * HD, dtype=torch.float32, device=dev)
