@@ -27,10 +27,10 @@ import time
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
-# HBM bytes per launch of the decode split kernel at KV 1024 (decode_kernel<1,4,2,true,false>),
+# HBM bytes per launch of the decode split kernel at KV 1024 (decode_lanes_kernel<1,4,2,true>),
 # from rocprofv3 --pmc FETCH_SIZE (x1.999: a 64 MiB copy reads 32786 KiB on it) plus
-# WRITE_SIZE (x1.000): (2140.0 * 1.999 + 524.0) KiB.  Re-measured whenever that kernel changes.
-DECODE_KERNEL_TRAFFIC = int((2140.0 * 1.999 + 524.0) * 1024)
+# WRITE_SIZE (x1.000): (2102.5 * 1.999 + 524.0) KiB.  Re-measured whenever that kernel changes.
+DECODE_KERNEL_TRAFFIC = int((2102.5 * 1.999 + 524.0) * 1024)
 
 
 def decode_bytes(live: int, nh: int = 32, nkv: int = 8, hd: int = 128) -> int:
@@ -54,9 +54,10 @@ def parse() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-sweep", action="store_true", help="skip the per-bucket decode extras")
-    p.add_argument("--only", choices=("all", "decode", "prefill"), default="all",
-                   help="decode: the decode step and its kernel only; prefill: the prefill kernels only "
-                        "(for per-workload profiles)")
+    p.add_argument("--only", choices=("all", "decode", "prefill", "long", "verify"), default="all",
+                   help="decode: the decode step and its kernel only; prefill: the prefill kernels only; "
+                        "long: the Qwen3-8B KV 32768 decode only; verify: the speculative verify and argmax "
+                        "only (for per-workload profiles)")
     return p.parse_args()
 
 
@@ -100,6 +101,12 @@ def main() -> int:
 
     if args.only == "prefill":
         print(json.dumps({"prefill": prefill_extras(torch, ops, runners, dev, sh)}), flush=True)
+        return 0
+    if args.only == "long":
+        print(json.dumps({"decode_8b_kv32768": long_decode_extras(torch, ops, wl, dev)}), flush=True)
+        return 0
+    if args.only == "verify":
+        print(json.dumps(verify_extras(torch, ops, wl, runners, dev, sh)), flush=True)
         return 0
 
     # ---------------------------------------------------------------- timed graph replays
@@ -146,7 +153,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": DECODE_KERNEL_TRAFFIC if live == 1024 else None,
-                     "kernel": "solort_decode_layer = decode_kernel<1,4,2,fused> + combine_kernel<1,4>",
+                     "kernel": "solort_decode_layer = decode_lanes_kernel<1,4,2,fused> + combine_kernel<1,4>",
                      "kernel_us": round(kern_us, 3),
                      "algorithmic_bytes": kbytes},
     }

@@ -414,27 +414,33 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint1
   const int kstat = min(kbeg + chunk, bound);
   const int kclamp = kstat > kbeg ? kstat - 1 : (kbeg > 0 ? kbeg - 1 : 0);  // a row this split may read
 
-  // 1. Loads for this slot's first prologue row (fused: with its norm
-  //    weights and its token's cos/sin), issued before the K/V loads: vector
-  //    loads complete in issue order, so the prologue then waits for its own
-  //    rows only.  Every load of phases 1 and 2 is unconditional (idle lanes
-  //    load a valid row they ignore): a load skipped on some path would make
-  //    the compiler wait for all of them before the first use.
-  uint4 raw0, wq0 = make_uint4(0u, 0u, 0u, 0u), wk0 = wq0, c0 = wq0, s0 = wq0;
-  {
-    const int row = min(slot, NROWS - 1);
+  // 1. Loads for this slot's prologue rows slot, slot + 16, ... (fused: with
+  //    the norm weights and each row's token's cos/sin), issued before the K/V
+  //    loads: vector loads complete in issue order, so the prologue then waits
+  //    for its own rows only.  Every load of phases 1 and 2 is unconditional
+  //    (idle lanes load a valid row they ignore): a load skipped on some path
+  //    would make the compiler wait for all of them before the first use.
+  constexpr int NPASS = (NROWS + 15) / 16;
+  uint4 raw[NPASS], cr[NPASS], sr[NPASS];
+  uint4 wq0 = make_uint4(0u, 0u, 0u, 0u), wk0 = wq0;
+#pragma unroll
+  for (int ps = 0; ps < NPASS; ++ps) {
+    const int row = min(slot + 16 * ps, NROWS - 1);
+    cr[ps] = sr[ps] = make_uint4(0u, 0u, 0u, 0u);
     if constexpr (FUSED) {
       const int t = row / (G + 2), c = row % (G + 2);
       const int hs = c < G ? kvh * G + c : (c == G ? nh + kvh : nh + nkv + kvh);
-      raw0 = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + hs * SOLORT_HD + j * 8);
-      wq0 = *reinterpret_cast<const uint4*>(qn_w + j * 8);
-      wk0 = *reinterpret_cast<const uint4*>(a.kn_w + j * 8);
-      c0 = *reinterpret_cast<const uint4*>(a.rope_cs + t * 64 + (j & 7) * 8);
-      s0 = *reinterpret_cast<const uint4*>(a.rope_cs + (NQ + t) * 64 + (j & 7) * 8);
+      raw[ps] = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + hs * SOLORT_HD + j * 8);
+      cr[ps] = *reinterpret_cast<const uint4*>(a.rope_cs + t * 64 + (j & 7) * 8);
+      sr[ps] = *reinterpret_cast<const uint4*>(a.rope_cs + (NQ + t) * 64 + (j & 7) * 8);
     } else {
       const int t = row / G, g = row % G;
-      raw0 = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + (kvh * G + g) * SOLORT_HD + j * 8);
+      raw[ps] = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + (kvh * G + g) * SOLORT_HD + j * 8);
     }
+  }
+  if constexpr (FUSED) {
+    wq0 = *reinterpret_cast<const uint4*>(qn_w + j * 8);
+    wk0 = *reinterpret_cast<const uint4*>(a.kn_w + j * 8);
   }
   __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the K/V loads
 
@@ -453,29 +459,24 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint1
 
   // 3. q rows (and, fused, the new tokens' K/V rows) into LDS; rows R..31 of
   //    the q tile are zero.
-  for (int row = slot; row < NROWS; row += 16) {
-    uint4 raw = raw0, w8, c8 = c0, s8 = s0;
+#pragma unroll
+  for (int ps = 0; ps < NPASS; ++ps) {
+    const int row = slot + 16 * ps;
+    if (row >= NROWS) break;
     if constexpr (FUSED) {
       const int t = row / (G + 2), c = row % (G + 2);
-      w8 = c < G ? wq0 : wk0;
       const int64_t pos = pos0 + t;
       const bool pos_ok = pos >= 0 && pos < a.pos_limit;
-      if (row != slot) {  // rows past the first (verify): loaded here
-        const int hs = c < G ? kvh * G + c : (c == G ? nh + kvh : nh + nkv + kvh);
-        raw = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + hs * SOLORT_HD + j * 8);
-        c8 = *reinterpret_cast<const uint4*>(a.rope_cs + t * 64 + (j & 7) * 8);
-        s8 = *reinterpret_cast<const uint4*>(a.rope_cs + (NQ + t) * 64 + (j & 7) * 8);
-      }
       if (c == G + 1) {  // V row: raw
-        *reinterpret_cast<uint4*>(&s_new[(NQ + t) * 128 + j * 8]) = raw;
+        *reinterpret_cast<uint4*>(&s_new[(NQ + t) * 128 + j * 8]) = raw[ps];
         if (split == 0 && pos_ok)
-          *reinterpret_cast<uint4*>(vc + pos * tok_stride + (int64_t)kvh * head_stride + j * 8) = raw;
+          *reinterpret_cast<uint4*>(vc + pos * tok_stride + (int64_t)kvh * head_stride + j * 8) = raw[ps];
         continue;
       }
       float cs[8], sn[8];
-      unpack8(c8, cs);
-      unpack8(s8, sn);
-      const uint4 ov = qknorm_rope_row(raw, w8, cs, sn, a.eps, j);
+      unpack8(cr[ps], cs);
+      unpack8(sr[ps], sn);
+      const uint4 ov = qknorm_rope_row(raw[ps], c < G ? wq0 : wk0, cs, sn, a.eps, j);
       if (c < G) {
         *reinterpret_cast<uint4*>(&s_q[(t * G + c) * kQStride + j * 8]) = ov;
       } else {
@@ -484,10 +485,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint1
           *reinterpret_cast<uint4*>(kc + pos * tok_stride + (int64_t)kvh * head_stride + j * 8) = ov;
       }
     } else {
-      const int t = row / G, g = row % G;
-      if (row != slot)
-        raw = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + (kvh * G + g) * SOLORT_HD + j * 8);
-      *reinterpret_cast<uint4*>(&s_q[row * kQStride + j * 8]) = raw;
+      *reinterpret_cast<uint4*>(&s_q[row * kQStride + j * 8]) = raw[ps];
     }
   }
   for (int i = tid; i < (32 - R) * 16; i += 256)

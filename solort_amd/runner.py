@@ -35,15 +35,16 @@ PREFILL_BUCKETS = (16, 32, 64, 128, 256, 512, 1024)
 def decode_splits(bound: int, nkv: int) -> int:
     """Key splits per KV head for a decode bucket.  Up to 4096 keys: about 32 keys per split,
     enough workgroups to cover the 256 CUs (short chunks, latency-bound).  Longer buckets:
-    512-key chunks, so each workgroup streams several key tiles per wavefront."""
+    1024-key chunks, so each workgroup streams eight key tiles per wavefront."""
     if bound <= 4096:
         return max(1, min(256, bound // 32))
-    return max(1, min(1024, bound // 512))
+    return max(1, min(1024, bound // 1024))
 
 
 def verify_splits(bound: int) -> int:
-    """Key splits per KV head for a K+1-token verify bucket (64 keys per split, at most 64)."""
-    return max(1, min(64, bound // 64))
+    """Key splits per KV head for a K+1-token verify bucket (128 keys per split, one key tile per
+    wavefront, at most 64 splits)."""
+    return max(1, min(64, bound // 128))
 
 
 class GraphQwen3Attention:

@@ -5,7 +5,7 @@ from solort_amd.runner import DECODE_BUCKETS, PREFILL_BUCKETS, decode_splits
 def test_decode_splits_heuristic():
     assert decode_splits(1024, 8) == 32
     assert decode_splits(128, 8) == 4
-    assert decode_splits(32768, 8) == 64
+    assert decode_splits(32768, 8) == 32
     assert decode_splits(16, 8) == 1
 
 
