@@ -77,6 +77,20 @@ int solort_qknorm_rope_kvwrite(const void* qkv, int64_t qkv_row_stride, int T, i
                                int64_t kv_head_stride, int64_t max_len, solort_stream_t stream);
 
 /*
+ * The same prologue with the cos/sin rows given: rope_cs [2, T, 64] bf16 is
+ * solort_rope_rows(inv_freq, 64, pos0_dev, T) of this step (cos rows of
+ * positions pos0..pos0+T-1, then the sin rows), as the reference computes
+ * cos, sin once per forward (cuda_graph_executor.py:111, :164, :248) and every
+ * layer's prologue (:120-121, :176-177, :257-258) applies them.  Results are
+ * bit-identical to solort_qknorm_rope_kvwrite on the same inputs.
+ */
+int solort_qknorm_rope_kvwrite_cs(const void* qkv, int64_t qkv_row_stride, int T, int nh, int nkv, int hd,
+                                  const void* qn_w, const void* kn_w, float eps, const void* rope_cs,
+                                  const int64_t* pos0_dev, void* q_out, void* k_cache, void* v_cache,
+                                  int64_t kv_tok_stride, int64_t kv_head_stride, int64_t max_len,
+                                  solort_stream_t stream);
+
+/*
  * RoPE table on the device: cos_out/sin_out [rows, half_dim] bf16 with row p
  * = bf16(cos/sin(float(p) * inv_freq[i])), the first half of the reference's
  * _cos_sin(p) row (cuda_graph_executor.py:95-98); inv_freq [half_dim] fp32 as
@@ -86,10 +100,11 @@ int solort_rope_table(const float* inv_freq, int half_dim, int64_t rows, void* c
                       solort_stream_t stream);
 
 /*
- * cos/sin rows of the positions of one decode or verify step, computed once
- * per step and read by every layer's solort_decode_layer, as the reference
- * computes cos, sin = _cos_sin(pos) once per step (cuda_graph_executor.py:164,
- * :248) and every layer applies them.
+ * cos/sin rows of the positions of one step (decode, verify or prefill),
+ * computed once per step and read by every layer's solort_decode_layer or
+ * solort_qknorm_rope_kvwrite_cs, as the reference computes cos, sin =
+ * _cos_sin(positions) once per step (cuda_graph_executor.py:111, :164, :248)
+ * and every layer applies them.  n <= 2^20.
  * cs_out [2, n, half_dim] bf16: cos rows of positions *pos0_dev + t
  *        (t < n), then the sin rows; values as in solort_rope_table.
  */

@@ -15,13 +15,18 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before ours)
 
 LIB_PATH = Path(__file__).resolve().parent / "libsolort_hip.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 # name -> (restype, argtypes); mirrors include/solort_hip.h
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "solort_abi_version": (c_int, []),
     "solort_last_error": (ctypes.c_char_p, []),
     "solort_qknorm_rope_kvwrite": (
+        c_int,
+        [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p],
+    ),
+    "solort_qknorm_rope_kvwrite_cs": (
         c_int,
         [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p,
          c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_void_p],

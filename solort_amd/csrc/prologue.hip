@@ -6,52 +6,71 @@
 // The row arithmetic (and its fixed summation order) lives in qknorm_rope.h,
 // shared with the fused decode kernel.
 //
-// Mapping: one block per token; its cos/sin are evaluated once into LDS; one
-// 16-lane group per (token, head) row of the fused qkv output, lane j holding
-// dims [8j, 8j+8) as one 16-byte vector.  Rows are the nh q heads, then nkv k
-// heads (normed + roped, written to k_cache), then nkv v heads (copied raw to
-// v_cache).
+// Mapping: one block per token; one 16-lane group per (token, head) row of
+// the fused qkv output, lane j holding dims [8j, 8j+8) as one 16-byte vector.
+// Rows are the nh q heads, then nkv k heads (normed + roped, written to
+// k_cache), then nkv v heads (copied raw to v_cache).  The token's cos/sin
+// come either from a table of the step's rows (rope_rows_kernel, the values
+// the reference computes once per forward, :111, :164, :248) or are
+// evaluated once per block into LDS from inv_freq.
 #include "common.h"
 #include "capi_internal.h"
 #include "qknorm_rope.h"
 
 namespace solort {
 
+template <bool TABLE>
 __global__ __launch_bounds__(256) void qknorm_rope_kvwrite_kernel(
     const uint16_t* __restrict__ qkv, int64_t qkv_stride, int T, int nh, int nkv,
     const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w, float eps,
-    const float* __restrict__ inv_freq, int64_t pos_limit, const int64_t* __restrict__ pos0_dev,
-    uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int64_t tok_stride,
-    int64_t head_stride) {
-  // Block = one token: its 128 cos/sin values are evaluated once (one per
-  // thread) into LDS, then the 16 slots of 16 lanes take its head rows.
-  __shared__ float s_cs[64], s_sn[64];
+    const float* __restrict__ inv_freq, const uint16_t* __restrict__ rope_cs, int64_t pos_limit,
+    const int64_t* __restrict__ pos0_dev, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
+    uint16_t* __restrict__ vc, int64_t tok_stride, int64_t head_stride) {
+  // Block = one token; the 16 slots of 16 lanes take its head rows.
   const int tid = threadIdx.x, j = tid & 15, slot = tid >> 4;
   const int t = blockIdx.x;
   const int heads = nh + 2 * nkv;
   const int64_t pos = (pos0_dev ? pos0_dev[0] : 0) + t;
   const bool pos_ok = pos >= 0 && pos < pos_limit;
-  if (tid < 128) {
-    const float ang = rope_angle(pos, inv_freq[tid >> 1]);
-    if (tid & 1) s_sn[tid >> 1] = rope_sin(ang);
-    else s_cs[tid >> 1] = rope_cos(ang);
-  }
-  __syncthreads();
   float c[8], s[8];
+  if constexpr (TABLE) {  // rope_cs [2][T][64]: this lane's 8 cos then sin values of row t
+    unpack8(*reinterpret_cast<const uint4*>(rope_cs + (int64_t)t * 64 + (j & 7) * 8), c);
+    unpack8(*reinterpret_cast<const uint4*>(rope_cs + ((int64_t)T + t) * 64 + (j & 7) * 8), s);
+  } else {  // the token's 128 cos/sin values, one per thread, through LDS
+    __shared__ float s_cs[64], s_sn[64];
+    if (tid < 128) {
+      const float ang = rope_angle(pos, inv_freq[tid >> 1]);
+      if (tid & 1) s_sn[tid >> 1] = rope_sin(ang);
+      else s_cs[tid >> 1] = rope_cos(ang);
+    }
+    __syncthreads();
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    c[i] = s_cs[(j & 7) * 8 + i];
-    s[i] = s_sn[(j & 7) * 8 + i];
+    for (int i = 0; i < 8; ++i) {
+      c[i] = s_cs[(j & 7) * 8 + i];
+      s[i] = s_sn[(j & 7) * 8 + i];
+    }
   }
-  for (int hs = slot; hs < heads; hs += 16) {  // whole 16-lane groups take a row
-    const uint4 raw = *reinterpret_cast<const uint4*>(qkv + (int64_t)t * qkv_stride + hs * SOLORT_HD + j * 8);
+  // This slot's rows hs = slot + 16 p, all loaded before any is computed (a
+  // load issued after the previous row's math would add a memory latency per
+  // row); past the last row the loads re-read it and are not used.
+  constexpr int kMaxPass = 6;  // heads <= 96
+  const uint4 wq = *reinterpret_cast<const uint4*>(qn_w + j * 8), wk = *reinterpret_cast<const uint4*>(kn_w + j * 8);
+  uint4 raws[kMaxPass];
+#pragma unroll
+  for (int p = 0; p < kMaxPass; ++p)
+    raws[p] = *reinterpret_cast<const uint4*>(qkv + (int64_t)t * qkv_stride + min(slot + 16 * p, heads - 1) * SOLORT_HD +
+                                              j * 8);
+#pragma unroll
+  for (int p = 0; p < kMaxPass; ++p) {  // whole 16-lane groups take a row
+    const int hs = slot + 16 * p;
+    if (hs >= heads) break;
+    const uint4 raw = raws[p];
     if (hs >= nh + nkv) {  // V rows: raw copy (V is neither normed nor roped)
       if (pos_ok)
         *reinterpret_cast<uint4*>(vc + pos * tok_stride + (int64_t)(hs - nh - nkv) * head_stride + j * 8) = raw;
       continue;
     }
-    const uint16_t* w = (hs < nh) ? qn_w : kn_w;
-    const uint4 ov = qknorm_rope_row(raw, *reinterpret_cast<const uint4*>(w + j * 8), c, s, eps, j);
+    const uint4 ov = qknorm_rope_row(raw, hs < nh ? wq : wk, c, s, eps, j);
     if (hs < nh) {
       *reinterpret_cast<uint4*>(q_out + ((int64_t)t * nh + hs) * SOLORT_HD + j * 8) = ov;
     } else if (pos_ok) {
@@ -64,29 +83,54 @@ __global__ __launch_bounds__(256) void qknorm_rope_kvwrite_kernel(
 
 using namespace solort;
 
+// Checks shared by both entry points.
+static int check_prologue(const char* name, const void* qkv, int64_t qkv_row_stride, int T, int nh, int nkv, int hd,
+                          const void* qn_w, const void* kn_w, const void* rope_src, const void* q_out,
+                          const void* k_cache, const void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride,
+                          int64_t max_len) {
+  if (hd != SOLORT_HD) return set_error(SOLORT_EINVAL, "%s: head_dim %d != 128", name, hd);
+  if (T < 0 || nh <= 0 || nkv <= 0 || nh % nkv != 0)
+    return set_error(SOLORT_EINVAL, "%s: bad shape T=%d nh=%d nkv=%d", name, T, nh, nkv);
+  if (!qkv || !qn_w || !kn_w || !rope_src || !q_out || !k_cache || !v_cache)
+    return set_error(SOLORT_EINVAL, "%s: null pointer", name);
+  if (!aligned16(qkv) || !aligned16(qn_w) || !aligned16(kn_w) || !aligned16(rope_src) || !aligned16(q_out) ||
+      !aligned16(k_cache) || !aligned16(v_cache))
+    return set_error(SOLORT_EINVAL, "%s: pointers must be 16-byte aligned", name);
+  if (qkv_row_stride < (int64_t)(nh + 2 * nkv) * hd || qkv_row_stride % 8 != 0)
+    return set_error(SOLORT_EINVAL, "%s: qkv_row_stride %lld", name, (long long)qkv_row_stride);
+  if (kv_tok_stride % 8 != 0 || kv_head_stride % 8 != 0 || kv_tok_stride <= 0 || kv_head_stride <= 0)
+    return set_error(SOLORT_EINVAL, "%s: KV strides must be positive multiples of 8", name);
+  if (max_len <= 0) return set_error(SOLORT_EINVAL, "%s: max_len must be positive", name);
+  if (nh + 2 * nkv > 96) return set_error(SOLORT_EINVAL, "%s: %d head rows exceed 96", name, nh + 2 * nkv);
+  return 0;
+}
+
 extern "C" int solort_qknorm_rope_kvwrite(const void* qkv, int64_t qkv_row_stride, int T, int nh,
                                           int nkv, int hd, const void* qn_w, const void* kn_w,
                                           float eps, const float* inv_freq, const int64_t* pos0_dev,
                                           void* q_out, void* k_cache, void* v_cache, int64_t kv_tok_stride,
                                           int64_t kv_head_stride, int64_t max_len, solort_stream_t stream) {
-  if (hd != SOLORT_HD) return set_error(SOLORT_EINVAL, "qknorm_rope_kvwrite: head_dim %d != 128", hd);
-  if (T < 0 || nh <= 0 || nkv <= 0 || nh % nkv != 0)
-    return set_error(SOLORT_EINVAL, "qknorm_rope_kvwrite: bad shape T=%d nh=%d nkv=%d", T, nh, nkv);
-  if (!qkv || !qn_w || !kn_w || !inv_freq || !q_out || !k_cache || !v_cache)
-    return set_error(SOLORT_EINVAL, "qknorm_rope_kvwrite: null pointer");
-  if (!aligned16(qkv) || !aligned16(qn_w) || !aligned16(kn_w) || !aligned16(inv_freq) || !aligned16(q_out) ||
-      !aligned16(k_cache) || !aligned16(v_cache))
-    return set_error(SOLORT_EINVAL, "qknorm_rope_kvwrite: pointers must be 16-byte aligned");
-  if (qkv_row_stride < (int64_t)(nh + 2 * nkv) * hd || qkv_row_stride % 8 != 0)
-    return set_error(SOLORT_EINVAL, "qknorm_rope_kvwrite: qkv_row_stride %lld", (long long)qkv_row_stride);
-  if (kv_tok_stride % 8 != 0 || kv_head_stride % 8 != 0 || kv_tok_stride <= 0 || kv_head_stride <= 0)
-    return set_error(SOLORT_EINVAL, "qknorm_rope_kvwrite: KV strides must be positive multiples of 8");
-  if (max_len <= 0) return set_error(SOLORT_EINVAL, "qknorm_rope_kvwrite: max_len must be positive");
-  if (T == 0) return 0;
-  if (T > 0x7fffffff) return set_error(SOLORT_EINVAL, "qknorm_rope_kvwrite: too many rows");
-  hipLaunchKernelGGL(qknorm_rope_kvwrite_kernel, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
+  int rc = check_prologue("qknorm_rope_kvwrite", qkv, qkv_row_stride, T, nh, nkv, hd, qn_w, kn_w, inv_freq, q_out,
+                          k_cache, v_cache, kv_tok_stride, kv_head_stride, max_len);
+  if (rc || T == 0) return rc;
+  hipLaunchKernelGGL(qknorm_rope_kvwrite_kernel<false>, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)qkv, qkv_row_stride, T, nh, nkv, (const uint16_t*)qn_w,
-                     (const uint16_t*)kn_w, eps, inv_freq, max_len, pos0_dev, (uint16_t*)q_out,
-                     (uint16_t*)k_cache, (uint16_t*)v_cache, kv_tok_stride, kv_head_stride);
+                     (const uint16_t*)kn_w, eps, inv_freq, (const uint16_t*)nullptr, max_len, pos0_dev,
+                     (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, kv_tok_stride, kv_head_stride);
   return check_launch("qknorm_rope_kvwrite");
+}
+
+extern "C" int solort_qknorm_rope_kvwrite_cs(const void* qkv, int64_t qkv_row_stride, int T, int nh, int nkv,
+                                             int hd, const void* qn_w, const void* kn_w, float eps,
+                                             const void* rope_cs, const int64_t* pos0_dev, void* q_out,
+                                             void* k_cache, void* v_cache, int64_t kv_tok_stride,
+                                             int64_t kv_head_stride, int64_t max_len, solort_stream_t stream) {
+  int rc = check_prologue("qknorm_rope_kvwrite_cs", qkv, qkv_row_stride, T, nh, nkv, hd, qn_w, kn_w, rope_cs,
+                          q_out, k_cache, v_cache, kv_tok_stride, kv_head_stride, max_len);
+  if (rc || T == 0) return rc;
+  hipLaunchKernelGGL(qknorm_rope_kvwrite_kernel<true>, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
+                     (const uint16_t*)qkv, qkv_row_stride, T, nh, nkv, (const uint16_t*)qn_w,
+                     (const uint16_t*)kn_w, eps, (const float*)nullptr, (const uint16_t*)rope_cs, max_len, pos0_dev,
+                     (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, kv_tok_stride, kv_head_stride);
+  return check_launch("qknorm_rope_kvwrite_cs");
 }

@@ -54,7 +54,7 @@ using namespace solort;
 extern "C" int solort_rope_rows(const float* inv_freq, int half_dim, const int64_t* pos0_dev, int n, void* cs_out,
                                 solort_stream_t stream) {
   if (!inv_freq || !pos0_dev || !cs_out) return set_error(SOLORT_EINVAL, "rope_rows: null pointer");
-  if (half_dim < 1 || half_dim > 1024 || n < 1 || n > 64)
+  if (half_dim < 1 || half_dim > 1024 || n < 1 || n > (1 << 20))
     return set_error(SOLORT_EINVAL, "rope_rows: bad shape half_dim=%d n=%d", half_dim, n);
   const int total = 2 * n * half_dim;
   hipLaunchKernelGGL(rope_rows_kernel, dim3((total + 255) / 256), dim3(256), 0, (hipStream_t)stream, inv_freq,

@@ -138,6 +138,36 @@ def qknorm_rope_kvwrite(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tenso
     _lib.check(rc, "qknorm_rope_kvwrite")
 
 
+def qknorm_rope_kvwrite_cs(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps: float,
+                           rope_cs: torch.Tensor, pos0: torch.Tensor | None, q_out: torch.Tensor,
+                           k_cache: torch.Tensor, v_cache: torch.Tensor, nh: int, nkv: int) -> None:
+    """qknorm_rope_kvwrite with this step's cos/sin rows given: rope_cs = rope_rows(inv_f, pos0, T).
+    Bit-identical results; see solort_qknorm_rope_kvwrite_cs."""
+    _on_gpu("qkv", qkv, torch.bfloat16)
+    _need(qkv.dim() == 2 and qkv.shape[1] == (nh + 2 * nkv) * HD and qkv.stride(1) == 1,
+          f"qkv must be [T, {(nh + 2 * nkv) * HD}] with unit column stride")
+    T = qkv.shape[0]
+    for name, w in (("qn_w", qn_w), ("kn_w", kn_w)):
+        _on_gpu(name, w, torch.bfloat16)
+        _need(w.shape == (HD,) and w.is_contiguous(), f"{name} must be [{HD}] contiguous")
+    _rope_rows_ok(rope_cs, T)
+    _on_gpu("q_out", q_out, torch.bfloat16)
+    _need(q_out.shape == (T, nh, HD) and q_out.is_contiguous(), f"q_out must be [{T}, {nh}, {HD}]")
+    ts, hs, max_len = _cache_strides("k_cache", k_cache, nkv)
+    _need(v_cache.shape == k_cache.shape and v_cache.stride() == k_cache.stride(),
+          "v_cache must match k_cache in shape and strides")
+    _on_gpu("v_cache", v_cache, torch.bfloat16)
+    pos_ptr = None
+    if pos0 is not None:
+        _need(pos0.is_cuda and pos0.dtype == torch.int64 and pos0.numel() >= 1, "pos0 must be int64 on the device")
+        pos_ptr = pos0.data_ptr()
+    rc = _lib.load().solort_qknorm_rope_kvwrite_cs(
+        qkv.data_ptr(), qkv.stride(0), T, nh, nkv, HD, qn_w.data_ptr(), kn_w.data_ptr(), float(eps),
+        rope_cs.data_ptr(), pos_ptr, q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), ts, hs, max_len,
+        _stream(qkv))
+    _lib.check(rc, "qknorm_rope_kvwrite_cs")
+
+
 def attn_workspace(nq: int, nh: int, nkv: int, n_split: int, device: torch.device | str) -> torch.Tensor:
     """Workspace for decode_attn / verify_attn / decode_layer (the splits' partials; allocate once,
     reuse for any call with no larger nq or n_split)."""

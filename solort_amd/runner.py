@@ -97,6 +97,8 @@ class GraphQwen3Attention:
         pmax = self.pre_buckets[-1]
         self.qkv_pre = torch.zeros(layers, pmax, self.width, dtype=torch.bfloat16, device=self.dev)
         self.q_pre = torch.zeros(pmax, nh, HD, dtype=torch.bfloat16, device=self.dev)
+        self.zero_pos = torch.zeros(1, dtype=torch.long, device=self.dev)  # prefill positions start at 0
+        self.cs_pre = torch.zeros(2 * pmax * (HD // 2), dtype=torch.bfloat16, device=self.dev)  # step cos/sin
         self.ctx_pre = torch.zeros(layers, pmax, nh * HD, dtype=torch.bfloat16, device=self.dev)
         self._pre_graphs: dict[int, torch.cuda.CUDAGraph] = {}
 
@@ -150,9 +152,11 @@ class GraphQwen3Attention:
 
     def _prefill_forward(self, bound: int) -> None:
         """cuda_graph_executor.py:109-130 (attention part): rows 0..bound-1 at positions 0..bound-1."""
+        cs = self.cs_pre[: 2 * bound * (HD // 2)].view(2, bound, HD // 2)
+        ops.rope_rows(self.inv_freq, self.zero_pos, bound, cs)  # cos/sin once per step (:111)
         for li in range(self.L):
-            ops.qknorm_rope_kvwrite(self.qkv_pre[li, :bound], self.qn_w[li], self.kn_w[li], self.eps, self.inv_freq,
-                                    None, self.q_pre[:bound], self.kc[li], self.vc[li], self.nh, self.nkv)
+            ops.qknorm_rope_kvwrite_cs(self.qkv_pre[li, :bound], self.qn_w[li], self.kn_w[li], self.eps, cs, None,
+                                       self.q_pre[:bound], self.kc[li], self.vc[li], self.nh, self.nkv)
             ops.prefill_attn(self.q_pre[:bound], self.kc[li], self.vc[li], self.scale, self.ctx_pre[li, :bound])
 
     def prefill(self, qkv: torch.Tensor) -> torch.Tensor:

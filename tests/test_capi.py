@@ -82,6 +82,12 @@ def test_prologue_and_argmax_reject_bad_arguments(lib):
     rc = lib.solort_qknorm_rope_kvwrite(p, 6000, 1, 32, 8, 128, p, p, 1e-6, p, None, p, p, p, 1024, 128, 1024,
                                         None)
     assert rc == EINVAL and "stride" in _err(lib)
+    rc = lib.solort_qknorm_rope_kvwrite_cs(p, 6144, 4, 32, 8, 128, p, p, 1e-6, None, None, p, p, p, 1024, 128,
+                                           1024, None)
+    assert rc == EINVAL and "null" in _err(lib)
+    rc = lib.solort_qknorm_rope_kvwrite_cs(p, 6144, 4, 30, 8, 128, p, p, 1e-6, p, None, p, p, p, 1024, 128, 1024,
+                                           None)
+    assert rc == EINVAL and "shape" in _err(lib)
     rc = lib.solort_decode_layer(p, 6144, 1, 32, 8, 128, p, p, 1e-6, None, p, p, p, 1024, 128, 1024, 1024, 0.088,
                                  p, 32, p, 0, None)
     assert rc == EINVAL and "null" in _err(lib)

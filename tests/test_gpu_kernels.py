@@ -206,6 +206,36 @@ def test_prologue_prefill_rows_bitexact(gpu):
     assert torch.equal(vc.cpu()[:case.T], torch.from_numpy(vx).to(torch.bfloat16))
 
 
+@pytest.mark.parametrize("T,pos0", [(1024, None), (5, 2048), (1, 32767)])
+def test_prologue_with_step_table_equals_in_kernel_cos_sin(gpu, T, pos0):
+    """qknorm_rope_kvwrite_cs (cos/sin rows from rope_rows, once per step) writes the same q, K and V
+    bits as qknorm_rope_kvwrite (cos/sin evaluated in the kernel)."""
+    dev = gpu
+    sh = wl.QWEN3_4B
+    g = torch.Generator().manual_seed(77 + T)
+    qkv = torch.randn(T, sh.qkv_width, generator=g).to(torch.bfloat16).to(dev)
+    qn = (1 + 0.1 * torch.randn(HD, generator=g)).to(torch.bfloat16).to(dev)
+    kn = (1 + 0.1 * torch.randn(HD, generator=g)).to(torch.bfloat16).to(dev)
+    max_len = 32768
+    p0 = 0 if pos0 is None else pos0
+    pos = torch.tensor([p0], dtype=torch.long, device=dev)
+    outs = []
+    for use_table in (False, True):
+        kc = torch.zeros(max_len, sh.nkv, HD, dtype=torch.bfloat16, device=dev)
+        vc = torch.zeros_like(kc)
+        q = torch.empty(T, sh.nh, HD, dtype=torch.bfloat16, device=dev)
+        pos_arg = None if pos0 is None else pos
+        if use_table:
+            cs = ops.rope_rows(_ifr(dev), pos, T)
+            ops.qknorm_rope_kvwrite_cs(qkv, qn, kn, wl.EPS, cs, pos_arg, q, kc, vc, sh.nh, sh.nkv)
+        else:
+            ops.qknorm_rope_kvwrite(qkv, qn, kn, wl.EPS, _ifr(dev), pos_arg, q, kc, vc, sh.nh, sh.nkv)
+        torch.cuda.synchronize()
+        outs.append((q.cpu(), kc[p0:p0 + T].cpu(), vc[p0:p0 + T].cpu()))
+    for a, b in zip(outs[0], outs[1]):
+        assert torch.equal(a.view(torch.int16), b.view(torch.int16))
+
+
 def test_prologue_skips_out_of_range_positions(gpu):
     dev = gpu
     kc = torch.full((64, 8, HD), 7.0, dtype=torch.bfloat16, device=dev)
