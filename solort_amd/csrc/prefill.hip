@@ -46,16 +46,6 @@ namespace solort {
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
-struct PrefillArgs {
-  const uint16_t* q;  // [T][nh][128]
-  const uint16_t* kc;
-  const uint16_t* vc;
-  int64_t tok_stride, head_stride;
-  void* out;     // [T][nh * 128]
-  float qscale;  // softmax scale * log2(e)
-  int T, nh, nkv, n_qtiles, out_f32;
-};
-
 constexpr int kThreads = 512;      // 8 wavefronts
 constexpr int kKeys = 64;          // keys per wave per iteration
 constexpr int kStage = 2 * kKeys;  // keys staged per iteration
@@ -125,7 +115,15 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
 }
 
 template <int G>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(const PrefillArgs a) {
+// Scalar arguments, in the order the prologue needs them: the leading ones
+// arrive preloaded in SGPRs (-amdgpu-kernarg-preload-count), so the first
+// loads issue without a kernel-argument round trip.  q [T][nh][128]; out
+// [T][nh * 128]; qscale = softmax scale * log2(e).
+__global__ __launch_bounds__(kThreads) void prefill_kernel(const uint16_t* __restrict__ q,
+                                                           const uint16_t* __restrict__ kc,
+                                                           const uint16_t* __restrict__ vc, int T, int nkv,
+                                                           int n_qtiles, int tok_stride, int head_stride, int nh,
+                                                           float qscale, void* __restrict__ out_ptr, int out_f32) {
   constexpr int PB = 32 * (4 / G);  // positions per block
   __shared__ __align__(16) uint16_t sK[2][kStage * kKStride];
   __shared__ __align__(16) uint16_t sV[2][kStage * kVStride];
@@ -133,30 +131,29 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const PrefillArgs a) 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int kh = wave >> 2, ww = wave & 3;
   const int l32 = lane & 31, hi = lane >> 5;
-  const int kvh = blockIdx.x % a.nkv;
-  const int tile = a.n_qtiles - 1 - (int)(blockIdx.x / a.nkv);  // heaviest first
+  const int kvh = blockIdx.x % nkv;
+  const int tile = n_qtiles - 1 - (int)(blockIdx.x / nkv);  // heaviest first
   const int p0 = tile * PB;
   const int head = kvh * G + (ww % G);
   const int pw = p0 + 32 * (ww / G);  // this wave's first position
   const int qrow = pw + l32;          // the query row of this lane's scores
-  const int T = a.T;
 
   // Q^T operand of the eight 16-dim steps: Q[qrow][16 kk + 8 hi .. +7].
   bf16x8 qb[8];
   {
-    const uint16_t* qp = a.q + ((int64_t)min(qrow, T - 1) * a.nh + head) * SOLORT_HD + 8 * hi;
+    const uint16_t* qp = q + ((int64_t)min(qrow, T - 1) * nh + head) * SOLORT_HD + 8 * hi;
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) qb[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 16 * kk));
   }
 
-  const uint16_t* kbase = a.kc + (int64_t)kvh * a.head_stride;
-  const uint16_t* vbase = a.vc + (int64_t)kvh * a.head_stride;
+  const uint16_t* kbase = kc + kvh * head_stride;
+  const uint16_t* vbase = vc + kvh * head_stride;
   const int kend = min(T, p0 + PB);    // keys the block reads
   const int kend_w = min(T, pw + 32);  // keys this wave attends (wave-uniform)
   const int nit = (kend + kStage - 1) / kStage;
   const int r0 = tid >> 4, ch = tid & 15;  // staging: key rows r0 + 32i, dims 8ch..8ch+7
-  const __amdgpu_buffer_rsrc_t krs = kv_rsrc(kbase, T, a.tok_stride), vrs = kv_rsrc(vbase, T, a.tok_stride);
-  const int ts2 = (int)a.tok_stride * 2;  // bytes per key row
+  const __amdgpu_buffer_rsrc_t krs = kv_rsrc(kbase, T, tok_stride), vrs = kv_rsrc(vbase, T, tok_stride);
+  const int ts2 = tok_stride * 2;  // bytes per key row
   int voff[4];
 #pragma unroll
   for (int i = 0; i < 4; ++i) voff[i] = (r0 + 32 * i) * ts2 + ch * 16;
@@ -165,7 +162,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const PrefillArgs a) 
 #pragma unroll
   for (int dt = 0; dt < 4; ++dt) o[dt] = f32x16{};
   float m = -INFINITY, lsum = 0.f;  // running max of raw scores; this lane's share of the row sum
-  const float qs = a.qscale;
+  const float qs = qscale;
 
   // The next staged block's loads fly while this one is computed.  Fetches
   // past the last block are issued anyway (buffer loads beyond the head's
@@ -290,24 +287,45 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const PrefillArgs a) 
 
   const float lt = xor32_combine(lsum, [](float x, float y) { return x + y; });  // both halves of the row
   const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  if (qrow < T) {
-    const int64_t base = ((int64_t)qrow * a.nh + head) * SOLORT_HD + 4 * hi;
+  // Normalise and store through this wave's LDS area (its merge reads above
+  // come first in program order): lane (l32, hi) holds dims 32dt + 8g + 4hi
+  // .. +3 of row l32, the tile goes to LDS row-major, and each store
+  // instruction then writes whole 256-byte (bf16) or 512-byte (fp32) rows.
+  const int64_t orow = (int64_t)nh * SOLORT_HD;  // elements per output row
+  if (out_f32) {
+    constexpr int kOS = SOLORT_HD + 4;  // 528-byte rows: 32 * 132 floats fill the [66][64] area
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+      for (int g = 0; g < 4; ++g)
+        *reinterpret_cast<float4*>(xf + l32 * kOS + 32 * dt + 8 * g + 4 * hi) =
+            make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+    float* out = reinterpret_cast<float*>(out_ptr) + (int64_t)head * SOLORT_HD;
+#pragma unroll
+    for (int it = 0; it < 16; ++it) {
+      const int r = 2 * it + (lane >> 5), c = 4 * (lane & 31);
+      const float4 v = *reinterpret_cast<const float4*>(xf + r * kOS + c);
+      if (pw + r < T) *reinterpret_cast<float4*>(out + (pw + r) * orow + c) = v;
+    }
+  } else {
+    constexpr int kOS = SOLORT_HD + 8;  // 272-byte rows
+    uint16_t* xo = reinterpret_cast<uint16_t*>(xf);
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const float4 v = make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv,
-                                     o[dt][4 * g + 3] * inv);
-        const int64_t oi = base + 32 * dt + 8 * g;
-        if (a.out_f32) {
-          *reinterpret_cast<float4*>(reinterpret_cast<float*>(a.out) + oi) = v;
-        } else {
-          uint2 pkd;
-          pkd.x = pack2(v.x, v.y);
-          pkd.y = pack2(v.z, v.w);
-          *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.out) + oi) = pkd;
-        }
+        uint2 pkd;
+        pkd.x = pack2(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv);
+        pkd.y = pack2(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
+        *reinterpret_cast<uint2*>(xo + l32 * kOS + 32 * dt + 8 * g + 4 * hi) = pkd;
       }
+    uint16_t* out = reinterpret_cast<uint16_t*>(out_ptr) + (int64_t)head * SOLORT_HD;
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int r = 4 * it + (lane >> 4), c = 8 * (lane & 15);
+      const uint4 v = *reinterpret_cast<const uint4*>(xo + r * kOS + c);
+      if (pw + r < T) *reinterpret_cast<uint4*>(out + (pw + r) * orow + c) = v;
+    }
   }
 }
 
@@ -340,27 +358,28 @@ extern "C" int solort_prefill_attn(const void* q, int T, int nh, int nkv, int hd
   if (((int64_t)T + 4 * kStage) * kv_tok_stride * 2 >= ((int64_t)1 << 31))
     return set_error(SOLORT_EINVAL, "%s: T=%d rows of stride %lld exceed 32-bit byte offsets", name, T,
                      (long long)kv_tok_stride);
-  PrefillArgs a;
-  a.q = (const uint16_t*)q;
-  a.kc = (const uint16_t*)k_cache;
-  a.vc = (const uint16_t*)v_cache;
-  a.tok_stride = kv_tok_stride;
-  a.head_stride = kv_head_stride;
-  a.out = out;
-  a.qscale = scale * 1.4426950408889634f;
-  a.T = T;
-  a.nh = nh;
-  a.nkv = nkv;
-  a.out_f32 = out_dtype == SOLORT_DTYPE_F32;
+  // The kernel takes 32-bit strides: every K/V row it addresses lies within
+  // 2^31 bytes of its head's row 0 (checked above) and the heads' offsets
+  // within 2^31 elements of the cache base.
+  if ((int64_t)nkv * kv_head_stride >= ((int64_t)1 << 31))
+    return set_error(SOLORT_EINVAL, "%s: KV head stride %lld exceeds 32-bit offsets", name,
+                     (long long)kv_head_stride);
   const int pb = 32 * (4 / G);  // positions per block
-  a.n_qtiles = (T + pb - 1) / pb;
-  const int64_t blocks = (int64_t)a.n_qtiles * nkv;
+  const int n_qtiles = (T + pb - 1) / pb;
+  const int64_t blocks = (int64_t)n_qtiles * nkv;
   if (blocks > 0x7fffffff) return set_error(SOLORT_EINVAL, "%s: too many tiles", name);
   hipStream_t s = (hipStream_t)stream;
+  const float qscale = scale * 1.4426950408889634f;
+  const int f32 = out_dtype == SOLORT_DTYPE_F32;
+#define SOLORT_PREFILL_LAUNCH(GG)                                                                           \
+  hipLaunchKernelGGL(prefill_kernel<GG>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (const uint16_t*)q,   \
+                     (const uint16_t*)k_cache, (const uint16_t*)v_cache, T, nkv, n_qtiles, (int)kv_tok_stride, \
+                     (int)kv_head_stride, nh, qscale, out, f32)
   switch (G) {
-    case 1: hipLaunchKernelGGL(prefill_kernel<1>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a); break;
-    case 2: hipLaunchKernelGGL(prefill_kernel<2>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a); break;
-    case 4: hipLaunchKernelGGL(prefill_kernel<4>, dim3((unsigned)blocks), dim3(kThreads), 0, s, a); break;
+    case 1: SOLORT_PREFILL_LAUNCH(1); break;
+    case 2: SOLORT_PREFILL_LAUNCH(2); break;
+    case 4: SOLORT_PREFILL_LAUNCH(4); break;
   }
+#undef SOLORT_PREFILL_LAUNCH
   return check_launch(name);
 }
