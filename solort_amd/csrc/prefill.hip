@@ -114,17 +114,18 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
-template <int G>
-// Scalar arguments, in the order the prologue needs them: the leading ones
-// arrive preloaded in SGPRs (-amdgpu-kernarg-preload-count), so the first
-// loads issue without a kernel-argument round trip.  q [T][nh][128]; out
-// [T][nh * 128]; qscale = softmax scale * log2(e).
+// Scalar arguments: all of them (13 SGPRs) arrive preloaded
+// (-amdgpu-kernarg-preload-count), so neither the first loads nor the final
+// stores wait for a kernel-argument load.  q [T][nh][128]; out [T][nh * 128]
+// in fp32 (F32) or bf16; qscale = softmax scale * log2(e).
+template <int G, bool F32>
 __global__ __launch_bounds__(kThreads) void prefill_kernel(const uint16_t* __restrict__ q,
                                                            const uint16_t* __restrict__ kc,
                                                            const uint16_t* __restrict__ vc, int T, int nkv,
-                                                           int n_qtiles, int tok_stride, int head_stride, int nh,
-                                                           float qscale, void* __restrict__ out_ptr, int out_f32) {
+                                                           int tok_stride, int head_stride, float qscale,
+                                                           void* __restrict__ out_ptr) {
   constexpr int PB = 32 * (4 / G);  // positions per block
+  const int nh = nkv * G, n_qtiles = (T + PB - 1) / PB;
   __shared__ __align__(16) uint16_t sK[2][kStage * kKStride];
   __shared__ __align__(16) uint16_t sV[2][kStage * kVStride];
 
@@ -138,12 +139,15 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const uint16_t* __res
   const int pw = p0 + 32 * (ww / G);  // this wave's first position
   const int qrow = pw + l32;          // the query row of this lane's scores
 
-  // Q^T operand of the eight 16-dim steps: Q[qrow][16 kk + 8 hi .. +7].
-  bf16x8 qb[8];
-  {
-    const uint16_t* qp = q + ((int64_t)min(qrow, T - 1) * nh + head) * SOLORT_HD + 8 * hi;
+  // The block's four 32-row Q tiles (one per wave of a key half), loaded
+  // coalesced: thread t takes row t / 16, bytes 16 (t % 16) .. +15 of each
+  // tile (rows past T repeat row T-1).  They pass through the second K buffer.
+  uint4 qv[4];
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk) qb[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(qp + 16 * kk));
+  for (int w = 0; w < 4; ++w) {
+    const int pos = min(p0 + 32 * (w / G) + (tid >> 4), T - 1);
+    qv[w] = *reinterpret_cast<const uint4*>(q + ((int64_t)pos * nh + kvh * G + (w % G)) * SOLORT_HD +
+                                           8 * (tid & 15));
   }
 
   const uint16_t* kbase = kc + kvh * head_stride;
@@ -164,17 +168,24 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const uint16_t* __res
   float m = -INFINITY, lsum = 0.f;  // running max of raw scores; this lane's share of the row sum
   const float qs = qscale;
 
-  // The next staged block's loads fly while this one is computed.  Fetches
-  // past the last block are issued anyway (buffer loads beyond the head's
-  // rows return zeros), so every fetch and stage is unconditional and each
-  // stage waits only for the loads it consumes.
+  // The next staged block's loads fly while this one is computed; buffer
+  // loads beyond the head's rows return zeros.
   Staged st = prefill_fetch(krs, vrs, voff, 0);
+#pragma unroll
+  for (int w = 0; w < 4; ++w)
+    *reinterpret_cast<uint4*>(&sK[1][(32 * w + (tid >> 4)) * kKStride + 8 * (tid & 15)]) = qv[w];
   prefill_stage(st, sK[0], sV[0], r0, ch);
-  // Every load issued so far (q and block 0) is complete past this point, so
+  // Every load issued so far (Q and block 0) is complete past this point, so
   // the loop's waits count only the staged block in flight.
   __builtin_amdgcn_s_waitcnt(0);
   lds_barrier();
-  st = prefill_fetch(krs, vrs, voff, kStage * ts2);
+  if (nit > 1) st = prefill_fetch(krs, vrs, voff, kStage * ts2);
+  // Q^T operand of the eight 16-dim steps: Q[qrow][16 kk + 8 hi .. +7].
+  bf16x8 qb[8];
+#pragma unroll
+  for (int kk = 0; kk < 8; ++kk)
+    qb[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(&sK[1][(32 * ww + l32) * kKStride + 16 * kk + 8 * hi]));
+  lds_barrier();  // every wave holds its Q before the first iteration restages this buffer
 
   for (int j = 0; j < nit; ++j) {
     const int buf = j & 1;
@@ -255,10 +266,12 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const uint16_t* __res
         }
       }
   }
-    // buffer (j+1)%2 was last read before the previous barrier
-    prefill_stage(st, sK[(j + 1) & 1], sV[(j + 1) & 1], r0, ch);
+    // The last block stages and fetches nothing: a load left in flight would
+    // hold the epilogue (its registers cannot be reused before it lands).  Its
+    // barrier stays: the merge below reuses the staging buffers.
+    if (j + 1 < nit) prefill_stage(st, sK[(j + 1) & 1], sV[(j + 1) & 1], r0, ch);  // block-uniform
     lds_barrier();  // orders the LDS tiles only: the loads below stay in flight
-    st = prefill_fetch(krs, vrs, voff, (j + 2) * kStage * ts2);
+    if (j + 2 < nit) st = prefill_fetch(krs, vrs, voff, (j + 2) * kStage * ts2);
   }
 
   // Merge the two key halves of every row: half 1 hands (m, l, O) to half 0
@@ -292,7 +305,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const uint16_t* __res
   // .. +3 of row l32, the tile goes to LDS row-major, and each store
   // instruction then writes whole 256-byte (bf16) or 512-byte (fp32) rows.
   const int64_t orow = (int64_t)nh * SOLORT_HD;  // elements per output row
-  if (out_f32) {
+  if constexpr (F32) {
     constexpr int kOS = SOLORT_HD + 4;  // 528-byte rows: 32 * 132 floats fill the [66][64] area
 #pragma unroll
     for (int dt = 0; dt < 4; ++dt)
@@ -370,15 +383,18 @@ extern "C" int solort_prefill_attn(const void* q, int T, int nh, int nkv, int hd
   if (blocks > 0x7fffffff) return set_error(SOLORT_EINVAL, "%s: too many tiles", name);
   hipStream_t s = (hipStream_t)stream;
   const float qscale = scale * 1.4426950408889634f;
-  const int f32 = out_dtype == SOLORT_DTYPE_F32;
-#define SOLORT_PREFILL_LAUNCH(GG)                                                                           \
-  hipLaunchKernelGGL(prefill_kernel<GG>, dim3((unsigned)blocks), dim3(kThreads), 0, s, (const uint16_t*)q,   \
-                     (const uint16_t*)k_cache, (const uint16_t*)v_cache, T, nkv, n_qtiles, (int)kv_tok_stride, \
-                     (int)kv_head_stride, nh, qscale, out, f32)
-  switch (G) {
-    case 1: SOLORT_PREFILL_LAUNCH(1); break;
-    case 2: SOLORT_PREFILL_LAUNCH(2); break;
-    case 4: SOLORT_PREFILL_LAUNCH(4); break;
+  const bool f32 = out_dtype == SOLORT_DTYPE_F32;
+#define SOLORT_PREFILL_LAUNCH(GG, FF)                                                                           \
+  hipLaunchKernelGGL((prefill_kernel<GG, FF>), dim3((unsigned)blocks), dim3(kThreads), 0, s, (const uint16_t*)q, \
+                     (const uint16_t*)k_cache, (const uint16_t*)v_cache, T, nkv, (int)kv_tok_stride,             \
+                     (int)kv_head_stride, qscale, out)
+  switch (G * 2 + (f32 ? 1 : 0)) {
+    case 2: SOLORT_PREFILL_LAUNCH(1, false); break;
+    case 3: SOLORT_PREFILL_LAUNCH(1, true); break;
+    case 4: SOLORT_PREFILL_LAUNCH(2, false); break;
+    case 5: SOLORT_PREFILL_LAUNCH(2, true); break;
+    case 8: SOLORT_PREFILL_LAUNCH(4, false); break;
+    case 9: SOLORT_PREFILL_LAUNCH(4, true); break;
   }
 #undef SOLORT_PREFILL_LAUNCH
   return check_launch(name);
