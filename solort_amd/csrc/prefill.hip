@@ -51,6 +51,8 @@ constexpr int kKeys = 64;          // keys per wave per iteration
 constexpr int kStage = 2 * kKeys;  // keys staged per iteration
 constexpr int kKStride = 128 + 8;   // K tile row stride (bf16): 272 B, conflict-free 16-byte reads
 constexpr int kVStride = 128 + 16;  // V tile row stride (bf16): 288 B, conflict-free transposing reads
+constexpr int kKAhead = 6;          // K operand reads in flight ahead of the score MFMAs
+constexpr int kVAhead = 6;          // V operand reads in flight ahead of the P V MFMAs
 
 __device__ __forceinline__ bf16x8 as_bf16x8(const uint4 v) { return __builtin_bit_cast(bf16x8, v); }
 
@@ -190,17 +192,37 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const uint16_t* __res
   for (int j = 0; j < nit; ++j) {
     const int buf = j & 1;
     const int k0 = j * kStage + kh * kKeys;  // this half's 64 keys
+    const uint16_t* vb;
+    uint2 vlo[16], vup[16];
     if (k0 < kend_w) {  // wave-uniform
       // S^T for the 64 keys: s[kt][i] = score of key k0 + 32kt + 8(i/4) + 4hi + i%4.
       f32x16 s[2] = {f32x16{}, f32x16{}};
       const uint16_t* kr = &sK[buf][(kh * kKeys + l32) * kKStride + 8 * hi];
+      // Step g = (kk, kt) = (g / 2, g % 2), two independent accumulation
+      // chains; the K operand of step g+kKAhead is read before MFMA g issues,
+      // so LDS latency hides behind the MFMAs in between.
+      bf16x8 ka[16];
 #pragma unroll
-      for (int kk = 0; kk < 8; ++kk)
+      for (int g = 0; g < kKAhead; ++g)
+        ka[g] = as_bf16x8(*reinterpret_cast<const uint4*>(kr + (g & 1) * 32 * kKStride + 16 * (g >> 1)));
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {  // two independent accumulation chains
-          const bf16x8 ka = as_bf16x8(*reinterpret_cast<const uint4*>(kr + kt * 32 * kKStride + 16 * kk));
-          s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka, qb[kk], s[kt], 0, 0, 0);
-        }
+      for (int g = 0; g < 16; ++g) {
+        if (g + kKAhead < 16)
+          ka[g + kKAhead] = as_bf16x8(*reinterpret_cast<const uint4*>(kr + ((g + kKAhead) & 1) * 32 * kKStride +
+                                                                      16 * ((g + kKAhead) >> 1)));
+        s[g & 1] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ka[g], qb[g >> 1], s[g & 1], 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      // The first V^T operands of the P V product below (independent of the
+      // softmax, whose work hides their latency).
+      vb = &sV[buf][(kh * kKeys + 4 * hi + ((lane & 15) >> 2)) * kVStride + 16 * ((lane >> 4) & 1) +
+                    4 * (lane & 3)];
+#pragma unroll
+      for (int q = 0; q < kVAhead; ++q) {
+        const uint16_t* vr = vb + (16 * (q >> 2)) * kVStride + 32 * (q & 3);
+        vlo[q] = lds_read_tr16(vr);
+        vup[q] = lds_read_tr16(vr + 8 * kVStride);
+      }
       if (k0 + kKeys - 1 > pw) {  // the block crosses this wave's diagonal: mask keys past each row
 #pragma unroll
         for (int kt = 0; kt < 2; ++kt)
@@ -248,23 +270,23 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const uint16_t* __res
     // lane 16G + jj addresses key row 4(G/2) + jj/4 (+8 for the upper four
     // keys) at dims 16(G%2) + 4(jj%4), so lane l receives dim l%32 of the
     // four keys its P^T slots hold.
-    const uint16_t* vb = &sV[buf][(kh * kKeys + 4 * hi + ((lane & 15) >> 2)) * kVStride +
-                                  16 * ((lane >> 4) & 1) + 4 * (lane & 3)];
+    // Step q = (kt, h, dt) = (q / 8, q / 4 % 2, q % 4); the V operand of step
+    // q+kVAhead is read before MFMA q issues (the first ones before the
+    // softmax above).
 #pragma unroll
-    for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const bf16x8 pb = as_bf16x8(make_uint4(pk[kt][4 * h], pk[kt][4 * h + 1], pk[kt][4 * h + 2],
-                                               pk[kt][4 * h + 3]));
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-          const uint16_t* vr = vb + (32 * kt + 16 * h) * kVStride + 32 * dt;
-          const uint2 lo = lds_read_tr16(vr);
-          const uint2 up = lds_read_tr16(vr + 8 * kVStride);
-          const bf16x8 va = as_bf16x8(make_uint4(lo.x, lo.y, up.x, up.y));
-          o[dt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, o[dt], 0, 0, 0);
-        }
+    for (int q = 0; q < 16; ++q) {
+      if (q + kVAhead < 16) {
+        const uint16_t* vr = vb + (16 * ((q + kVAhead) >> 2)) * kVStride + 32 * ((q + kVAhead) & 3);
+        vlo[q + kVAhead] = lds_read_tr16(vr);
+        vup[q + kVAhead] = lds_read_tr16(vr + 8 * kVStride);
       }
+      const int kt = q >> 3, h = (q >> 2) & 1;
+      const bf16x8 pb = as_bf16x8(make_uint4(pk[kt][4 * h], pk[kt][4 * h + 1], pk[kt][4 * h + 2],
+                                             pk[kt][4 * h + 3]));
+      const bf16x8 va = as_bf16x8(make_uint4(vlo[q].x, vlo[q].y, vup[q].x, vup[q].y));
+      o[q & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, o[q & 3], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
     // The last block stages and fetches nothing: a load left in flight would
     // hold the epilogue (its registers cannot be reused before it lands).  Its
