@@ -134,15 +134,17 @@ def test_prefill_graph_then_decode_continues(gpu):
     torch.cuda.synchronize()
     assert torch.equal(r.kc, eager_kc) and torch.equal(r.vc, eager_vc)
     assert torch.equal(ctx, out[:, :T])
-    # causal: rows < T do not depend on the zero padding rows
-    q2 = torch.empty(T, sh.nh, HD, dtype=torch.bfloat16, device=gpu)
+    # causal: rows < T do not depend on the padding rows (random rows in their place change nothing)
+    junk = padded[0].clone()
+    junk[T:] = torch.randn(512 - T, r.width, generator=g).to(torch.bfloat16) * 4
     kc2, vc2 = eager_kc.clone(), eager_vc.clone()
-    out2 = torch.empty(T, sh.nh * HD, dtype=torch.bfloat16, device=gpu)
-    ops.qknorm_rope_kvwrite(qkv[0].to(gpu), r.qn_w[0], r.kn_w[0], r.eps, r.inv_freq, None, q2, kc2[0], vc2[0],
+    out2 = torch.empty(512, sh.nh * HD, dtype=torch.bfloat16, device=gpu)
+    ops.qknorm_rope_kvwrite(junk.to(gpu), r.qn_w[0], r.kn_w[0], r.eps, r.inv_freq, None, q, kc2[0], vc2[0],
                             sh.nh, sh.nkv)
-    ops.prefill_attn(q2, kc2[0], vc2[0], r.scale, out2)
+    ops.prefill_attn(q, kc2[0], vc2[0], r.scale, out2)
     torch.cuda.synchronize()
-    assert torch.equal(out2, ctx[0])
+    assert torch.equal(out2[:T], ctx[0])
+    assert not torch.equal(out2[T:], out[0, T:])
     # decode continues at position T over the prefilled cache
     qd = torch.randn(r.L, 1, r.width, generator=g).to(torch.bfloat16)
     dctx = r.decode(qd.to(gpu), T).clone()
