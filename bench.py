@@ -332,9 +332,10 @@ def verify_extras(torch, ops, wl, runners, dev, sh) -> dict:
 
 
 def prefill_extras(torch, ops, runners, dev, sh) -> dict:
-    """Prefill attention at T in {128, 512, 1024}: the MFMA kernel alone (graph of one launch per
-    layer of every KV set, HIP events around replays) and the graphed prefill step (prologue + KV
-    write + attention, 36 layers) per layer.  Overwrites cache rows 0..T-1 of every set."""
+    """Prefill attention at T in {128, 512, 1024}: the MFMA kernel alone (solort_prefill_attn on a
+    materialised q; graph of one launch per layer of every KV set, HIP events around replays) and
+    the graphed prefill step (cos/sin rows, then per layer the K/V prologue and the attention
+    normalising q itself, 36 layers) per layer.  Overwrites cache rows 0..T-1 of every set."""
     out = {}
     stream = torch.cuda.current_stream(dev)
     gen = torch.Generator(device=dev).manual_seed(1002)
@@ -343,11 +344,20 @@ def prefill_extras(torch, ops, runners, dev, sh) -> dict:
             r.prefill((torch.randn(sh.layers, T, sh.qkv_width, generator=gen, device=dev)).to(torch.bfloat16))
         torch.cuda.synchronize()
         outs = [torch.empty(T, sh.nh * 128, dtype=torch.bfloat16, device=dev) for _ in range(2)]
+        # the attention kernel alone reads a materialised q: layer 0's, from the prompt just
+        # prefilled (the prologue rewrites the same cache rows with the same values)
+        qs = []
+        for r in runners:
+            q = torch.empty(T, sh.nh, 128, dtype=torch.bfloat16, device=dev)
+            cs = ops.rope_rows(r.inv_freq, r.zero_pos, T)
+            ops.qknorm_rope_kvwrite_cs(r.qkv_pre[0, :T], r.qn_w[0], r.kn_w[0], r.eps, cs, None, q, r.kc[0], r.vc[0],
+                                       sh.nh, sh.nkv)
+            qs.append(q)
 
         def run_all():
             for i, r in enumerate(runners):
                 for li in range(sh.layers):
-                    ops.prefill_attn(r.q_pre[:T], r.kc[li], r.vc[li], sh.scale, outs[(i + li) % 2])
+                    ops.prefill_attn(qs[i], r.kc[li], r.vc[li], sh.scale, outs[(i + li) % 2])
 
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph):

@@ -189,6 +189,28 @@ int solort_prefill_attn(const void* q, int T, int nh, int nkv, int hd, const voi
                         const void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride,
                         int64_t max_len, float scale, void* out, int out_dtype, solort_stream_t stream);
 
+/*
+ * One layer's prefill attention block: QK-RMSNorm + RoPE of the T prompt
+ * rows' q and k heads, the cache write of their K and V rows at positions
+ * 0..T-1, and the causal attention into out.  Replaces, per layer,
+ * cuda_graph_executor.py:117-130 (the norms and rope :120-121, the cache
+ * writes :122-123, the SDPA :124-130).  Results equal
+ * solort_qknorm_rope_kvwrite_cs followed by solort_prefill_attn on the same
+ * inputs, bit for bit (the cache rows and out); q is not materialised: the
+ * attention kernel normalises the q rows it stages.  Two launches on
+ * `stream` (the K/V rows, then the attention).  It saves the q round trip
+ * through HBM but puts the q normalisation ahead of each attention
+ * workgroup's first MFMA: on MI355X it wins from about 400 rows on (Qwen3-4B
+ * shape, 1024 rows: 27.0 against 30.1 us per layer) and loses below.
+ * qkv [T, qkv_row_stride] bf16 (q, k, v heads of each row); rope_cs [2, T, 64]
+ * bf16 from solort_rope_rows(inv_freq, 64, pos0 = 0, T).  Other arguments as
+ * in solort_qknorm_rope_kvwrite_cs and solort_prefill_attn.
+ */
+int solort_prefill_layer(const void* qkv, int64_t qkv_row_stride, int T, int nh, int nkv, int hd, const void* qn_w,
+                         const void* kn_w, float eps, const void* rope_cs, void* k_cache, void* v_cache,
+                         int64_t kv_tok_stride, int64_t kv_head_stride, int64_t max_len, float scale, void* out,
+                         int out_dtype, solort_stream_t stream);
+
 /* Workspace bytes for solort_argmax_rows with `rows` rows. Allocate once,
  * zero-fill once, reuse; overlapping calls must not share it. */
 size_t solort_argmax_workspace_bytes(int rows);

@@ -15,4 +15,17 @@ int check_launch(const char* what);
 
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// prologue.hip: argument checks of the QK-RMSNorm + RoPE + KV-write entry
+// points (rope_src: inv_freq or the cos/sin table); 0 or the error code.
+int check_prologue(const char* name, const void* qkv, int64_t qkv_row_stride, int T, int nh, int nkv, int hd,
+                   const void* qn_w, const void* kn_w, const void* rope_src, const void* q_out, const void* k_cache,
+                   const void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride, int64_t max_len);
+
+// prologue.hip: QK-RMSNorm + RoPE of the K rows and the cache write of the K
+// and V rows of T tokens at positions 0..T-1 (no q rows), cos/sin from a
+// solort_rope_rows table; arguments already validated.
+int launch_kv_rows_cs(const void* qkv, int64_t qkv_row_stride, int T, int nh, int nkv, const void* kn_w, float eps,
+                      const void* rope_cs, void* k_cache, void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride,
+                      int64_t max_len, hipStream_t stream);
+
 }  // namespace solort

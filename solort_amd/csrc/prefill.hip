@@ -40,6 +40,7 @@
 
 #include "common.h"
 #include "capi_internal.h"
+#include "qknorm_rope.h"
 
 namespace solort {
 
@@ -116,16 +117,20 @@ __device__ __forceinline__ uint2 lds_read_tr16(const uint16_t* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
-// Scalar arguments: all of them (13 SGPRs) arrive preloaded
-// (-amdgpu-kernarg-preload-count), so neither the first loads nor the final
-// stores wait for a kernel-argument load.  q [T][nh][128]; out [T][nh * 128]
-// in fp32 (F32) or bf16; qscale = softmax scale * log2(e).
-template <int G, bool F32>
-__global__ __launch_bounds__(kThreads) void prefill_kernel(const uint16_t* __restrict__ q,
-                                                           const uint16_t* __restrict__ kc,
-                                                           const uint16_t* __restrict__ vc, int T, int nkv,
-                                                           int tok_stride, int head_stride, float qscale,
-                                                           void* __restrict__ out_ptr) {
+// Scalar arguments: the first nine (14 SGPRs: every address the first loads
+// need) arrive preloaded (-amdgpu-kernarg-preload-count); qscale, eps and out
+// load meanwhile.  q: row pos, head h at q + pos * q_stride + 128 h (the
+// [T][nh][128] buffer, or with FUSED the raw q rows of the qkv projection,
+// which the kernel normalises with qn_w, eps and the cos/sin rows rope_cs
+// [2][T][64] as solort_qknorm_rope_kvwrite_cs would, bit for bit);
+// t_nkv = T | nkv << 24; out [T][nh * 128] in fp32 (F32) or bf16; qscale =
+// softmax scale * log2(e).
+template <int G, bool F32, bool FUSED>
+__global__ __launch_bounds__(kThreads) void prefill_kernel(
+    const uint16_t* __restrict__ q, const uint16_t* __restrict__ kc, const uint16_t* __restrict__ vc,
+    const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ rope_cs, int t_nkv, int tok_stride,
+    int head_stride, int q_stride, float qscale, float eps, void* __restrict__ out_ptr) {
+  const int T = t_nkv & 0xffffff, nkv = (int)((unsigned)t_nkv >> 24);
   constexpr int PB = 32 * (4 / G);  // positions per block
   const int nh = nkv * G, n_qtiles = (T + PB - 1) / PB;
   __shared__ __align__(16) uint16_t sK[2][kStage * kKStride];
@@ -148,8 +153,22 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const uint16_t* __res
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     const int pos = min(p0 + 32 * (w / G) + (tid >> 4), T - 1);
-    qv[w] = *reinterpret_cast<const uint4*>(q + ((int64_t)pos * nh + kvh * G + (w % G)) * SOLORT_HD +
+    qv[w] = *reinterpret_cast<const uint4*>(q + (int64_t)pos * q_stride + (kvh * G + (w % G)) * SOLORT_HD +
                                            8 * (tid & 15));
+  }
+  // FUSED: this lane's weights and cos/sin values of the q rows it stages
+  // (4 / G distinct positions: tile w at position group w / G), loaded with
+  // the raw rows; the normalisation waits until block 0's loads are issued.
+  constexpr int NP = FUSED ? 4 / G : 1;
+  uint4 wq{}, cs4[NP], sn4[NP];
+  if constexpr (FUSED) {
+    wq = *reinterpret_cast<const uint4*>(qn_w + 8 * (tid & 15));
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+      const int pos = min(p0 + 32 * pp + (tid >> 4), T - 1);
+      cs4[pp] = *reinterpret_cast<const uint4*>(rope_cs + (int64_t)pos * 64 + (tid & 7) * 8);
+      sn4[pp] = *reinterpret_cast<const uint4*>(rope_cs + ((int64_t)T + pos) * 64 + (tid & 7) * 8);
+    }
   }
 
   const uint16_t* kbase = kc + kvh * head_stride;
@@ -173,6 +192,19 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const uint16_t* __res
   // The next staged block's loads fly while this one is computed; buffer
   // loads beyond the head's rows return zeros.
   Staged st = prefill_fetch(krs, vrs, voff, 0);
+  if constexpr (FUSED) {
+    // QK-RMSNorm + RoPE of the q rows: each 16-lane group holds one row, as
+    // in the prologue kernel (qknorm_rope_row).
+    __builtin_amdgcn_sched_barrier(0);  // block 0's loads issue first and fly meanwhile
+    float c[NP][8], sn[NP][8];
+#pragma unroll
+    for (int pp = 0; pp < NP; ++pp) {
+      unpack8(cs4[pp], c[pp]);
+      unpack8(sn4[pp], sn[pp]);
+    }
+#pragma unroll
+    for (int w = 0; w < 4; ++w) qv[w] = qknorm_rope_row(qv[w], wq, c[w / G], sn[w / G], eps, tid & 15);
+  }
 #pragma unroll
   for (int w = 0; w < 4; ++w)
     *reinterpret_cast<uint4*>(&sK[1][(32 * w + (tid >> 4)) * kKStride + 8 * (tid & 15)]) = qv[w];
@@ -368,56 +400,104 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(const uint16_t* __res
 
 using namespace solort;
 
-extern "C" int solort_prefill_attn(const void* q, int T, int nh, int nkv, int hd, const void* k_cache,
-                                   const void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride,
-                                   int64_t max_len, float scale, void* out, int out_dtype,
-                                   solort_stream_t stream) {
-  const char* name = "prefill_attn";
+// Checks shared by the prefill entry points; 0 or the error code.
+static int check_prefill(const char* name, int T, int nh, int nkv, int hd, const void* k_cache, const void* v_cache,
+                         int64_t kv_tok_stride, int64_t kv_head_stride, int64_t max_len, void* out, int out_dtype) {
   if (hd != SOLORT_HD) return set_error(SOLORT_EINVAL, "%s: head_dim %d != 128", name, hd);
   if (nh <= 0 || nkv <= 0 || nh % nkv != 0)
     return set_error(SOLORT_EINVAL, "%s: nh=%d must be a positive multiple of nkv=%d", name, nh, nkv);
   const int G = nh / nkv;
   if (G != 1 && G != 2 && G != 4) return set_error(SOLORT_EINVAL, "%s: query group %d not in {1,2,4}", name, G);
-  if (T < 0 || T > max_len || T > (1 << 24))
+  if (nkv > 255) return set_error(SOLORT_EINVAL, "%s: nkv=%d above 255", name, nkv);
+  if (T < 0 || T > max_len || T >= (1 << 24))
     return set_error(SOLORT_EINVAL, "%s: T=%d outside [0, max_len=%lld]", name, T, (long long)max_len);
-  if (!q || !k_cache || !v_cache || !out) return set_error(SOLORT_EINVAL, "%s: null pointer", name);
-  if (!aligned16(q) || !aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
+  if (!k_cache || !v_cache || !out) return set_error(SOLORT_EINVAL, "%s: null pointer", name);
+  if (!aligned16(k_cache) || !aligned16(v_cache) || !aligned16(out))
     return set_error(SOLORT_EINVAL, "%s: pointers must be 16-byte aligned", name);
   if (kv_tok_stride <= 0 || kv_head_stride <= 0 || kv_tok_stride % 8 || kv_head_stride % 8)
     return set_error(SOLORT_EINVAL, "%s: KV strides must be positive multiples of 8", name);
   if (out_dtype != SOLORT_DTYPE_BF16 && out_dtype != SOLORT_DTYPE_F32)
     return set_error(SOLORT_EINVAL, "%s: out_dtype %d", name, out_dtype);
-  if (T == 0) return 0;
   // K/V rows are addressed with 32-bit byte offsets from the head's row 0, up
-  // to two staged blocks past T.
+  // to two staged blocks past T; the kernel takes 32-bit strides, the heads'
+  // offsets within 2^31 elements of the cache base.
   if (((int64_t)T + 4 * kStage) * kv_tok_stride * 2 >= ((int64_t)1 << 31))
     return set_error(SOLORT_EINVAL, "%s: T=%d rows of stride %lld exceed 32-bit byte offsets", name, T,
                      (long long)kv_tok_stride);
-  // The kernel takes 32-bit strides: every K/V row it addresses lies within
-  // 2^31 bytes of its head's row 0 (checked above) and the heads' offsets
-  // within 2^31 elements of the cache base.
   if ((int64_t)nkv * kv_head_stride >= ((int64_t)1 << 31))
     return set_error(SOLORT_EINVAL, "%s: KV head stride %lld exceeds 32-bit offsets", name,
                      (long long)kv_head_stride);
+  return 0;
+}
+
+// The attention launch; q rows at q + pos * q_stride (elements), fused: raw
+// q rows normalised in the kernel.
+static int launch_prefill(const char* name, const void* q, int64_t q_stride, bool fused, const void* qn_w,
+                          const void* rope_cs, float eps, int T, int nh, int nkv, const void* k_cache,
+                          const void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride, float scale, void* out,
+                          int out_dtype, hipStream_t s) {
+  if (q_stride > 0x7fffffff) return set_error(SOLORT_EINVAL, "%s: q row stride %lld too large", name, (long long)q_stride);
+  const int G = nh / nkv;
   const int pb = 32 * (4 / G);  // positions per block
   const int n_qtiles = (T + pb - 1) / pb;
   const int64_t blocks = (int64_t)n_qtiles * nkv;
   if (blocks > 0x7fffffff) return set_error(SOLORT_EINVAL, "%s: too many tiles", name);
-  hipStream_t s = (hipStream_t)stream;
   const float qscale = scale * 1.4426950408889634f;
   const bool f32 = out_dtype == SOLORT_DTYPE_F32;
-#define SOLORT_PREFILL_LAUNCH(GG, FF)                                                                           \
-  hipLaunchKernelGGL((prefill_kernel<GG, FF>), dim3((unsigned)blocks), dim3(kThreads), 0, s, (const uint16_t*)q, \
-                     (const uint16_t*)k_cache, (const uint16_t*)v_cache, T, nkv, (int)kv_tok_stride,             \
-                     (int)kv_head_stride, qscale, out)
-  switch (G * 2 + (f32 ? 1 : 0)) {
-    case 2: SOLORT_PREFILL_LAUNCH(1, false); break;
-    case 3: SOLORT_PREFILL_LAUNCH(1, true); break;
-    case 4: SOLORT_PREFILL_LAUNCH(2, false); break;
-    case 5: SOLORT_PREFILL_LAUNCH(2, true); break;
-    case 8: SOLORT_PREFILL_LAUNCH(4, false); break;
-    case 9: SOLORT_PREFILL_LAUNCH(4, true); break;
+  const int t_nkv = T | nkv << 24;
+#define SOLORT_PREFILL_LAUNCH(GG, FF, QQ)                                                                          \
+  hipLaunchKernelGGL((prefill_kernel<GG, FF, QQ>), dim3((unsigned)blocks), dim3(kThreads), 0, s, (const uint16_t*)q, \
+                     (const uint16_t*)k_cache, (const uint16_t*)v_cache, (const uint16_t*)qn_w,                      \
+                     (const uint16_t*)rope_cs, t_nkv, (int)kv_tok_stride, (int)kv_head_stride, (int)q_stride, qscale, \
+                     eps, out)
+  switch (G * 4 + (f32 ? 2 : 0) + (fused ? 1 : 0)) {
+    case 4: SOLORT_PREFILL_LAUNCH(1, false, false); break;
+    case 5: SOLORT_PREFILL_LAUNCH(1, false, true); break;
+    case 6: SOLORT_PREFILL_LAUNCH(1, true, false); break;
+    case 7: SOLORT_PREFILL_LAUNCH(1, true, true); break;
+    case 8: SOLORT_PREFILL_LAUNCH(2, false, false); break;
+    case 9: SOLORT_PREFILL_LAUNCH(2, false, true); break;
+    case 10: SOLORT_PREFILL_LAUNCH(2, true, false); break;
+    case 11: SOLORT_PREFILL_LAUNCH(2, true, true); break;
+    case 16: SOLORT_PREFILL_LAUNCH(4, false, false); break;
+    case 17: SOLORT_PREFILL_LAUNCH(4, false, true); break;
+    case 18: SOLORT_PREFILL_LAUNCH(4, true, false); break;
+    case 19: SOLORT_PREFILL_LAUNCH(4, true, true); break;
   }
 #undef SOLORT_PREFILL_LAUNCH
   return check_launch(name);
+}
+
+extern "C" int solort_prefill_attn(const void* q, int T, int nh, int nkv, int hd, const void* k_cache,
+                                   const void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride,
+                                   int64_t max_len, float scale, void* out, int out_dtype,
+                                   solort_stream_t stream) {
+  const char* name = "prefill_attn";
+  int rc = check_prefill(name, T, nh, nkv, hd, k_cache, v_cache, kv_tok_stride, kv_head_stride, max_len, out,
+                         out_dtype);
+  if (rc) return rc;
+  if (!q) return set_error(SOLORT_EINVAL, "%s: null pointer", name);
+  if (!aligned16(q)) return set_error(SOLORT_EINVAL, "%s: pointers must be 16-byte aligned", name);
+  if (T == 0) return 0;
+  return launch_prefill(name, q, (int64_t)nh * SOLORT_HD, false, nullptr, nullptr, 0.f, T, nh, nkv, k_cache, v_cache,
+                        kv_tok_stride, kv_head_stride, scale, out, out_dtype, (hipStream_t)stream);
+}
+
+extern "C" int solort_prefill_layer(const void* qkv, int64_t qkv_row_stride, int T, int nh, int nkv, int hd,
+                                    const void* qn_w, const void* kn_w, float eps, const void* rope_cs,
+                                    void* k_cache, void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride,
+                                    int64_t max_len, float scale, void* out, int out_dtype, solort_stream_t stream) {
+  const char* name = "prefill_layer";
+  // q_out is not materialised: out stands in for it in the null/alignment checks.
+  int rc = check_prologue(name, qkv, qkv_row_stride, T, nh, nkv, hd, qn_w, kn_w, rope_cs, out, k_cache, v_cache,
+                          kv_tok_stride, kv_head_stride, max_len);
+  if (rc) return rc;
+  rc = check_prefill(name, T, nh, nkv, hd, k_cache, v_cache, kv_tok_stride, kv_head_stride, max_len, out, out_dtype);
+  if (rc || T == 0) return rc;
+  hipStream_t s = (hipStream_t)stream;
+  rc = launch_kv_rows_cs(qkv, qkv_row_stride, T, nh, nkv, kn_w, eps, rope_cs, k_cache, v_cache, kv_tok_stride,
+                         kv_head_stride, max_len, s);
+  if (rc) return rc;
+  return launch_prefill(name, qkv, qkv_row_stride, true, qn_w, rope_cs, eps, T, nh, nkv, k_cache, v_cache,
+                        kv_tok_stride, kv_head_stride, scale, out, out_dtype, s);
 }

@@ -25,8 +25,9 @@ __global__ __launch_bounds__(256) void qknorm_rope_kvwrite_kernel(
     const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w, float eps,
     const float* __restrict__ inv_freq, const uint16_t* __restrict__ rope_cs, int64_t pos_limit,
     const int64_t* __restrict__ pos0_dev, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
-    uint16_t* __restrict__ vc, int64_t tok_stride, int64_t head_stride) {
-  // Block = one token; the 16 slots of 16 lanes take its head rows.
+    uint16_t* __restrict__ vc, int64_t tok_stride, int64_t head_stride, int row0) {
+  // Block = one token; the 16 slots of 16 lanes take its head rows row0 ..
+  // (row0 = nh: the K and V rows only, q_out unused).
   const int tid = threadIdx.x, j = tid & 15, slot = tid >> 4;
   const int t = blockIdx.x;
   const int heads = nh + 2 * nkv;
@@ -58,11 +59,11 @@ __global__ __launch_bounds__(256) void qknorm_rope_kvwrite_kernel(
   uint4 raws[kMaxPass];
 #pragma unroll
   for (int p = 0; p < kMaxPass; ++p)
-    raws[p] = *reinterpret_cast<const uint4*>(qkv + (int64_t)t * qkv_stride + min(slot + 16 * p, heads - 1) * SOLORT_HD +
-                                              j * 8);
+    raws[p] = *reinterpret_cast<const uint4*>(qkv + (int64_t)t * qkv_stride +
+                                              min(row0 + slot + 16 * p, heads - 1) * SOLORT_HD + j * 8);
 #pragma unroll
   for (int p = 0; p < kMaxPass; ++p) {  // whole 16-lane groups take a row
-    const int hs = slot + 16 * p;
+    const int hs = row0 + slot + 16 * p;
     if (hs >= heads) break;
     const uint4 raw = raws[p];
     if (hs >= nh + nkv) {  // V rows: raw copy (V is neither normed nor roped)
@@ -83,8 +84,8 @@ __global__ __launch_bounds__(256) void qknorm_rope_kvwrite_kernel(
 
 using namespace solort;
 
-// Checks shared by both entry points.
-static int check_prologue(const char* name, const void* qkv, int64_t qkv_row_stride, int T, int nh, int nkv, int hd,
+// Checks shared by the prologue entry points and solort_prefill_layer.
+int solort::check_prologue(const char* name, const void* qkv, int64_t qkv_row_stride, int T, int nh, int nkv, int hd,
                           const void* qn_w, const void* kn_w, const void* rope_src, const void* q_out,
                           const void* k_cache, const void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride,
                           int64_t max_len) {
@@ -116,7 +117,7 @@ extern "C" int solort_qknorm_rope_kvwrite(const void* qkv, int64_t qkv_row_strid
   hipLaunchKernelGGL(qknorm_rope_kvwrite_kernel<false>, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)qkv, qkv_row_stride, T, nh, nkv, (const uint16_t*)qn_w,
                      (const uint16_t*)kn_w, eps, inv_freq, (const uint16_t*)nullptr, max_len, pos0_dev,
-                     (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, kv_tok_stride, kv_head_stride);
+                     (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, kv_tok_stride, kv_head_stride, 0);
   return check_launch("qknorm_rope_kvwrite");
 }
 
@@ -131,6 +132,19 @@ extern "C" int solort_qknorm_rope_kvwrite_cs(const void* qkv, int64_t qkv_row_st
   hipLaunchKernelGGL(qknorm_rope_kvwrite_kernel<true>, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
                      (const uint16_t*)qkv, qkv_row_stride, T, nh, nkv, (const uint16_t*)qn_w,
                      (const uint16_t*)kn_w, eps, (const float*)nullptr, (const uint16_t*)rope_cs, max_len, pos0_dev,
-                     (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, kv_tok_stride, kv_head_stride);
+                     (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, kv_tok_stride, kv_head_stride, 0);
   return check_launch("qknorm_rope_kvwrite_cs");
+}
+
+// The K and V rows of T tokens at positions 0..T-1 (the prefill layer's
+// prologue; its q rows are normalised inside the attention kernel).  The
+// caller has validated the arguments as for solort_qknorm_rope_kvwrite_cs.
+int solort::launch_kv_rows_cs(const void* qkv, int64_t qkv_row_stride, int T, int nh, int nkv, const void* kn_w,
+                              float eps, const void* rope_cs, void* k_cache, void* v_cache, int64_t kv_tok_stride,
+                              int64_t kv_head_stride, int64_t max_len, hipStream_t stream) {
+  hipLaunchKernelGGL(qknorm_rope_kvwrite_kernel<true>, dim3((unsigned)T), dim3(256), 0, stream, (const uint16_t*)qkv,
+                     qkv_row_stride, T, nh, nkv, (const uint16_t*)kn_w, (const uint16_t*)kn_w, eps,
+                     (const float*)nullptr, (const uint16_t*)rope_cs, max_len, (const int64_t*)nullptr,
+                     (uint16_t*)nullptr, (uint16_t*)k_cache, (uint16_t*)v_cache, kv_tok_stride, kv_head_stride, nh);
+  return check_launch("prefill_layer (K/V rows)");
 }

@@ -271,6 +271,35 @@ def prefill_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, 
     _lib.check(rc, "prefill_attn")
 
 
+def prefill_layer(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps: float, rope_cs: torch.Tensor,
+                  k_cache: torch.Tensor, v_cache: torch.Tensor, scale: float, out: torch.Tensor, nh: int,
+                  nkv: int) -> None:
+    """One layer's prefill attention block for T prompt rows at positions 0..T-1: qkv
+    [T, (nh+2nkv)*128] -> K/V cache rows 0..T-1 and out [T, nh*128]; rope_cs = rope_rows(inv_f,
+    0, T).  Equal, bit for bit, to qknorm_rope_kvwrite_cs + prefill_attn; see solort_prefill_layer."""
+    _on_gpu("qkv", qkv, torch.bfloat16)
+    _need(qkv.dim() == 2 and qkv.shape[1] == (nh + 2 * nkv) * HD and qkv.stride(1) == 1,
+          f"qkv must be [T, {(nh + 2 * nkv) * HD}] with unit column stride")
+    T = qkv.shape[0]
+    for name, w in (("qn_w", qn_w), ("kn_w", kn_w)):
+        _on_gpu(name, w, torch.bfloat16)
+        _need(w.shape == (HD,) and w.is_contiguous(), f"{name} must be [{HD}] contiguous")
+    _rope_rows_ok(rope_cs, T)
+    ts, hs, max_len = _cache_strides("k_cache", k_cache, nkv)
+    _on_gpu("v_cache", v_cache, torch.bfloat16)
+    _need(v_cache.shape == k_cache.shape and v_cache.stride() == k_cache.stride(),
+          "v_cache must match k_cache in shape and strides")
+    _need(out.is_cuda and out.dtype in (torch.bfloat16, torch.float32), "out must be bf16 or fp32 on the device")
+    _need(out.shape == (T, nh * HD) and out.is_contiguous() and out.data_ptr() % 16 == 0,
+          f"out must be [{T}, {nh * HD}] contiguous and 16-byte aligned")
+    dt = DTYPE_F32 if out.dtype == torch.float32 else DTYPE_BF16
+    rc = _lib.load().solort_prefill_layer(
+        qkv.data_ptr(), qkv.stride(0), T, nh, nkv, HD, qn_w.data_ptr(), kn_w.data_ptr(), float(eps),
+        rope_cs.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), ts, hs, max_len, float(scale), out.data_ptr(), dt,
+        _stream(qkv))
+    _lib.check(rc, "prefill_layer")
+
+
 def argmax_workspace(rows: int, device: torch.device | str) -> torch.Tensor:
     """Zero-filled workspace for argmax_rows (allocate once, reuse)."""
     nbytes = _lib.load().solort_argmax_workspace_bytes(rows)

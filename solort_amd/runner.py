@@ -32,6 +32,14 @@ DECODE_BUCKETS = (128, 256, 512, 1024, 2048, 4096)
 PREFILL_BUCKETS = (16, 32, 64, 128, 256, 512, 1024)
 
 
+# Prefill buckets from this length on use solort_prefill_layer (q normalised inside the attention
+# kernel); shorter ones the two-launch prologue + attention.  Measured on MI355X, Qwen3-4B shape:
+# the fused layer saves the q round trip through HBM (5.2 us of prologue per layer at 1024 rows,
+# 2.2 us at 512) and adds 1.2-1.7 us of normalisation work ahead of each attention workgroup's
+# first MFMA, so it loses at 128 rows (prologue 4.3 -> 4.0 us, attention 7.3 -> 9.0 us).
+FUSED_PREFILL_MIN = 512
+
+
 def decode_splits(bound: int, nkv: int) -> int:
     """Key splits per KV head for a decode bucket.  Up to 4096 keys: about 32 keys per split,
     enough workgroups to cover the 256 CUs (short chunks, latency-bound).  Longer buckets:
@@ -96,10 +104,11 @@ class GraphQwen3Attention:
         # prefill: padded prompt rows per layer, bucketed graphs
         pmax = self.pre_buckets[-1]
         self.qkv_pre = torch.zeros(layers, pmax, self.width, dtype=torch.bfloat16, device=self.dev)
-        self.q_pre = torch.zeros(pmax, nh, HD, dtype=torch.bfloat16, device=self.dev)
         self.zero_pos = torch.zeros(1, dtype=torch.long, device=self.dev)  # prefill positions start at 0
         self.cs_pre = torch.zeros(2 * pmax * (HD // 2), dtype=torch.bfloat16, device=self.dev)  # step cos/sin
         self.ctx_pre = torch.zeros(layers, pmax, nh * HD, dtype=torch.bfloat16, device=self.dev)
+        # q of the short buckets (the fused layer does not materialise it)
+        self.q_pre = torch.zeros(min(pmax, FUSED_PREFILL_MIN), nh, HD, dtype=torch.bfloat16, device=self.dev)
         self._pre_graphs: dict[int, torch.cuda.CUDAGraph] = {}
 
     # ------------------------------------------------------------ decode
@@ -155,9 +164,14 @@ class GraphQwen3Attention:
         cs = self.cs_pre[: 2 * bound * (HD // 2)].view(2, bound, HD // 2)
         ops.rope_rows(self.inv_freq, self.zero_pos, bound, cs)  # cos/sin once per step (:111)
         for li in range(self.L):
-            ops.qknorm_rope_kvwrite_cs(self.qkv_pre[li, :bound], self.qn_w[li], self.kn_w[li], self.eps, cs, None,
-                                       self.q_pre[:bound], self.kc[li], self.vc[li], self.nh, self.nkv)
-            ops.prefill_attn(self.q_pre[:bound], self.kc[li], self.vc[li], self.scale, self.ctx_pre[li, :bound])
+            if bound >= FUSED_PREFILL_MIN:  # prologue of the K/V rows, then attention normalising q itself
+                ops.prefill_layer(self.qkv_pre[li, :bound], self.qn_w[li], self.kn_w[li], self.eps, cs, self.kc[li],
+                                  self.vc[li], self.scale, self.ctx_pre[li, :bound], self.nh, self.nkv)
+            else:  # short prompts: the whole prologue, then attention on the materialised q
+                ops.qknorm_rope_kvwrite_cs(self.qkv_pre[li, :bound], self.qn_w[li], self.kn_w[li], self.eps, cs,
+                                           None, self.q_pre[:bound], self.kc[li], self.vc[li], self.nh, self.nkv)
+                ops.prefill_attn(self.q_pre[:bound], self.kc[li], self.vc[li], self.scale,
+                                 self.ctx_pre[li, :bound])
 
     def prefill(self, qkv: torch.Tensor) -> torch.Tensor:
         """Graphed bucketed prefill (cuda_graph_executor.py:149-161): qkv [layers, plen, width] for

@@ -103,6 +103,24 @@ def test_prologue_and_argmax_reject_bad_arguments(lib):
     assert rc == EINVAL
 
 
+def test_prefill_entry_points_reject_bad_arguments(lib):
+    p = ctypes.c_void_p(4096)
+    rc = lib.solort_prefill_layer(p, 6144, 100, 24, 8, 128, p, p, 1e-6, p, p, p, 1024, 128, 1024, 0.088, p, 0, None)
+    assert rc == EINVAL and "group" in _err(lib)
+    rc = lib.solort_prefill_layer(p, 6144, 100, 32, 8, 128, p, p, 1e-6, None, p, p, 1024, 128, 1024, 0.088, p, 0,
+                                  None)
+    assert rc == EINVAL and "null" in _err(lib)
+    rc = lib.solort_prefill_layer(p, 6000, 100, 32, 8, 128, p, p, 1e-6, p, p, p, 1024, 128, 1024, 0.088, p, 0, None)
+    assert rc == EINVAL and "stride" in _err(lib)
+    rc = lib.solort_prefill_layer(p, 6144, 2000, 32, 8, 128, p, p, 1e-6, p, p, p, 1024, 128, 1024, 0.088, p, 0,
+                                  None)
+    assert rc == EINVAL and "max_len" in _err(lib)
+    rc = lib.solort_prefill_attn(p, 100, 32, 8, 128, p, p, 1024, 128, 1024, 0.088, p, 5, None)
+    assert rc == EINVAL and "out_dtype" in _err(lib)
+    rc = lib.solort_prefill_attn(None, 100, 32, 8, 128, p, p, 1024, 128, 1024, 0.088, p, 0, None)
+    assert rc == EINVAL and "null" in _err(lib)
+
+
 def test_torch_front_end_refuses_cpu_tensors():
     q = torch.zeros(1, 32, 128, dtype=torch.bfloat16)
     kc = torch.zeros(1024, 8, 128, dtype=torch.bfloat16)

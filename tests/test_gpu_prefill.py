@@ -124,3 +124,34 @@ def test_prefill_other_groups(gpu, shape):
         blk = exact.prefill_blockwise(qg[:, h], kg[:, kvh], vg[:, kvh], shape.scale)
         e = np.abs(o32[:, h] - blk)
         assert e.max() <= 2e-2 and e.mean() <= 1e-5 and (e.max(axis=1) > 1e-4).sum() <= max(1, 0.01 * T), h
+
+
+@pytest.mark.parametrize("T,shape", [(1, wl.QWEN3_4B), (17, wl.QWEN3_4B), (128, wl.QWEN3_4B), (333, wl.QWEN3_4B),
+                                     (1024, wl.QWEN3_4B), (200, wl.QWEN3_0_6B), (150, wl.AttnShape("g1", 8, 8, 1))],
+                         ids=["4b-1", "4b-17", "4b-128", "4b-333", "4b-1024", "g2-200", "g1-150"])
+def test_prefill_layer_equals_prologue_then_attention(gpu, T, shape):
+    """solort_prefill_layer (K/V prologue + attention normalising q itself) writes the same cache
+    rows and the same outputs, bit for bit, as solort_qknorm_rope_kvwrite_cs followed by
+    solort_prefill_attn on a materialised q, in bf16 and fp32."""
+    _say(f"[prefill_layer {shape.name} T={T}]")
+    case = wl.prefill_case(T, layers=1)
+    nh, nkv = shape.nh, shape.nkv
+    g = torch.Generator().manual_seed(3000 + T)
+    qkv = (torch.randn(T, (nh + 2 * nkv) * HD, generator=g) * 2).to(torch.bfloat16).to(gpu)
+    qn_w, kn_w = case.qn_w[0].to(gpu), case.kn_w[0].to(gpu)
+    inv_f = ops.inv_freq(HD, wl.THETA, gpu)
+    cs = ops.rope_rows(inv_f, torch.zeros(1, dtype=torch.long, device=gpu), T)
+    kc1 = torch.full((case.max_len, nkv, HD), 7.0, dtype=torch.bfloat16, device=gpu)
+    vc1 = kc1.clone()
+    kc2, vc2 = kc1.clone(), kc1.clone()
+    q = torch.empty(T, nh, HD, dtype=torch.bfloat16, device=gpu)
+    for dt in (torch.bfloat16, torch.float32):
+        o1 = torch.empty(T, nh * HD, dtype=dt, device=gpu)
+        o2 = torch.empty_like(o1)
+        ops.qknorm_rope_kvwrite_cs(qkv, qn_w, kn_w, wl.EPS, cs, None, q, kc1, vc1, nh, nkv)
+        ops.prefill_attn(q, kc1, vc1, shape.scale, o1)
+        ops.prefill_layer(qkv, qn_w, kn_w, wl.EPS, cs, kc2, vc2, shape.scale, o2, nh, nkv)
+        torch.cuda.synchronize()
+        assert torch.equal(kc1, kc2) and torch.equal(vc1, vc2)
+        assert torch.equal(o1, o2), (dt, (o1.float() - o2.float()).abs().max().item())
+    assert torch.all(kc2[T:] == 7.0)  # rows past the prompt untouched
