@@ -211,6 +211,16 @@ int solort_prefill_layer(const void* qkv, int64_t qkv_row_stride, int T, int nh,
                          int64_t kv_tok_stride, int64_t kv_head_stride, int64_t max_len, float scale, void* out,
                          int out_dtype, solort_stream_t stream);
 
+/*
+ * Greedy speculative acceptance, on the device.  Replaces
+ * cuda_graph_executor.py:476, a = int((tg[:k] == draft).cumprod(0).sum()),
+ * and picks the token the round appends after the accepted drafts, tg[a]
+ * (:478, :481).  target [k + 1] int64: the argmax of the K+1 verify rows
+ * (solort_argmax_rows); draft [k] int64; out [2] int64 receives a and
+ * target[a].  One tiny launch, no host synchronisation.  1 <= k <= 2^20.
+ */
+int solort_accept_prefix(const int64_t* target, const int64_t* draft, int k, int64_t* out, solort_stream_t stream);
+
 /* Workspace bytes for solort_argmax_rows with `rows` rows. Allocate once,
  * zero-fill once, reuse; overlapping calls must not share it. */
 size_t solort_argmax_workspace_bytes(int rows);

@@ -111,6 +111,14 @@ def verify_attn(q: torch.Tensor, kc_l: torch.Tensor, vc_l: torch.Tensor, pos0: i
     return ctx.transpose(0, 1).reshape(k1, nh * hd)
 
 
+def accept_prefix(tg: torch.Tensor, draft: torch.Tensor) -> tuple[int, int]:
+    """cuda_graph_executor.py:476: a = (tg[:k] == draft).cumprod(0).sum(); with the token the round
+    appends after the accepted drafts, tg[a] (:478, :481).  tg [k+1], draft [k] int64."""
+    k = draft.numel()
+    a = int((tg[:k] == draft).cumprod(0).sum().item())
+    return a, int(tg[a].item())
+
+
 def argmax(logits: torch.Tensor) -> torch.Tensor:
     """cuda_graph_executor.py:190, :206 (and :234, :475): argmax(-1) of fp32 logits."""
     return logits.to(torch.float32).argmax(dim=-1)

@@ -323,3 +323,17 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor, ws: torch.Tensor) -> No
     rc = lib.solort_argmax_rows(logits.data_ptr(), dt, rows, vocab, logits.stride(0), out.data_ptr(),
                                 ws.data_ptr(), _stream(logits))
     _lib.check(rc, "argmax_rows")
+
+
+def accept_prefix(target: torch.Tensor, draft: torch.Tensor, out: torch.Tensor) -> None:
+    """out[0] = length of the prefix of draft [k] that target [k+1] agrees with, out[1] = target[out[0]]
+    (int64, on the device); see solort_accept_prefix."""
+    _need(target.is_cuda and draft.is_cuda and out.is_cuda, "target, draft and out must be on the ROCm device")
+    _need(target.dtype == torch.int64 and draft.dtype == torch.int64 and out.dtype == torch.int64,
+          "target, draft and out must be int64")
+    k = draft.numel()
+    _need(draft.is_contiguous() and target.is_contiguous() and target.numel() == k + 1,
+          f"target must hold k+1 = {k + 1} tokens")
+    _need(out.is_contiguous() and out.numel() >= 2, "out must hold 2 int64")
+    rc = _lib.load().solort_accept_prefix(target.data_ptr(), draft.data_ptr(), k, out.data_ptr(), _stream(target))
+    _lib.check(rc, "accept_prefix")

@@ -97,6 +97,8 @@ class GraphQwen3Attention:
         self.ctx_ver = torch.zeros(layers, self.k1, nh * HD, dtype=torch.bfloat16, device=self.dev)
         self.logits_ver = torch.zeros(self.k1, self.vocab, dtype=torch.float32, device=self.dev)
         self.tok_ver = torch.zeros(self.k1, dtype=torch.long, device=self.dev)
+        self.draft_ver = torch.zeros(max(1, self.k1 - 1), dtype=torch.long, device=self.dev)  # the K drafts
+        self.acc_ver = torch.zeros(2, dtype=torch.long, device=self.dev)  # accepted count, next token
         self.vpos0 = torch.zeros(1, dtype=torch.long, device=self.dev)
         self.cs_ver = torch.zeros(2, self.k1, HD // 2, dtype=torch.bfloat16, device=self.dev)
         self.ws_ver = ops.attn_workspace(self.k1, nh, nkv, max(verify_splits(b) for b in self.buckets), self.dev)
@@ -202,12 +204,16 @@ class GraphQwen3Attention:
                              self.kc[li], self.vc[li], bound, self.scale, self.ws_ver, ns,
                              self.ctx_ver[li], self.nh, self.nkv)
         ops.argmax_rows(self.logits_ver, self.tok_ver, self.ws_arg)
+        if self.k1 > 1:  # greedy acceptance on the device (:476, :478, :481)
+            ops.accept_prefix(self.tok_ver, self.draft_ver, self.acc_ver)
 
-    def verify(self, qkv: torch.Tensor, pos_start: int, logits: torch.Tensor | None = None) -> torch.Tensor:
+    def verify(self, qkv: torch.Tensor, pos_start: int, logits: torch.Tensor | None = None,
+               draft: torch.Tensor | None = None) -> torch.Tensor:
         """Score K+1 tokens at pos_start..pos_start+K (cuda_graph_executor.py:270-289).
 
         qkv [layers, K+1, width]; returns ctx [layers, K+1, nh*128].  If logits [K+1, vocab] are
-        given, tok_ver holds their argmax after the replay.
+        given, tok_ver holds their argmax after the replay; with the K draft tokens (int64), acc_ver
+        then holds the accepted-prefix length and the token that follows it.
         """
         if not 0 <= pos_start <= self.max_len - self.k1:
             raise RuntimeError(f"verify positions {pos_start}..{pos_start + self.k1 - 1} exceed max_len")
@@ -220,6 +226,8 @@ class GraphQwen3Attention:
         self.qkv_ver.copy_(qkv)
         if logits is not None:
             self.logits_ver.copy_(logits)
+        if draft is not None:
+            self.draft_ver.copy_(draft)
         self.vpos0.fill_(int(pos_start))
         self._ver_graphs[bound].replay()
         return self.ctx_ver

@@ -366,3 +366,23 @@ def test_device_rope_table_equals_torch_table(gpu):
     ds = (sin_k.view(torch.int16) != sin_t.view(torch.int16)).sum().item()
     _say(f"[rope table] differing cos {dc}, sin {ds} of {rows * 64}")
     assert dc == 0 and ds == 0
+
+
+def test_accept_prefix_equals_reference_expression(gpu):
+    """solort_accept_prefix against cuda_graph_executor.py:476 (restated in oracle/ref.py) on planted
+    mismatch positions, k up to 1000 (several 64-pair scans)."""
+    g = torch.Generator().manual_seed(32)
+    out = torch.zeros(2, dtype=torch.long, device=gpu)
+    n = 0
+    for k in (1, 4, 63, 64, 65, 200, 1000):
+        for miss in sorted({0, 1 % k, k // 2, k - 1, k}):
+            draft = torch.randint(0, 151936, (k,), generator=g)
+            tg = torch.cat([draft.clone(), torch.randint(0, 151936, (1,), generator=g)])
+            if miss < k:
+                tg[miss] = (draft[miss] + 7) % 151936
+            out.fill_(-5)
+            ops.accept_prefix(tg.to(gpu), draft.to(gpu), out)
+            torch.cuda.synchronize()
+            assert tuple(out.cpu().tolist()) == ref.accept_prefix(tg, draft), (k, miss)
+            n += 1
+    _say(f"  accept_prefix: {n} cases equal")

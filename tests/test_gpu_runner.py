@@ -92,14 +92,17 @@ def test_verify_graph_replays_match_eager(gpu):
     r, g, sh = _make(gpu, layers=2, max_len=4096, k1=5)
     eager_kc, eager_vc = r.kc.clone(), r.vc.clone()
     q = torch.empty(5, sh.nh, HD, dtype=torch.bfloat16, device=gpu)
-    for pos0 in (2048, 17, 4091, 2048, 100):
+    for rep, pos0 in enumerate((2048, 17, 4091, 2048, 100)):
         bound = r._bucket_for(pos0 + 4)
         ns = verify_splits(bound)
         ws = ops.attn_workspace(5, sh.nh, sh.nkv, ns, gpu)
         _say(f"[verify replay pos0={pos0} bound={bound}]")
         qkv = torch.randn(r.L, 5, r.width, generator=g).to(torch.bfloat16)
         logits = torch.randn(5, wl.VOCAB, generator=g)
-        ctx = r.verify(qkv.to(gpu), pos0, logits.to(gpu))
+        draft = logits.argmax(-1)[:4].clone()  # drafts the target agrees with up to a planted mismatch
+        if rep < 4:
+            draft[rep] = (draft[rep] + 1) % wl.VOCAB
+        ctx = r.verify(qkv.to(gpu), pos0, logits.to(gpu), draft.to(gpu))
         p = torch.tensor([pos0], dtype=torch.long, device=gpu)
         out = torch.empty(r.L, 5, sh.nh * HD, dtype=torch.bfloat16, device=gpu)
         for li in range(r.L):
@@ -110,6 +113,9 @@ def test_verify_graph_replays_match_eager(gpu):
         assert torch.equal(r.kc, eager_kc) and torch.equal(r.vc, eager_vc)
         assert torch.equal(ctx, out)
         assert torch.equal(r.tok_ver.cpu(), logits.argmax(-1))
+        # in-graph acceptance (cuda_graph_executor.py:476): the planted mismatch, or all four
+        assert tuple(r.acc_ver.cpu().tolist()) == ref.accept_prefix(logits.argmax(-1), draft)
+        assert r.acc_ver[0].item() == (rep if rep < 4 else 4)
     assert sorted(r._ver_graphs) == [128, 4096]
 
 

@@ -313,3 +313,20 @@ def test_prefill_blockwise_equals_exact_without_rounding_and_close_with_it():
     assert err.max() < 2e-2 and err.mean() < 2e-3
     # row 0 sees only key 0
     assert np.allclose(got_b[0], v[0], atol=1e-12)
+
+
+def test_accept_prefix_matches_a_first_mismatch_scan():
+    """The reference expression (cumprod of the element-wise match) is the index of the first mismatch,
+    k when there is none; pinned by a plain scan on planted mismatch positions."""
+    g = torch.Generator().manual_seed(31)
+    for k in (1, 2, 4, 7, 64, 65, 300):
+        for miss in sorted({0, k // 2, k - 1, k}):
+            draft = torch.randint(0, 151936, (k,), generator=g)
+            tg = torch.cat([draft.clone(), torch.randint(0, 151936, (1,), generator=g)])
+            if miss < k:
+                tg[miss] = (draft[miss] + 1) % 151936
+                tg[miss + 1:k] = torch.randint(0, 151936, (k - miss - 1,), generator=g)  # anything after
+            a, nxt = ref.accept_prefix(tg, draft)
+            scan = next((i for i in range(k) if int(tg[i]) != int(draft[i])), k)
+            assert (a, nxt) == (scan, int(tg[scan]))
+            assert a == miss
