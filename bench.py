@@ -54,7 +54,7 @@ def parse() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-sweep", action="store_true", help="skip the per-bucket decode extras")
-    p.add_argument("--only", choices=("all", "decode", "prefill", "long", "verify"), default="all",
+    p.add_argument("--only", choices=("all", "decode", "prefill", "long", "verify", "gemv"), default="all",
                    help="decode: the decode step and its kernel only; prefill: the prefill kernels only; "
                         "long: the Qwen3-8B KV 32768 decode only; verify: the speculative verify and argmax "
                         "only (for per-workload profiles)")
@@ -107,6 +107,9 @@ def main() -> int:
         return 0
     if args.only == "verify":
         print(json.dumps(verify_extras(torch, ops, wl, runners, dev, sh)), flush=True)
+        return 0
+    if args.only == "gemv":
+        print(json.dumps({"decode_gemv": gemv_extras(torch, ops, dev)}), flush=True)
         return 0
 
     # ---------------------------------------------------------------- timed graph replays
@@ -162,6 +165,7 @@ def main() -> int:
         result["extras"] = extras(torch, ops, wl, runners, dev, sh)
         result["extras"].update(verify_extras(torch, ops, wl, runners, dev, sh))
         result["extras"]["decode_8b_kv32768"] = long_decode_extras(torch, ops, wl, dev)
+        result["extras"]["decode_gemv"] = gemv_extras(torch, ops, dev)
     if args.only == "all":
         result["prefill"] = prefill_extras(torch, ops, runners, dev, sh)
         p1024 = result["prefill"].get("1024")
@@ -242,6 +246,52 @@ def _graph_us(torch, dev, calls, reps=3) -> float:
     e1.record(stream)
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) * 1e3 / (reps * len(calls))
+
+
+def gemv_extras(torch, ops, dev, copies: int = 4) -> dict:
+    """Qwen3-4B decode-step GEMVs (one token) with their fused neighbours (RMSNorm before qkv, gate_up
+    and lm_head; residual add after o_proj and down; SwiGLU after gate_up), next to torch's F.linear
+    (hipBLASLt) on the same weights without the neighbours.  Each is timed in a graph over `copies`
+    weight sets (2 for the 778 MB lm_head; 808 MB in all for the layer GEMVs, more than the 256 MB
+    Infinity Cache), four calls per set, HIP events around replays.  Bytes = the weight matrix."""
+    import functools
+    F = torch.nn.functional
+    gen = torch.Generator(device=dev).manual_seed(1005)
+    K, I = 2560, 9728
+    shapes = {"qkv": (6144, K, "norm"), "o_proj": (K, 4096, "resid"), "gate_up": (2 * I, K, "swiglu"),
+              "down": (K, I, "resid"), "lm_head": (151936, K, "norm")}
+    out = {}
+    for name, (rows, k, kind) in shapes.items():
+        nset = 2 if name == "lm_head" else copies
+        ws = [(torch.randn(rows, k, generator=gen, device=dev) * 0.02).to(torch.bfloat16) for _ in range(nset)]
+        x = torch.randn(k, generator=gen, device=dev).to(torch.bfloat16)
+        nw = (torch.randn(k, generator=gen, device=dev) * 0.1 + 1).to(torch.bfloat16)
+        n = I if kind == "swiglu" else rows
+        y = torch.zeros(n, dtype=torch.bfloat16, device=dev)
+
+        def call(w, kind=kind, x=x, nw=nw, y=y):
+            if kind == "norm":
+                ops.gemv(w, x, y, nw, 1e-6)
+            elif kind == "resid":
+                ops.gemv(w, x, y, res=y, mode=ops.GEMV_RESID)
+            else:
+                ops.gemv(w, x, y, nw, 1e-6, mode=ops.GEMV_SWIGLU, inter=I)
+
+        xm = x.view(1, k)
+        F.linear(xm, ws[0])  # the BLAS initialises outside the capture
+        torch.cuda.synchronize()
+        us = _graph_us(torch, dev, [functools.partial(call, w) for w in ws] * 4)
+        tus = _graph_us(torch, dev, [functools.partial(F.linear, xm, w) for w in ws] * 4)
+        nbytes = rows * k * 2
+        out[name] = {"us": round(us, 3), "gbps": round(nbytes / (us * 1e-6) / 1e9, 1),
+                     "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "torch_linear_us": round(tus, 3), "bytes": nbytes, "fused": kind}
+        del ws
+        torch.cuda.empty_cache()
+    layer = sum(out[n]["us"] for n in ("qkv", "o_proj", "gate_up", "down"))
+    out["layer_gemv_us"] = round(layer, 3)
+    out["layer_torch_linear_us"] = round(sum(out[n]["torch_linear_us"] for n in ("qkv", "o_proj", "gate_up", "down")), 3)
+    return out
 
 
 def long_decode_extras(torch, ops, wl, dev, n_caches: int = 8) -> dict:

@@ -40,6 +40,10 @@ extern "C" {
 #define SOLORT_DTYPE_BF16 0
 #define SOLORT_DTYPE_F32 1
 
+#define SOLORT_GEMV_PLAIN 0
+#define SOLORT_GEMV_RESID 1
+#define SOLORT_GEMV_SWIGLU 2
+
 /* hipStream_t, passed opaquely (torch.cuda.current_stream().cuda_stream). */
 typedef void* solort_stream_t;
 
@@ -220,6 +224,22 @@ int solort_prefill_layer(const void* qkv, int64_t qkv_row_stride, int T, int nh,
  * target[a].  One tiny launch, no host synchronisation.  1 <= k <= 2^20.
  */
 int solort_accept_prefix(const int64_t* target, const int64_t* draft, int k, int64_t* out, solort_stream_t stream);
+
+/*
+ * Decode-step matrix-vector product around the attention block, one token:
+ * W [rows][w_row_stride] bf16 row-major (torch Linear weight), x [k] bf16,
+ * fp32 accumulation, bf16 out [n_out].  Replaces the T = 1 GEMMs of
+ * cuda_graph_executor.py:165-190 with their neighbours fused:
+ *   norm_w non-NULL: x is first _rmsnorm(x, norm_w, eps) (:25-28; :170, :186, :190)
+ *   mode SOLORT_GEMV_PLAIN   out = W x                          (qkv :171, logits :190)
+ *   mode SOLORT_GEMV_RESID   out = res + W x (out may be res)   (:185, :188)
+ *   mode SOLORT_GEMV_SWIGLU  out[i] = silu(g_i) * u_i, g = rows 0..n_out-1,
+ *                            u = rows inter..inter+n_out-1 of W (wgu, :187-188)
+ * with the reference's bf16 rounding of each intermediate tensor.  x must not
+ * alias out.  k a multiple of 8 up to 65536; w, x, norm_w 16-byte aligned.
+ */
+int solort_gemv(const void* w, int64_t w_row_stride, int n_out, int k, const void* x, const void* norm_w, float eps,
+                const void* res, int mode, int64_t inter, void* out, solort_stream_t stream);
 
 /* Workspace bytes for solort_argmax_rows with `rows` rows. Allocate once,
  * zero-fill once, reuse; overlapping calls must not share it. */

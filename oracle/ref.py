@@ -111,6 +111,29 @@ def verify_attn(q: torch.Tensor, kc_l: torch.Tensor, vc_l: torch.Tensor, pos0: i
     return ctx.transpose(0, 1).reshape(k1, nh * hd)
 
 
+def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """cuda_graph_executor.py:25-28, over the last dim, in the dtype of x."""
+    d = x.float()
+    d = d * torch.rsqrt(d.pow(2).mean(-1, keepdim=True) + eps)
+    return (d * w.float()).to(x.dtype)
+
+
+def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
+    """x @ w.T in x's dtype with fp32 accumulation (the bf16 GEMMs of :171, :185, :187, :188, :190),
+    evaluated on the CPU in fp32 and rounded once."""
+    return (x.float() @ w.float().T).to(x.dtype)
+
+
+def decode_mlp_block(x: torch.Tensor, ctx: torch.Tensor, wo: torch.Tensor, post_ln: torch.Tensor, wgu: torch.Tensor,
+                     wd: torch.Tensor, eps: float) -> torch.Tensor:
+    """The non-attention tail of one decode layer, cuda_graph_executor.py:185-188, bf16:
+    x = x + ctx @ wo.T; h2 = rmsnorm(x); gate, up = split(h2 @ wgu.T); x = x + (silu(gate) * up) @ wd.T."""
+    x = x + linear(ctx, wo)
+    h2 = rmsnorm(x, post_ln, eps)
+    gate, up = linear(h2, wgu).split(wgu.shape[0] // 2, dim=-1)
+    return x + linear(F.silu(gate) * up, wd)
+
+
 def accept_prefix(tg: torch.Tensor, draft: torch.Tensor) -> tuple[int, int]:
     """cuda_graph_executor.py:476: a = (tg[:k] == draft).cumprod(0).sum(); with the token the round
     appends after the accepted drafts, tg[a] (:478, :481).  tg [k+1], draft [k] int64."""

@@ -61,6 +61,10 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
          c_int64, c_int64, c_int64, c_float, c_void_p, c_int, c_void_p],
     ),
     "solort_accept_prefix": (c_int, [c_void_p, c_void_p, c_int, c_void_p, c_void_p]),
+    "solort_gemv": (
+        c_int,
+        [c_void_p, c_int64, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_int, c_int64, c_void_p, c_void_p],
+    ),
     "solort_argmax_workspace_bytes": (c_size_t, [c_int]),
     "solort_argmax_rows": (
         c_int, [c_void_p, c_int, c_int, c_int64, c_int64, c_void_p, c_void_p, c_void_p]

@@ -1,0 +1,253 @@
+// Decode-step matrix-vector products around the attention block, HBM-bound
+// weight streams: y = W x for one token, W [N][K] bf16 row-major (the torch
+// Linear weight layout), fp32 accumulation, bf16 results.
+//
+// Follows src/solort/model/cuda_graph_executor.py:165-190 (decode) with the
+// fused weights of :54-63:
+//   h  = _rmsnorm(x, in_ln);   qkv = h @ wqkv.T            (NORM, PLAIN)
+//   x  = x + ctx @ wo.T                                    (RESID)
+//   h2 = _rmsnorm(x, post_ln); gate, up = (h2 @ wgu.T).split
+//   x  = x + (silu(gate) * up) @ wd.T                      (NORM + SWIGLU, RESID)
+//   _rmsnorm(x, final_norm) @ lm_head.T                    (NORM, PLAIN)
+// Each op rounds to bf16 as the reference's bf16 tensors do: the RMSNorm
+// output (_rmsnorm :25-28: fp32 x * rsqrt(mean(x^2) + eps), * fp32 w, to
+// bf16), the product, silu(gate), silu(gate) * up and the residual sum.
+//
+// Mapping: a workgroup (4 wavefronts) first stages x into LDS, normalised
+// when NORM (every workgroup recomputes the 1-row norm: K <= 16384, a few KB
+// from L2), then each wavefront streams R weight rows: lane l takes the
+// 16-byte chunks l, l + 64, ... of each row (1 KB per row per instruction,
+// coalesced), dotting them with x by v_dot2_f32_bf16, and the 64 lanes'
+// sums meet by DPP/permute reductions.  SWIGLU wavefronts take R / 2 outputs:
+// gate rows o and up rows o + inter.  R is chosen so the grid holds at least
+// two workgroups per CU.
+#include "common.h"
+#include "capi_internal.h"
+
+namespace solort {
+
+enum { kGemvPlain = 0, kGemvResid = 1, kGemvSwiglu = 2 };
+
+__device__ __forceinline__ float wave_sum64(float v) {
+  v += xshfl(v, 1);
+  v += xshfl(v, 2);
+  v += xshfl(v, 4);
+  v += xshfl(v, 8);
+  v += xshfl(v, 16);
+  return xor32_combine(v, [](float x, float y) { return x + y; });
+}
+
+// silu(g) = g * sigmoid(g) = g / (1 + exp(-g)) in fp32 (torch's formula),
+// rounded to bf16 as F.silu on a bf16 tensor.
+__device__ __forceinline__ float silu_bf16(float g) { return rbf(g / (1.0f + __expf(-g))); }
+
+template <int R, int U, int EPI, bool NORM>
+__global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ w, int64_t w_stride, int n_out,
+                                                   int K, const uint16_t* __restrict__ x,
+                                                   const uint16_t* __restrict__ norm_w, float eps,
+                                                   const uint16_t* res, int64_t inter, uint16_t* out) {
+  extern __shared__ uint4 sx[];  // x as K / 8 chunks of 16 bytes
+  __shared__ float s_red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nch = K >> 3;
+
+  // This wavefront's R weight rows; lane l streams their 16-byte chunks
+  // l + 64 i, U chunks per row in flight.
+  constexpr int NO = EPI == kGemvSwiglu ? R / 2 : R;  // outputs per wavefront
+  const int o0 = (blockIdx.x * 4 + wave) * NO;
+  const uint16_t* rows[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int o = min(o0 + (EPI == kGemvSwiglu ? r % NO : r), n_out - 1);  // past the end: repeat the last
+    const int64_t row = EPI == kGemvSwiglu && r >= NO ? o + inter : o;
+    rows[r] = w + row * w_stride;
+  }
+  uint4 wv[U][R];
+#define SOLORT_GEMV_LOADS(C0)                                                                    \
+  _Pragma("unroll") for (int u = 0; u < U; ++u) {                                                \
+    const int c = (C0) + 64 * u;                                                                 \
+    if (c < nch) {                                                                               \
+      _Pragma("unroll") for (int r = 0; r < R; ++r) wv[u][r] = *reinterpret_cast<const uint4*>(rows[r] + 8 * c); \
+    }                                                                                            \
+  }
+  // The first weight loads go out before x is staged: they do not depend on
+  // it, and its load and norm then overlap their latency.
+  SOLORT_GEMV_LOADS(lane)
+
+  // x into LDS (normalised: sum of squares in fp32, one block reduction).
+  if constexpr (NORM) {
+    // The first kXReg chunks of this thread stay in registers between the two
+    // passes (k <= 8192 in one round); larger k re-reads the rest.
+    constexpr int kXReg = 4;
+    uint4 xr[kXReg], gr[kXReg];
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < kXReg; ++q) {
+      const int i = tid + 256 * q;
+      if (i < nch) {
+        xr[q] = *reinterpret_cast<const uint4*>(x + 8 * i);
+        gr[q] = *reinterpret_cast<const uint4*>(norm_w + 8 * i);
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < kXReg; ++q) {
+      if (tid + 256 * q < nch) {
+        float v[8];
+        unpack8(xr[q], v);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+      }
+    }
+    for (int i = tid + 256 * kXReg; i < nch; i += 256) {
+      float v[8];
+      unpack8(*reinterpret_cast<const uint4*>(x + 8 * i), v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
+    }
+    ss = wave_sum64(ss);
+    if (lane == 0) s_red[wave] = ss;
+    __syncthreads();
+    const float mean = (s_red[0] + s_red[1] + s_red[2] + s_red[3]) / (float)K;
+    const float r = 1.0f / __builtin_sqrtf(mean + eps);
+#pragma unroll
+    for (int q = 0; q < kXReg; ++q) {
+      const int i = tid + 256 * q;
+      if (i < nch) {
+        float v[8], g[8];
+        unpack8(xr[q], v);
+        unpack8(gr[q], g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = (v[e] * r) * g[e];
+        sx[i] = pack8(v);
+      }
+    }
+    for (int i = tid + 256 * kXReg; i < nch; i += 256) {
+      float v[8], g[8];
+      unpack8(*reinterpret_cast<const uint4*>(x + 8 * i), v);
+      unpack8(*reinterpret_cast<const uint4*>(norm_w + 8 * i), g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (v[e] * r) * g[e];
+      sx[i] = pack8(v);
+    }
+  } else {
+    for (int i = tid; i < nch; i += 256) sx[i] = *reinterpret_cast<const uint4*>(x + 8 * i);
+  }
+  __syncthreads();
+
+  float acc[R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = 0.f;
+  for (int c0 = lane;;) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      if (c0 + 64 * u < nch) {
+        const uint4 xv = sx[c0 + 64 * u];
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float d = dot2bf(wv[u][r].x, xv.x, acc[r]);
+          d = dot2bf(wv[u][r].y, xv.y, d);
+          d = dot2bf(wv[u][r].z, xv.z, d);
+          acc[r] = dot2bf(wv[u][r].w, xv.w, d);
+        }
+      }
+    }
+    c0 += 64 * U;
+    if (c0 >= nch) break;
+    SOLORT_GEMV_LOADS(c0)
+  }
+#undef SOLORT_GEMV_LOADS
+#pragma unroll
+  for (int r = 0; r < R; ++r) acc[r] = wave_sum64(acc[r]);
+
+  // Epilogue: lane i < NO stores output o0 + i.
+  if (lane < NO) {
+    float a = acc[0], b = 0.f;
+#pragma unroll
+    for (int i = 1; i < NO; ++i)
+      if (lane == i) a = acc[i];
+    if constexpr (EPI == kGemvSwiglu) {
+#pragma unroll
+      for (int i = 0; i < NO; ++i)
+        if (lane == i) b = acc[NO + i];
+    }
+    const int o = o0 + lane;
+    if (o < n_out) {
+      float y;
+      if constexpr (EPI == kGemvPlain) {
+        y = a;
+      } else if constexpr (EPI == kGemvResid) {
+        y = bf2f(res[o]) + rbf(a);
+      } else {
+        y = silu_bf16(rbf(a)) * rbf(b);
+      }
+      out[o] = f2bf(y);
+    }
+  }
+}
+
+}  // namespace solort
+
+using namespace solort;
+
+extern "C" int solort_gemv(const void* w, int64_t w_row_stride, int n_out, int k, const void* x, const void* norm_w,
+                           float eps, const void* res, int mode, int64_t inter, void* out, solort_stream_t stream) {
+  const char* name = "gemv";
+  if (mode != kGemvPlain && mode != kGemvResid && mode != kGemvSwiglu)
+    return set_error(SOLORT_EINVAL, "%s: mode %d", name, mode);
+  if (n_out < 1 || k < 8 || k % 8 != 0 || k > 65536)
+    return set_error(SOLORT_EINVAL, "%s: bad shape n_out=%d k=%d (k a multiple of 8, <= 65536)", name, n_out, k);
+  if (w_row_stride < k || w_row_stride % 8 != 0)
+    return set_error(SOLORT_EINVAL, "%s: w_row_stride %lld", name, (long long)w_row_stride);
+  if (!w || !x || !out || (mode == kGemvResid && !res)) return set_error(SOLORT_EINVAL, "%s: null pointer", name);
+  if (!aligned16(w) || !aligned16(x) || (norm_w && !aligned16(norm_w)) || ((uintptr_t)out & 1u) ||
+      (res && ((uintptr_t)res & 1u)))
+    return set_error(SOLORT_EINVAL, "%s: w, x and norm_w must be 16-byte aligned", name);
+  if (mode == kGemvSwiglu && inter < n_out)
+    return set_error(SOLORT_EINVAL, "%s: swiglu needs inter >= n_out (up rows follow the gate rows)", name);
+  // Rows per wavefront: enough workgroups (4 wavefronts each) for two per CU.
+  int R = 4;
+  const int per = mode == kGemvSwiglu ? 2 : 1;  // weight rows per output
+  if ((int64_t)n_out * per / (4 * 4) < 512) R = 2;
+  if ((int64_t)n_out * per / (4 * 2) < 512) R = mode == kGemvSwiglu ? 2 : 1;
+  const int no = mode == kGemvSwiglu ? R / 2 : R;
+  const int64_t blocks = ((int64_t)n_out + 4 * no - 1) / (4 * no);
+  if (blocks > 0x7fffffff) return set_error(SOLORT_EINVAL, "%s: too many rows", name);
+  const size_t lds = (size_t)k * 2;
+  hipStream_t s = (hipStream_t)stream;
+  const bool norm = norm_w != nullptr;
+  // Chunks per row in flight: 5 when a lane's share is a multiple of 5 (k = 2560: one batch) or for
+  // four-row wavefronts (registers); single-row wavefronts take up to 20 (k = 9728: one batch); else 8.
+  const int cpl = (k / 8 + 63) / 64;
+  const int U = (R == 4 || cpl % 5 == 0 || cpl < 5) ? 5 : (R == 1 && cpl > 8 && cpl <= 20 ? 20 : 8);
+#define SOLORT_GEMV_U(RR, UU, EE, NN)                                                                         \
+  hipLaunchKernelGGL((gemv_kernel<RR, UU, EE, NN>), dim3((unsigned)blocks), dim3(256), lds, s,               \
+                     (const uint16_t*)w, w_row_stride, n_out, k, (const uint16_t*)x, (const uint16_t*)norm_w,   \
+                     eps, (const uint16_t*)res, inter, (uint16_t*)out)
+#define SOLORT_GEMV(RR, EE, NN)                              \
+  do {                                                       \
+    if (U == 5) SOLORT_GEMV_U(RR, 5, EE, NN);                \
+    else if (U == 8) SOLORT_GEMV_U(RR, 8, EE, NN);           \
+    else SOLORT_GEMV_U(1, 20, EE, NN); /* U = 20 only with R = 1 */ \
+  } while (0)
+#define SOLORT_GEMV_R(EE, NN)        \
+  switch (R) {                       \
+    case 1: SOLORT_GEMV(1, EE, NN); break; \
+    case 2: SOLORT_GEMV(2, EE, NN); break; \
+    default: SOLORT_GEMV(4, EE, NN); break; \
+  }
+  if (mode == kGemvPlain) {
+    if (norm) { SOLORT_GEMV_R(kGemvPlain, true) } else { SOLORT_GEMV_R(kGemvPlain, false) }
+  } else if (mode == kGemvResid) {
+    if (norm) { SOLORT_GEMV_R(kGemvResid, true) } else { SOLORT_GEMV_R(kGemvResid, false) }
+  } else {  // R is 2 or 4 here
+    if (norm) {
+      if (R == 2) SOLORT_GEMV(2, kGemvSwiglu, true); else SOLORT_GEMV(4, kGemvSwiglu, true);
+    } else {
+      if (R == 2) SOLORT_GEMV(2, kGemvSwiglu, false); else SOLORT_GEMV(4, kGemvSwiglu, false);
+    }
+  }
+#undef SOLORT_GEMV_R
+#undef SOLORT_GEMV
+#undef SOLORT_GEMV_U
+  return check_launch(name);
+}

@@ -337,3 +337,37 @@ def accept_prefix(target: torch.Tensor, draft: torch.Tensor, out: torch.Tensor) 
     _need(out.is_contiguous() and out.numel() >= 2, "out must hold 2 int64")
     rc = _lib.load().solort_accept_prefix(target.data_ptr(), draft.data_ptr(), k, out.data_ptr(), _stream(target))
     _lib.check(rc, "accept_prefix")
+
+
+GEMV_PLAIN, GEMV_RESID, GEMV_SWIGLU = 0, 1, 2
+
+
+def gemv(w: torch.Tensor, x: torch.Tensor, out: torch.Tensor, norm_w: torch.Tensor | None = None,
+         eps: float = 1e-6, res: torch.Tensor | None = None, mode: int = GEMV_PLAIN, inter: int = 0) -> None:
+    """One-token matrix-vector product out = W x with the decode step's fused neighbours (see
+    solort_gemv): optional RMSNorm of x (norm_w), residual add (mode GEMV_RESID, res, may be out), or
+    SwiGLU over gate rows 0..n-1 and up rows inter..inter+n-1 (GEMV_SWIGLU).  w [rows, k] bf16, x [k]
+    bf16, out [n] bf16."""
+    for name, t in (("w", w), ("x", x), ("out", out)):
+        _on_gpu(name, t, torch.bfloat16)
+    _need(w.dim() == 2 and w.stride(1) == 1, "w must be [rows, k] with unit column stride")
+    k = w.shape[1]
+    _need(x.numel() == k and x.is_contiguous(), f"x must hold k = {k} contiguous values")
+    n = out.numel()
+    _need(out.is_contiguous(), "out must be contiguous")
+    if mode == GEMV_SWIGLU:
+        _need(inter >= n and w.shape[0] >= inter + n, f"w must hold gate and up rows (inter {inter}, n {n})")
+    else:
+        _need(w.shape[0] >= n, f"w has {w.shape[0]} rows, fewer than n = {n}")
+    if norm_w is not None:
+        _on_gpu("norm_w", norm_w, torch.bfloat16)
+        _need(norm_w.numel() == k and norm_w.is_contiguous(), f"norm_w must hold k = {k} values")
+    if mode == GEMV_RESID:
+        _need(res is not None, "GEMV_RESID needs res")
+        _on_gpu("res", res, torch.bfloat16)
+        _need(res.numel() == n and res.is_contiguous(), f"res must hold n = {n} values")
+    rc = _lib.load().solort_gemv(w.data_ptr(), w.stride(0), n, k, x.data_ptr(),
+                                 None if norm_w is None else norm_w.data_ptr(), float(eps),
+                                 None if res is None else res.data_ptr(), int(mode), int(inter), out.data_ptr(),
+                                 _stream(w))
+    _lib.check(rc, "gemv")

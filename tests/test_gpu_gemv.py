@@ -1,0 +1,109 @@
+"""GPU parity of the decode-step GEMVs (solort_gemv) with their fused RMSNorm, residual and SwiGLU.
+
+Bar (floating point): every output within four bf16 ulps (2^-6 relative) plus 2e-3 of the fp64 value
+of the same computation on the same bf16 inputs, and mean relative error <= 2e-3.  The kernel's fp32
+sums run in a different order than a BLAS, so a result can land one rounding away; a wrong row,
+scale, norm or epilogue shows up as errors of order one.  Compared also with the torch restatement
+of the reference's ops (oracle/ref.py).  Shapes: Qwen3-4B's fused QKV, o_proj, gate_up and down,
+the lm_head, and ragged small ones.
+"""
+from __future__ import annotations
+
+import sys
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import ref
+from solort_amd import ops
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def _close(got: torch.Tensor, want: np.ndarray, what: str) -> None:
+    got = got.float().cpu().numpy().astype(np.float64).reshape(want.shape)
+    err = np.abs(got - want)
+    rel = err / (np.abs(want) + 1e-3)
+    _say(f"  {what}: max-abs {err.max():.3e}, mean rel {rel.mean():.3e}, worst ulp-scaled "
+         f"{(err / (np.abs(want) * 2 ** -8 + 1e-6)).max():.2f}")
+    assert (err <= np.abs(want) * 2 ** -6 + 2e-3).all(), what
+    assert rel.mean() <= 2e-3, what
+
+
+def _data(n_rows, k, seed):
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(n_rows, k, generator=g) * 0.02).to(torch.bfloat16)
+    x = torch.randn(k, generator=g).to(torch.bfloat16)
+    nw = (torch.randn(k, generator=g) * 0.1 + 1).to(torch.bfloat16)
+    return w, x, nw
+
+
+@pytest.mark.parametrize("n,k,norm", [(6144, 2560, True), (151936, 2560, True), (7, 24, False), (1000, 136, True),
+                                      (2560, 4096, False)], ids=["qkv", "lm_head", "tiny", "odd", "plain"])
+def test_gemv_plain(gpu, n, k, norm):
+    _say(f"[gemv plain n={n} k={k} norm={norm}]")
+    w, x, nw = _data(n, k, 40 + n % 97)
+    out = torch.empty(n, dtype=torch.bfloat16, device=gpu)
+    ops.gemv(w.to(gpu), x.to(gpu), out, nw.to(gpu) if norm else None, 1e-6)
+    torch.cuda.synchronize()
+    xin = ref.rmsnorm(x.view(1, k), nw, 1e-6).view(k) if norm else x
+    _close(out, w.double().numpy() @ xin.double().numpy(), "vs fp64 of the same bf16 input")
+    _close(out, ref.linear(xin.view(1, k), w).float().numpy().reshape(n).astype(np.float64), "vs torch ops")
+
+
+@pytest.mark.parametrize("n,k", [(2560, 4096), (2560, 9728), (33, 520)], ids=["o_proj", "down", "small"])
+def test_gemv_residual_in_place(gpu, n, k):
+    _say(f"[gemv residual n={n} k={k}]")
+    w, x, _ = _data(n, k, 50 + k % 97)
+    g = torch.Generator().manual_seed(51)
+    res = torch.randn(n, generator=g).to(torch.bfloat16)
+    buf = res.to(gpu).clone()
+    ops.gemv(w.to(gpu), x.to(gpu), buf, res=buf, mode=ops.GEMV_RESID)  # x = x + W ctx, in place
+    torch.cuda.synchronize()
+    lin = ref.linear(x.view(1, k), w).view(n)
+    want = (res.double() + lin.double()).numpy()
+    _close(buf, want, "vs fp64 of res + bf16(W x)")
+    _close(buf, (res + lin).float().numpy().astype(np.float64), "vs torch ops")
+
+
+@pytest.mark.parametrize("inter,k", [(9728, 2560), (100, 264)], ids=["gate_up", "small"])
+def test_gemv_swiglu(gpu, inter, k):
+    _say(f"[gemv swiglu inter={inter} k={k}]")
+    w, x, nw = _data(2 * inter, k, 60 + inter % 97)
+    out = torch.empty(inter, dtype=torch.bfloat16, device=gpu)
+    ops.gemv(w.to(gpu), x.to(gpu), out, nw.to(gpu), 1e-6, mode=ops.GEMV_SWIGLU, inter=inter)
+    torch.cuda.synchronize()
+    h2 = ref.rmsnorm(x.view(1, k), nw, 1e-6)
+    gate, up = ref.linear(h2, w).split(inter, dim=-1)
+    want = (F.silu(gate) * up).view(inter)
+    g64, u64 = gate.double().view(inter).numpy(), up.double().view(inter).numpy()
+    _close(out, g64 / (1 + np.exp(-g64)) * u64, "vs fp64 silu(g) * u of the bf16 g, u")
+    _close(out, want.float().numpy().astype(np.float64), "vs torch ops")
+
+
+def test_decode_mlp_block_chain(gpu):
+    """o_proj + residual, post-norm + gate_up + SwiGLU, down + residual: the reference's layer tail."""
+    K, I = 2560, 9728
+    g = torch.Generator().manual_seed(70)
+    x = torch.randn(K, generator=g).to(torch.bfloat16)
+    ctx = torch.randn(4096, generator=g).to(torch.bfloat16)
+    wo = (torch.randn(K, 4096, generator=g) * 0.02).to(torch.bfloat16)
+    ln = (torch.randn(K, generator=g) * 0.1 + 1).to(torch.bfloat16)
+    wgu = (torch.randn(2 * I, K, generator=g) * 0.02).to(torch.bfloat16)
+    wd = (torch.randn(K, I, generator=g) * 0.02).to(torch.bfloat16)
+    xd, act = x.to(gpu), torch.empty(I, dtype=torch.bfloat16, device=gpu)
+    ops.gemv(wo.to(gpu), ctx.to(gpu), xd, res=xd, mode=ops.GEMV_RESID)
+    ops.gemv(wgu.to(gpu), xd, act, ln.to(gpu), 1e-6, mode=ops.GEMV_SWIGLU, inter=I)
+    ops.gemv(wd.to(gpu), act, xd, res=xd, mode=ops.GEMV_RESID)
+    torch.cuda.synchronize()
+    want = ref.decode_mlp_block(x.view(1, K), ctx.view(1, 4096), wo, ln, wgu, wd, 1e-6).view(K)
+    err = (xd.float().cpu() - want.float()).abs()
+    _say(f"  chain vs torch ops: max-abs {err.max().item():.3e} mean-abs {err.mean().item():.3e}")
+    assert err.max().item() <= 5e-2 and err.mean().item() <= 2e-3

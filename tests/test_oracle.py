@@ -330,3 +330,35 @@ def test_accept_prefix_matches_a_first_mismatch_scan():
             scan = next((i for i in range(k) if int(tg[i]) != int(draft[i])), k)
             assert (a, nxt) == (scan, int(tg[scan]))
             assert a == miss
+
+
+def test_rmsnorm_linear_and_mlp_block_restatements():
+    """ref.rmsnorm / ref.linear / ref.decode_mlp_block against fp64 numpy with one bf16 rounding per
+    tensor (cuda_graph_executor.py:25-28, :185-188)."""
+    g = torch.Generator().manual_seed(33)
+    K, N, I = 256, 96, 160
+    x = torch.randn(1, K, generator=g).to(torch.bfloat16)
+    w = (torch.randn(K, generator=g) * 0.1 + 1).to(torch.bfloat16)
+    xd, wd_ = x.double().numpy(), w.double().numpy()
+    want = exact.bf16_round((xd / np.sqrt((xd ** 2).mean(-1, keepdims=True) + 1e-6) * wd_).astype(np.float32))
+    got = ref.rmsnorm(x, w, 1e-6).float().numpy()
+    assert (np.abs(got - want) <= np.abs(want) * 2 ** -7 + 1e-6).all()  # at most one bf16 ulp apart
+    # constant row: y = sign(c) * w (bf16)
+    c = torch.full((1, K), -3.0, dtype=torch.bfloat16)
+    assert torch.equal(ref.rmsnorm(c, w, 0.0), (-w.float()).to(torch.bfloat16).view(1, K))
+    W = (torch.randn(N, K, generator=g) * 0.05).to(torch.bfloat16)
+    lin = ref.linear(x, W).float().numpy()
+    ex = xd @ W.double().numpy().T
+    assert (np.abs(lin - ex) <= np.abs(ex) * 2 ** -8 + 1e-5).all()  # one rounding of the fp32 sum
+    # the MLP tail: residual, norm, gate/up split, silu * up, residual
+    ctx = torch.randn(1, K, generator=g).to(torch.bfloat16)
+    wo = (torch.randn(K, K, generator=g) * 0.05).to(torch.bfloat16)
+    wgu = (torch.randn(2 * I, K, generator=g) * 0.05).to(torch.bfloat16)
+    wdn = (torch.randn(K, I, generator=g) * 0.05).to(torch.bfloat16)
+    out = ref.decode_mlp_block(x, ctx, wo, w, wgu, wdn, 1e-6).double().numpy()
+    x1 = x.double().numpy() + ref.linear(ctx, wo).double().numpy()
+    h2 = ref.rmsnorm(torch.from_numpy(x1).to(torch.bfloat16), w, 1e-6).double().numpy()
+    gu = h2 @ wgu.double().numpy().T
+    act = gu[:, :I] / (1 + np.exp(-gu[:, :I])) * gu[:, I:]
+    want = x1 + act @ wdn.double().numpy().T
+    assert np.abs(out - want).max() < 0.05 and np.abs(out - want).mean() < 5e-3
