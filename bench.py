@@ -54,10 +54,11 @@ def parse() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-sweep", action="store_true", help="skip the per-bucket decode extras")
-    p.add_argument("--only", choices=("all", "decode", "prefill", "long", "verify", "gemv"), default="all",
+    p.add_argument("--only", choices=("all", "decode", "prefill", "long", "verify", "gemv", "model"), default="all",
                    help="decode: the decode step and its kernel only; prefill: the prefill kernels only; "
                         "long: the Qwen3-8B KV 32768 decode only; verify: the speculative verify and argmax "
-                        "only (for per-workload profiles)")
+                        "only; gemv: the decode-step GEMVs only; model: whole-model greedy decode only (for "
+                        "per-workload profiles)")
     return p.parse_args()
 
 
@@ -110,6 +111,11 @@ def main() -> int:
         return 0
     if args.only == "gemv":
         print(json.dumps({"decode_gemv": gemv_extras(torch, ops, dev)}), flush=True)
+        return 0
+    if args.only == "model":
+        del runners
+        torch.cuda.empty_cache()
+        print(json.dumps({"decode_model": model_extras(torch, dev)}), flush=True)
         return 0
 
     # ---------------------------------------------------------------- timed graph replays
@@ -166,6 +172,7 @@ def main() -> int:
         result["extras"].update(verify_extras(torch, ops, wl, runners, dev, sh))
         result["extras"]["decode_8b_kv32768"] = long_decode_extras(torch, ops, wl, dev)
         result["extras"]["decode_gemv"] = gemv_extras(torch, ops, dev)
+        result["extras"]["decode_model"] = model_extras(torch, dev)
     if args.only == "all":
         result["prefill"] = prefill_extras(torch, ops, runners, dev, sh)
         p1024 = result["prefill"].get("1024")
@@ -291,6 +298,43 @@ def gemv_extras(torch, ops, dev, copies: int = 4) -> dict:
     layer = sum(out[n]["us"] for n in ("qkv", "o_proj", "gate_up", "down"))
     out["layer_gemv_us"] = round(layer, 3)
     out["layer_torch_linear_us"] = round(sum(out[n]["torch_linear_us"] for n in ("qkv", "o_proj", "gate_up", "down")), 3)
+    return out
+
+
+def model_extras(torch, dev, live: int = 960, n: int = 48) -> dict:
+    """Whole-model greedy decode of a random-weight Qwen3-4B (36 layers, tied 151,936 x 2560
+    embedding, 8.05 GB of bf16 weights): one graph replay per token, tokens `live`..`live`+n-1 in the
+    KV 1024 bucket over a seeded N(0,1) context, HIP events around n back-to-back replays.  Bytes per
+    token = every weight matrix once (the layer GEMVs and the lm_head) plus the K/V rows read."""
+    from solort_amd.model import QWEN3_4B, GraphQwen3Decode, RandomQwen3
+    s = QWEN3_4B
+    w = RandomQwen3(s, dev, seed=1011)
+    m = GraphQwen3Decode(w, 1024)
+    gen = torch.Generator(device=dev).manual_seed(1012)
+    m.kc[:, :live].copy_(torch.randn(s.layers, live, s.nkv, 128, generator=gen, device=dev).to(torch.bfloat16))
+    m.vc[:, :live].copy_(torch.randn(s.layers, live, s.nkv, 128, generator=gen, device=dev).to(torch.bfloat16))
+    m.generate(11, live, n)  # captures the bucket's graph and warms every kernel
+    g = m.graph(1024)
+    m.tok.fill_(11)
+    m.pos.fill_(live)
+    m.step.zero_()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(n):
+        g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / n
+    wbytes = 2 * (s.layers * s.hidden * (s.qkv_width + s.nh * 128 + 3 * s.inter) + s.vocab * s.hidden)
+    kvbytes = s.layers * 2 * (live + n // 2) * s.nkv * 128 * 2
+    out = {"model": s.name, "tokens_per_s": round(1e3 / ms, 1), "ms_per_token": round(ms, 4),
+           "bytes_per_token": wbytes + kvbytes, "gbps": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9, 1),
+           "frac_hbm": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+           "live_start": live, "tokens": n, "first_tokens": m.tokens[:8].tolist()}
+    del m, w, g
+    torch.cuda.empty_cache()
     return out
 
 

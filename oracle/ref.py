@@ -111,13 +111,6 @@ def verify_attn(q: torch.Tensor, kc_l: torch.Tensor, vc_l: torch.Tensor, pos0: i
     return ctx.transpose(0, 1).reshape(k1, nh * hd)
 
 
-def rmsnorm(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
-    """cuda_graph_executor.py:25-28, over the last dim, in the dtype of x."""
-    d = x.float()
-    d = d * torch.rsqrt(d.pow(2).mean(-1, keepdim=True) + eps)
-    return (d * w.float()).to(x.dtype)
-
-
 def linear(x: torch.Tensor, w: torch.Tensor) -> torch.Tensor:
     """x @ w.T in x's dtype with fp32 accumulation (the bf16 GEMMs of :171, :185, :187, :188, :190),
     evaluated on the CPU in fp32 and rounded once."""
@@ -161,3 +154,25 @@ def decode_layers(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps
         write_kv(kc[li], vc[li], k, v, pos)
         out.append(decode_attn(q, kc[li], vc[li], pos, bound, scale))
     return torch.cat(out, dim=0)
+
+
+def decode_model_step(w: dict, tok: int, pos: int, kc: torch.Tensor, vc: torch.Tensor, bound: int, nh: int,
+                      nkv: int, eps: float = 1e-6, theta: float = 1e6) -> torch.Tensor:
+    """One greedy decode step of a whole model, cuda_graph_executor.py:163-190, on the CPU:
+    embedding row, per layer input norm + fused QKV, q/k norm + RoPE + KV write + grouped attention,
+    o_proj + residual, post norm + fused gate/up + silu(gate) * up + down + residual; final norm and
+    lm_head.  w holds CPU tensors (embed, in_ln, post_ln, qn, kn, wqkv, wo, wgu, wd, final_norm,
+    lm_head; per-layer entries indexable by layer).  kc/vc [L, max_len, nkv, hd] are written in
+    place.  Every intermediate is rounded to the weights' dtype: bf16 as the reference runs, or fp32
+    weights and caches for an unrounded yardstick of the same model.  Returns the logits [V]."""
+    hd = kc.shape[-1]
+    cos, sin = cos_sin(torch.tensor([pos]), inv_freq(hd, theta), w["embed"].dtype)
+    x = w["embed"][tok].view(1, -1)
+    for li in range(kc.shape[0]):
+        h = rmsnorm(x, w["in_ln"][li], eps)
+        qkv = linear(h, w["wqkv"][li])
+        q, k, v = prologue(qkv, w["qn"][li], w["kn"][li], eps, cos, sin, nh, nkv, hd)
+        write_kv(kc[li], vc[li], k, v, pos)
+        ctx = decode_attn(q, kc[li], vc[li], pos, bound, hd ** -0.5)
+        x = decode_mlp_block(x, ctx.view(1, -1), w["wo"][li], w["post_ln"][li], w["wgu"][li], w["wd"][li], eps)
+    return linear(rmsnorm(x, w["final_norm"], eps), w["lm_head"]).view(-1)
