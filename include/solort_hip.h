@@ -241,6 +241,41 @@ int solort_accept_prefix(const int64_t* target, const int64_t* draft, int k, int
 int solort_gemv(const void* w, int64_t w_row_stride, int n_out, int k, const void* x, const void* norm_w, float eps,
                 const void* res, int mode, int64_t inter, void* out, solort_stream_t stream);
 
+/* Workspace bytes for solort_gemv_argmax with n_out outputs (one 8-byte key
+ * per workgroup; no zero-fill needed). */
+size_t solort_gemv_argmax_workspace_bytes(int n_out);
+
+/*
+ * The lm_head product fused with the greedy argmax, one token: logits =
+ * _rmsnorm(x, norm_w) @ W.T (norm_w may be NULL), then out_idx[0] =
+ * argmax(logits.float()) with the lowest index winning ties and NaN ranked
+ * highest, as cuda_graph_executor.py:189-190 followed by :206 computes it.
+ * The index is bit-identical to solort_argmax_rows over solort_gemv's bf16
+ * logits (the key is taken from the same bf16-rounded value).  Each
+ * workgroup of the product stores the best (value, index) key of its outputs
+ * in ws; a one-workgroup launch reduces those keys into out_idx.  With
+ * out_idx NULL that launch is skipped and the keys stay in ws for
+ * solort_greedy_advance.  logits [n_out] bf16 is written when non-NULL.  ws:
+ * solort_gemv_argmax_workspace_bytes(n_out) bytes, 8-byte aligned; calls
+ * that overlap in time must not share it.
+ */
+int solort_gemv_argmax(const void* w, int64_t w_row_stride, int n_out, int k, const void* x, const void* norm_w,
+                       float eps, void* logits, int64_t* out_idx, void* ws, solort_stream_t stream);
+
+/*
+ * The tail of a greedy decode step and the head of the next, in one launch
+ * after solort_gemv_argmax(..., out_idx = NULL, ws): the argmax token t of the
+ * keys in ws (vocab = that call's n_out) becomes the next input, *tok = t
+ * (tok_buf, cuda_graph_executor.py:206 and :241), is recorded at
+ * tokens[*step] when *step < max_tokens (the chunk's token list, :372-374),
+ * *step and *pos advance by one (pos_buf, :242), and x [hidden] bf16 receives
+ * embed row t (x = self.embed[self.tok_buf], :165).  embed [vocab,
+ * embed_row_stride] bf16 16-byte aligned, hidden a multiple of 8.
+ */
+int solort_greedy_advance(const void* ws, int vocab, const void* embed, int64_t embed_row_stride, int hidden,
+                          void* x, int64_t* tok, int64_t* tokens, int max_tokens, int64_t* step, int64_t* pos,
+                          solort_stream_t stream);
+
 /* Workspace bytes for solort_argmax_rows with `rows` rows. Allocate once,
  * zero-fill once, reuse; overlapping calls must not share it. */
 size_t solort_argmax_workspace_bytes(int rows);

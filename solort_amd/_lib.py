@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before ours)
 
 LIB_PATH = Path(__file__).resolve().parent / "libsolort_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 # name -> (restype, argtypes); mirrors include/solort_hip.h
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -64,6 +64,14 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "solort_gemv": (
         c_int,
         [c_void_p, c_int64, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_int, c_int64, c_void_p, c_void_p],
+    ),
+    "solort_gemv_argmax_workspace_bytes": (c_size_t, [c_int]),
+    "solort_gemv_argmax": (
+        c_int, [c_void_p, c_int64, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p, c_void_p],
+    ),
+    "solort_greedy_advance": (
+        c_int, [c_void_p, c_int, c_void_p, c_int64, c_int, c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_void_p,
+                c_void_p],
     ),
     "solort_argmax_workspace_bytes": (c_size_t, [c_int]),
     "solort_argmax_rows": (

@@ -15,17 +15,6 @@
 
 namespace solort {
 
-__device__ __forceinline__ uint64_t argmax_key(float f, int64_t idx) {
-  uint32_t u = __float_as_uint(f);
-  uint32_t k;
-  if ((u & 0x7fffffffu) > 0x7f800000u) k = 0xffffffffu;        // NaN
-  else if ((u & 0x7fffffffu) == 0u) k = 0x80000000u;           // +-0
-  else k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-  return ((uint64_t)k << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
-}
-
-__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
-
 template <int F32>
 __global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict__ logits, int64_t vocab,
                                                           int64_t row_stride, int64_t per_block,
@@ -34,7 +23,6 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict
                                                           int64_t* __restrict__ out) {
   constexpr int VEC = F32 ? 4 : 8;  // elements per 16-byte load
   __shared__ uint64_t s_best[4];
-  __shared__ unsigned s_ticket;
   const int tid = threadIdx.x;
   const int row = blockIdx.y;
   const int64_t beg = (int64_t)blockIdx.x * per_block;
@@ -66,17 +54,9 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict
   for (int mask = 32; mask >= 1; mask >>= 1) best = umax64(best, __shfl_xor(best, mask, 64));
   if ((tid & 63) == 0) s_best[tid >> 6] = best;
   __syncthreads();
-  if (tid == 0) {
-    best = umax64(umax64(s_best[0], s_best[1]), umax64(s_best[2], s_best[3]));
-    __hip_atomic_fetch_max(ws_best + row, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_ticket = __hip_atomic_fetch_add(ws_cnt + row, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    if (s_ticket == gridDim.x - 1) {
-      const uint64_t k = __hip_atomic_load(ws_best + row, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT);
-      out[row] = (int64_t)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
-      __hip_atomic_store(ws_best + row, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(ws_cnt + row, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-  }
+  if (tid == 0)
+    argmax_fold(umax64(umax64(s_best[0], s_best[1]), umax64(s_best[2], s_best[3])), ws_best + row, ws_cnt + row,
+                gridDim.x, out + row);
 }
 
 }  // namespace solort

@@ -173,4 +173,43 @@ __device__ __forceinline__ void lds_barrier() {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Greedy-argmax key of (value, index): high word = an order-preserving image
+// of the fp32 value (-0 and +0 equal, NaN above every number), low word =
+// 0xffffffff - index, so the integer maximum is torch.argmax's answer (the
+// lowest index among equal maxima, the first NaN if there is one).
+__device__ __forceinline__ uint64_t argmax_key(float f, int64_t idx) {
+  uint32_t u = __float_as_uint(f);
+  uint32_t k;
+  if ((u & 0x7fffffffu) > 0x7f800000u) k = 0xffffffffu;        // NaN
+  else if ((u & 0x7fffffffu) == 0u) k = 0x80000000u;           // +-0
+  else k = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)k << 32) | (uint64_t)(0xffffffffu - (uint32_t)idx);
+}
+
+__device__ __forceinline__ uint64_t umax64(uint64_t a, uint64_t b) { return a > b ? a : b; }
+
+// Folds a workgroup's best key into the row's slot and lets the last
+// workgroup of the grid (atomic ticket) decode the index and clear the slot
+// and ticket for the next launch.  Called by one thread per workgroup.
+//
+// Only atomics carry data between workgroups, so no release/acquire fence is
+// needed (on gfx950 an agent-scope fence is an L2 writeback plus invalidate,
+// which per workgroup of a 10,000-workgroup grid cost 4x the whole kernel).
+// The ticket must not be counted before the max has been performed: it is
+// issued with an operand computed from the max's returned value, so it waits
+// for that return.  The last workgroup reads the slot with an atomic
+// read-modify-write, after its ticket returned.
+__device__ __forceinline__ void argmax_fold(uint64_t best, uint64_t* slot, unsigned* ticket, unsigned nblocks,
+                                            int64_t* out) {
+  const uint64_t prev = __hip_atomic_fetch_max(slot, best, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  unsigned zero;
+  asm volatile("v_and_b32 %0, 0, %1" : "=v"(zero) : "v"((uint32_t)prev));
+  if (__hip_atomic_fetch_add(ticket, 1u + zero, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nblocks - 1) {
+    const uint64_t k = __hip_atomic_fetch_max(slot, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *out = (int64_t)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
+    __hip_atomic_store(slot, (uint64_t)0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(ticket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
 }  // namespace solort

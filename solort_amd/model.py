@@ -7,13 +7,14 @@ the fused QKV and gate/up weights of :54-63, the embedding row (:165), final nor
 so the weights are seeded random tensors of the real shapes; every launch and byte moved is what
 the real model would cost.
 
-Per token (graph of one bucket): embedding row -> cos/sin rows -> per layer
+Per token (graph of one bucket): cos/sin rows -> per layer
   solort_gemv (RMSNorm + QKV) -> solort_decode_layer (q/k norm + RoPE + KV write + split-KV
   attention) -> solort_gemv (o_proj + residual) -> solort_gemv (RMSNorm + gate_up + SwiGLU) ->
   solort_gemv (down + residual)
--> solort_gemv (final RMSNorm + lm_head) -> solort_argmax_rows into the token buffer, which the next
-replay embeds; the position advances and the token is recorded on the device, so K replays give K
-tokens with one host synchronisation, as the reference's chunked greedy decode does.
+-> solort_gemv_argmax (final RMSNorm + lm_head, each workgroup keeping the argmax key of its
+logits) -> solort_greedy_advance (the token becomes the next input and is recorded, position and
+count advance, and the token's embedding row becomes the next step's x).  K replays give K tokens
+with one host synchronisation, as the reference's chunked greedy decode does (:362-374).
 """
 from __future__ import annotations
 
@@ -76,8 +77,13 @@ class GraphQwen3Decode:
     """Greedy decode over a runner-owned bf16 KV cache, one captured graph per KV bucket."""
 
     def __init__(self, weights: RandomQwen3, max_len: int, eps: float = 1e-6, theta: float = 1e6,
-                 max_tokens: int = 4096) -> None:
+                 max_tokens: int = 4096, fused_tail: bool = True) -> None:
+        """fused_tail: the argmax folded into the lm_head launch and the token bookkeeping plus the
+        next embedding row in one launch (solort_gemv_argmax + solort_greedy_advance); False runs
+        the same step as the reference's separate ops (lm_head, argmax, token copy, counter adds,
+        embedding gather).  Both give the same tokens bit for bit."""
         self.w = weights
+        self.fused_tail = bool(fused_tail)
         s = self.s = weights.shape
         self.dev = weights.embed.device
         self.max_len, self.eps, self.scale = int(max_len), float(eps), HD ** -0.5
@@ -98,14 +104,23 @@ class GraphQwen3Decode:
         self.logits = torch.zeros(1, s.vocab, **bf)
         self.cs = torch.zeros(2, 1, HD // 2, **bf)
         self.ws = ops.attn_workspace(1, s.nh, s.nkv, max(decode_splits(b, s.nkv) for b in self.buckets), self.dev)
-        self.ws_arg = ops.argmax_workspace(1, self.dev)
+        self.ws_arg = ops.gemv_argmax_workspace(s.vocab, self.dev) if fused_tail else ops.argmax_workspace(1, self.dev)
         self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
 
+    def start(self, token: int, pos: int) -> None:
+        """The first input: token at position pos (rows 0..pos-1 of the cache hold the context)."""
+        self.tok.fill_(int(token))
+        self.pos.fill_(int(pos))
+        self.step.zero_()
+        torch.index_select(self.w.embed, 0, self.tok, out=self.x)     # :165 for the first step
+
     def _step(self, bound: int) -> None:
-        """One token: cuda_graph_executor.py:163-190, then argmax (:206) into self.tok."""
+        """One token: cuda_graph_executor.py:163-190 from the x the previous step (or start) left,
+        then argmax (:206), the token bookkeeping of :241-242 and :372, and the next step's :165."""
         s, w = self.s, self.w
         ns = decode_splits(bound, s.nkv)
-        torch.index_select(w.embed, 0, self.tok, out=self.x)          # :165
+        if not self.fused_tail:
+            torch.index_select(w.embed, 0, self.tok, out=self.x)                                       # :165
         ops.rope_rows(self.inv_freq, self.pos, 1, self.cs)             # :164, once per step
         x = self.x.view(s.hidden)
         for li in range(s.layers):
@@ -116,11 +131,16 @@ class GraphQwen3Decode:
             ops.gemv(w.wgu[li], x, self.act, w.post_ln[li], self.eps, mode=ops.GEMV_SWIGLU,
                      inter=s.inter)                                                                    # :186-187
             ops.gemv(w.wd[li], self.act, x, res=x, mode=ops.GEMV_RESID)                                # :188
-        ops.gemv(w.lm_head, x, self.logits.view(-1), w.final_norm, self.eps)                          # :189-190
-        ops.argmax_rows(self.logits, self.tok, self.ws_arg)                                            # :206
-        self.tokens.index_copy_(0, self.step, self.tok)
-        self.step.add_(1)
-        self.pos.add_(1)
+        if self.fused_tail:
+            ops.gemv_argmax(w.lm_head, x, None, self.ws_arg, w.final_norm, self.eps,
+                            logits=self.logits.view(-1))                                               # :189-190, :206
+            ops.greedy_advance(self.ws_arg, s.vocab, w.embed, x, self.tok, self.tokens, self.step, self.pos)
+        else:
+            ops.gemv(w.lm_head, x, self.logits.view(-1), w.final_norm, self.eps)                      # :189-190
+            ops.argmax_rows(self.logits, self.tok, self.ws_arg)                                        # :206
+            self.tokens.index_copy_(0, self.step, self.tok)                                            # :372
+            self.step.add_(1)
+            self.pos.add_(1)                                                                           # :242
 
     def bucket_for(self, pos: int) -> int:
         """cuda_graph_executor.py:192-193: the first bucket strictly above the position."""
@@ -142,9 +162,7 @@ class GraphQwen3Decode:
         context): n graph replays, one synchronisation."""
         if n < 1 or n > self.tokens.numel() or pos + n > self.max_len:
             raise RuntimeError(f"cannot generate {n} tokens from position {pos} (max_len {self.max_len})")
-        self.tok.fill_(int(first_token))
-        self.pos.fill_(int(pos))
-        self.step.zero_()
+        self.start(first_token, pos)
         for i in range(n):
             self.graph(self.bucket_for(pos + i)).replay()
         return self.tokens[:n].tolist()

@@ -371,3 +371,64 @@ def gemv(w: torch.Tensor, x: torch.Tensor, out: torch.Tensor, norm_w: torch.Tens
                                  None if res is None else res.data_ptr(), int(mode), int(inter), out.data_ptr(),
                                  _stream(w))
     _lib.check(rc, "gemv")
+
+
+def gemv_argmax_workspace(n_out: int, device: torch.device | str) -> torch.Tensor:
+    """Workspace for gemv_argmax over n_out outputs (allocate once, reuse)."""
+    nbytes = _lib.load().solort_gemv_argmax_workspace_bytes(int(n_out))
+    _need(nbytes > 0, f"bad gemv_argmax workspace request n_out={n_out}")
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
+
+
+def gemv_argmax(w: torch.Tensor, x: torch.Tensor, out_idx: torch.Tensor | None, ws: torch.Tensor,
+                norm_w: torch.Tensor | None = None, eps: float = 1e-6, logits: torch.Tensor | None = None) -> None:
+    """out_idx[0] = argmax(rmsnorm(x, norm_w) @ w.T) (lowest index on ties, NaN is max), the argmax
+    folded into the product's workgroups, optionally writing the bf16 logits; see solort_gemv_argmax.
+    w [V, k] bf16, x [k] bf16, out_idx int64 [1] (None: leave the keys in ws for greedy_advance), ws from
+    gemv_argmax_workspace(V)."""
+    for name, t in (("w", w), ("x", x)):
+        _on_gpu(name, t, torch.bfloat16)
+    _need(w.dim() == 2 and w.stride(1) == 1, "w must be [rows, k] with unit column stride")
+    n, k = w.shape
+    _need(x.numel() == k and x.is_contiguous(), f"x must hold k = {k} contiguous values")
+    if out_idx is not None:
+        _need(out_idx.is_cuda and out_idx.dtype == torch.int64 and out_idx.numel() >= 1 and out_idx.is_contiguous(),
+              "out_idx must be int64 on the device")
+    lib = _lib.load()
+    need = lib.solort_gemv_argmax_workspace_bytes(n)
+    _need(need > 0 and ws.is_cuda and ws.numel() * ws.element_size() >= need and ws.data_ptr() % 8 == 0,
+          f"gemv_argmax workspace too small or misaligned: need {need} bytes, 8-byte aligned")
+    if norm_w is not None:
+        _on_gpu("norm_w", norm_w, torch.bfloat16)
+        _need(norm_w.numel() == k and norm_w.is_contiguous(), f"norm_w must hold k = {k} values")
+    if logits is not None:
+        _on_gpu("logits", logits, torch.bfloat16)
+        _need(logits.numel() == n and logits.is_contiguous(), f"logits must hold {n} values")
+    rc = lib.solort_gemv_argmax(w.data_ptr(), w.stride(0), n, k, x.data_ptr(),
+                                None if norm_w is None else norm_w.data_ptr(), float(eps),
+                                None if logits is None else logits.data_ptr(),
+                                None if out_idx is None else out_idx.data_ptr(), ws.data_ptr(), _stream(w))
+    _lib.check(rc, "gemv_argmax")
+
+
+def greedy_advance(ws: torch.Tensor, vocab: int, embed: torch.Tensor, x: torch.Tensor, tok: torch.Tensor,
+                   tokens: torch.Tensor | None, step: torch.Tensor, pos: torch.Tensor) -> None:
+    """After gemv_argmax(..., out_idx=None, ws): tok = the argmax token, tokens[step] = tok (if step <
+    tokens.numel()), step += 1, pos += 1, x = embed[tok]; see solort_greedy_advance.  embed [vocab,
+    hidden] bf16, x [hidden] bf16, tok/step/pos int64 [1], tokens int64 [max_tokens]."""
+    _on_gpu("embed", embed, torch.bfloat16)
+    _on_gpu("x", x, torch.bfloat16)
+    _need(embed.dim() == 2 and embed.stride(1) == 1 and embed.shape[0] >= vocab, "embed must be [>= vocab, hidden]")
+    hidden = embed.shape[1]
+    _need(x.numel() == hidden and x.is_contiguous(), f"x must hold hidden = {hidden} values")
+    for name, t in (("tok", tok), ("step", step), ("pos", pos)) + ((("tokens", tokens),) if tokens is not None else ()):
+        _need(t.is_cuda and t.dtype == torch.int64 and t.is_contiguous() and t.numel() >= 1,
+              f"{name} must be int64 on the device")
+    lib = _lib.load()
+    _need(ws.is_cuda and ws.numel() * ws.element_size() >= lib.solort_gemv_argmax_workspace_bytes(int(vocab)),
+          "ws must be the gemv_argmax workspace of this vocabulary")
+    rc = lib.solort_greedy_advance(ws.data_ptr(), int(vocab), embed.data_ptr(), embed.stride(0), hidden, x.data_ptr(),
+                                   tok.data_ptr(), None if tokens is None else tokens.data_ptr(),
+                                   0 if tokens is None else tokens.numel(), step.data_ptr(), pos.data_ptr(),
+                                   _stream(x))
+    _lib.check(rc, "greedy_advance")

@@ -121,6 +121,26 @@ def test_prefill_entry_points_reject_bad_arguments(lib):
     assert rc == EINVAL and "null" in _err(lib)
 
 
+def test_gemv_entry_points_reject_bad_arguments(lib):
+    p = ctypes.c_void_p(4096)
+    rc = lib.solort_gemv(p, 2560, 100, 2560, p, None, 1e-6, None, 3, 0, p, None)
+    assert rc == EINVAL and "mode" in _err(lib)
+    rc = lib.solort_gemv(p, 2560, 100, 2564, p, None, 1e-6, None, 0, 0, p, None)
+    assert rc == EINVAL and "shape" in _err(lib)
+    rc = lib.solort_gemv(p, 2560, 100, 2560, p, None, 1e-6, None, 1, 0, p, None)
+    assert rc == EINVAL and "null" in _err(lib)
+    rc = lib.solort_gemv(p, 2560, 100, 2560, p, None, 1e-6, None, 2, 50, p, None)
+    assert rc == EINVAL and "swiglu" in _err(lib)
+    rc = lib.solort_gemv_argmax(p, 2560, 100, 2560, p, None, 1e-6, None, p, None, None)
+    assert rc == EINVAL and "null" in _err(lib)
+    rc = lib.solort_gemv_argmax(p, 2560, 100, 2560, p, None, 1e-6, None, p, ctypes.c_void_p(4096 + 4), None)
+    assert rc == EINVAL and "aligned" in _err(lib)
+    assert lib.solort_gemv_argmax_workspace_bytes(0) == 0
+    assert lib.solort_gemv_argmax_workspace_bytes(151936) >= 151936 // 4 * 8
+    rc = lib.solort_gemv_argmax(p, 2000, 100, 2560, p, None, 1e-6, None, p, p, None)
+    assert rc == EINVAL and "stride" in _err(lib)
+
+
 def test_torch_front_end_refuses_cpu_tensors():
     q = torch.zeros(1, 32, 128, dtype=torch.bfloat16)
     kc = torch.zeros(1024, 8, 128, dtype=torch.bfloat16)

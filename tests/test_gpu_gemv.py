@@ -107,3 +107,73 @@ def test_decode_mlp_block_chain(gpu):
     err = (xd.float().cpu() - want.float()).abs()
     _say(f"  chain vs torch ops: max-abs {err.max().item():.3e} mean-abs {err.mean().item():.3e}")
     assert err.max().item() <= 5e-2 and err.mean().item() <= 2e-3
+
+
+@pytest.mark.parametrize("n,k,norm", [(151936, 2560, True), (151936, 4096, False), (4099, 136, True), (1, 8, False)],
+                         ids=["lm_head_4b", "lm_head_8b", "odd", "one"])
+def test_gemv_argmax_equals_gemv_then_argmax(gpu, n, k, norm):
+    """The fused lm_head + argmax: logits bit-identical to solort_gemv's, index bit-identical to
+    solort_argmax_rows over them and equal to the first maximum of those logits, including exact ties
+    planted by duplicating the winning row at a lower and a higher index, and a NaN row (NaN ranks
+    highest, the first NaN wins).  The workspaces are reused across all calls."""
+    _say(f"[gemv_argmax n={n} k={k} norm={norm}]")
+    w, x, nw = _data(n, k, 70 + n % 89)
+    w, x, nw = w.to(gpu), x.to(gpu), nw.to(gpu) if norm else None
+    ws = ops.argmax_workspace(1, gpu)
+    gws = ops.gemv_argmax_workspace(n, gpu)
+    want_logits = torch.empty(n, dtype=torch.bfloat16, device=gpu)
+    got_logits = torch.empty(n, dtype=torch.bfloat16, device=gpu)
+    idx, idx2, idx_ref = (torch.full((1,), -1, dtype=torch.long, device=gpu) for _ in range(3))
+
+    def check(what):
+        ops.gemv(w, x, want_logits, nw, 1e-6)
+        ops.argmax_rows(want_logits.view(1, n), idx_ref, ws)
+        ops.gemv_argmax(w, x, idx, gws, nw, 1e-6, logits=got_logits)
+        ops.gemv_argmax(w, x, idx2, gws, nw, 1e-6)  # without the logits
+        torch.cuda.synchronize()
+        first = int(torch.argmax(want_logits.float()).item())
+        _say(f"  {what}: index {idx.item()} (argmax_rows {idx_ref.item()}, first max {first})")
+        assert torch.equal(got_logits.view(torch.int16), want_logits.view(torch.int16)), what  # bits (NaN too)
+        assert idx.item() == idx_ref.item() == idx2.item() == first, what
+
+    check("random")
+    if n < 3:
+        return
+    j = int(idx.item())
+    lo, hi = (j // 2, min(n - 1, j + 1 + (n - j) // 2)) if j > 0 else (0, min(n - 1, 1 + n // 2))
+    w[lo].copy_(w[j])
+    w[hi].copy_(w[j])
+    check(f"tie planted at {lo} and {hi}")
+    w[hi, 3] = float("nan")
+    w[min(n - 1, hi + 1), 0] = float("nan")
+    check(f"NaN rows {hi} and {min(n - 1, hi + 1)}")
+
+
+def test_greedy_advance_after_gemv_argmax(gpu):
+    """solort_gemv_argmax with no out_idx leaves the keys; solort_greedy_advance turns them into the
+    next input token (equal to the argmax of the logits), records it at tokens[step] while step is
+    below the list's length, advances step and pos, and copies the token's embedding row into x."""
+    n, k, hidden = 4099, 136, 64
+    w, x, nw = _data(n, k, 91)
+    w, x, nw = w.to(gpu), x.to(gpu), nw.to(gpu)
+    embed = torch.randn(n, hidden, device=gpu).to(torch.bfloat16)
+    gws = ops.gemv_argmax_workspace(n, gpu)
+    logits = torch.empty(n, dtype=torch.bfloat16, device=gpu)
+    xo = torch.zeros(hidden, dtype=torch.bfloat16, device=gpu)
+    tok = torch.full((1,), -1, dtype=torch.long, device=gpu)
+    tokens = torch.full((4,), -1, dtype=torch.long, device=gpu)
+    step = torch.tensor([3], dtype=torch.long, device=gpu)
+    pos = torch.tensor([17], dtype=torch.long, device=gpu)
+    first = None
+    for call in range(2):
+        ops.gemv_argmax(w, x, None, gws, nw, 1e-6, logits=logits)
+        ops.greedy_advance(gws, n, embed, xo, tok, tokens, step, pos)
+        torch.cuda.synchronize()
+        t = int(torch.argmax(logits.float()).item())
+        _say(f"  call {call}: token {tok.item()} (first max {t}), tokens {tokens.tolist()}, step {step.item()}, "
+             f"pos {pos.item()}")
+        assert tok.item() == t and torch.equal(xo, embed[t])
+        assert step.item() == 4 + call and pos.item() == 18 + call
+        first = t if first is None else first
+        assert tokens.tolist() == [-1, -1, -1, first]  # the second call's step 4 is past the list
+        x = (x.float() * -1.5).to(torch.bfloat16)  # another argmax for the second call

@@ -45,9 +45,7 @@ def test_decode_graph_replays_equal_eager_steps(gpu):
     _, m = _model(gpu, p0, TINY_UNTIED)
     _, e = _model(gpu, p0, TINY_UNTIED)
     toks = m.generate(7, p0, n)
-    e.tok.fill_(7)
-    e.pos.fill_(p0)
-    e.step.zero_()
+    e.start(7, p0)
     for i in range(n):
         e._step(e.bucket_for(p0 + i))
     torch.cuda.synchronize()
@@ -55,6 +53,12 @@ def test_decode_graph_replays_equal_eager_steps(gpu):
     assert torch.equal(m.kc, e.kc) and torch.equal(m.vc, e.vc)
     assert sorted(m._graphs) == [128, 256]
     assert len(set(toks)) > 1
+    # the separate-ops tail (lm_head, argmax, token copy, counter adds, embedding gather) agrees
+    w, u = _model(gpu, p0, TINY_UNTIED)
+    u2 = GraphQwen3Decode(w, 256, fused_tail=False)
+    u2.kc.copy_(u.kc)
+    u2.vc.copy_(u.vc)
+    assert u2.generate(7, p0, n) == toks and torch.equal(u2.kc, m.kc)
     _say(f"  tokens {toks}")
 
 
@@ -73,9 +77,7 @@ def test_decode_steps_match_reference_ops(gpu, shape):
     kc, vc = m.kc.cpu(), m.vc.cpu()
     kc32, vc32 = kc.float(), vc.float()
     tok = 7
-    m.tok.fill_(tok)
-    m.pos.fill_(p0)
-    m.step.zero_()
+    m.start(tok, p0)
     for i in range(n):
         pos = p0 + i
         bound = m.bucket_for(pos)
@@ -92,6 +94,8 @@ def test_decode_steps_match_reference_ops(gpu, shape):
         assert dg.mean().item() <= 0.05 * exact.std().item()
         nxt = int(m.tok.item())
         assert nxt == int(torch.argmax(got).item())  # the device argmax of its own logits
+        assert m.tokens[i].item() == nxt and m.step.item() == i + 1 and m.pos.item() == pos + 1
+        assert torch.equal(m.x.view(-1), w.embed[nxt])  # the next step's input row
         top2 = torch.topk(exact, 2).values
         if (top2[0] - top2[1]).item() > 2 * dg.max().item():
             assert nxt == int(torch.argmax(exact).item()), i
