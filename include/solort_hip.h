@@ -180,6 +180,36 @@ int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int nq, int nh,
                         int n_split, void* out, int out_dtype, solort_stream_t stream);
 
 /*
+ * solort_decode_layer over a paged KV cache: the layout of the reference's
+ * tensor-backed PagedKVCache (src/solort/cache/kv_cache.py:71-100: per layer
+ * [num_pages, 2, page_size, nkv, hd], K then V within a page, "NHD"), read
+ * and written through a page table as FlashInfer-style paged decode would
+ * (page_indices, :113-129).  Position t of the sequence is row
+ * t % page_size of page page_table[t / page_size], i.e. physical slot
+ * page_table[t / page_size] * page_size + t % page_size, the reference's
+ * slot_mapping (:131-145); the new tokens' K/V rows go to the slots of
+ * pos0..pos0+nq-1 (its store_layer_tokens, :191-230).
+ * k_pages, v_pages  page 0 of K and of V (for the reference layout, v_pages =
+ *                   k_pages + page_size * nkv * hd); page_stride elements
+ *                   from one page to the next (2 * page_size * nkv * hd).
+ * kv_tok_stride, kv_head_stride  strides of a row and of a head within a page.
+ * page_size         a power of two; num_pages pages in the pool.
+ * page_table        int32 [table_len]; entries 0..ceil(bound/page_size)-1 are
+ *                   read (entries past the live pages are read and their rows
+ *                   masked); an entry outside [0, num_pages) is clamped into
+ *                   the pool (a wrong row, never an out-of-bounds access).
+ * Positions >= table_len * page_size are not written.  Results equal
+ * solort_decode_layer over the same rows in a contiguous cache, bit for bit,
+ * for the same bound and n_split.  Other arguments as in solort_decode_layer.
+ */
+int solort_paged_decode_layer(const void* qkv, int64_t qkv_row_stride, int nq, int nh, int nkv, int hd,
+                              const void* qn_w, const void* kn_w, float eps, const void* rope_cs,
+                              const int64_t* pos0_dev, void* k_pages, void* v_pages, int64_t page_stride,
+                              int64_t kv_tok_stride, int64_t kv_head_stride, int page_size, int num_pages,
+                              const int32_t* page_table, int table_len, int bound, float scale, void* ws,
+                              int n_split, void* out, int out_dtype, solort_stream_t stream);
+
+/*
  * Causal grouped-query prefill attention on bf16 MFMA.
  * Replaces cuda_graph_executor.py:124-130: SDPA(q, repeat_interleave(k, g),
  * repeat_interleave(v, g), is_causal=True, scale) over T prompt rows at

@@ -176,3 +176,58 @@ def decode_model_step(w: dict, tok: int, pos: int, kc: torch.Tensor, vc: torch.T
         ctx = decode_attn(q, kc[li], vc[li], pos, bound, hd ** -0.5)
         x = decode_mlp_block(x, ctx.view(1, -1), w["wo"][li], w["post_ln"][li], w["wgu"][li], w["wd"][li], eps)
     return linear(rmsnorm(x, w["final_norm"], eps), w["lm_head"]).view(-1)
+
+
+# ---------------------------------------------------------------- paged KV cache (src/solort/cache/kv_cache.py)
+
+
+def pages_required(token_count: int, page_size: int) -> int:
+    """kv_cache.py:100-103."""
+    return 0 if token_count <= 0 else (token_count + page_size - 1) // page_size
+
+
+def last_page_len(token_count: int, page_size: int) -> int:
+    """kv_cache.py:147-151."""
+    if token_count <= 0:
+        return 0
+    rem = token_count % page_size
+    return rem if rem else page_size
+
+
+def slot_mapping(block_table: list[int], positions: list[int], page_size: int) -> list[int]:
+    """kv_cache.py:131-145: logical position -> physical slot page * page_size + offset; a position
+    whose logical page is past the block table raises IndexError."""
+    slots = []
+    for p in positions:
+        lp = p // page_size
+        if lp >= len(block_table):
+            raise IndexError(f"position {p} needs logical page {lp}, but block table has {len(block_table)} pages")
+        slots.append(block_table[lp] * page_size + p % page_size)
+    return slots
+
+
+def metadata_for(block_table: list[int], token_count: int, positions: list[int], page_size: int) -> dict:
+    """kv_cache.py:113-129: the page-table view of one sequence."""
+    n = pages_required(token_count, page_size)
+    return {"page_indptr": [0, len(block_table[:n])], "page_indices": list(block_table[:n]),
+            "last_page_len": [last_page_len(token_count, page_size)],
+            "slot_mapping": slot_mapping(block_table, positions, page_size)}
+
+
+def paged_store(kv_layer: torch.Tensor, slots: list[int], k: torch.Tensor, v: torch.Tensor) -> None:
+    """store_layer_tokens, kv_cache.py:191-230, for one layer's arena kv_layer [pages, 2, page, nkv, hd]
+    and rows k, v [tokens, nkv, hd] (the reference takes HF [1, nkv, tokens, hd] and transposes)."""
+    ps = kv_layer.shape[2]
+    for i, slot in enumerate(slots):
+        kv_layer[slot // ps, 0, slot % ps].copy_(k[i])
+        kv_layer[slot // ps, 1, slot % ps].copy_(v[i])
+
+
+def paged_gather(kv_layer: torch.Tensor, slots: list[int]) -> tuple[torch.Tensor, torch.Tensor]:
+    """gather_layer_tokens, kv_cache.py:232-256: rows [tokens, nkv, hd] of the given physical slots
+    (slot = page * page_size + offset indexes the flattened [pages, page] grid)."""
+    pages, _, ps, nkv, hd = kv_layer.shape
+    idx = torch.as_tensor(slots, dtype=torch.long)
+    flat_k = kv_layer[:, 0].reshape(pages * ps, nkv, hd)
+    flat_v = kv_layer[:, 1].reshape(pages * ps, nkv, hd)
+    return flat_k.index_select(0, idx).clone(), flat_v.index_select(0, idx).clone()

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before ours)
 
 LIB_PATH = Path(__file__).resolve().parent / "libsolort_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 # name -> (restype, argtypes); mirrors include/solort_hip.h
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -53,6 +53,12 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "solort_prefill_attn": (
         c_int,
         [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_float,
+         c_void_p, c_int, c_void_p],
+    ),
+    "solort_paged_decode_layer": (
+        c_int,
+        [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_int64, c_int64, c_int64, c_int, c_int, c_void_p, c_int, c_int, c_float, c_void_p, c_int,
          c_void_p, c_int, c_void_p],
     ),
     "solort_prefill_layer": (

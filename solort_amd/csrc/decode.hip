@@ -65,7 +65,26 @@ struct DecodeTail {
   float eps;
   int pos_limit;  // positions >= pos_limit are not written
   int out_f32;
+  // Paged cache (PAGED kernels): position t lives in page page_table[t >> page_shift], row
+  // t & (2^page_shift - 1); a page is page_stride elements from the next.
+  const int32_t* page_table;
+  int64_t page_stride;
+  int page_shift;
+  int num_pages;
 };
+
+// Element offset of the cache row at position t (head 0, dim 0).  Paged: a
+// table entry outside [0, num_pages) is clamped into the pool, so a bad
+// entry reads a wrong row but never leaves the allocation.
+template <bool PAGED>
+__device__ __forceinline__ int64_t row_off(int64_t t, int tok_stride, const DecodeTail& a) {
+  if constexpr (PAGED) {
+    const int p = min(max(a.page_table[t >> a.page_shift], 0), a.num_pages - 1);
+    return (int64_t)p * a.page_stride + (t & ((1 << a.page_shift) - 1)) * tok_stride;
+  } else {
+    return t * tok_stride;
+  }
+}
 
 __device__ __forceinline__ float4 f4fma(float w, const float4 v, float4 acc) {
   acc.x = fmaf(w, v.x, acc.x);
@@ -105,7 +124,7 @@ __device__ __forceinline__ void store_out2(void* out, int out_f32, int nh, int k
 // few key rows per slot).  Grid (nkv, n_split): block (kvh, split).  qsrc:
 // fused, the qkv rows (row stride qsrc_stride); unfused, the q rows
 // [nq][nh][128] (qsrc_stride = nh*128).
-template <int NQ, int G, int U, bool FUSED>
+template <int NQ, int G, int U, bool FUSED, bool PAGED>
 __global__ __launch_bounds__(256) void decode_lanes_kernel(uint16_t* kc, uint16_t* vc, int tok_stride, int head_stride,
                                                      int chunk, int bound, const uint16_t* qsrc, int qsrc_stride,
                                                      int nh, const uint16_t* qn_w, const DecodeTail a) {
@@ -157,8 +176,9 @@ __global__ __launch_bounds__(256) void decode_lanes_kernel(uint16_t* kc, uint16_
 #pragma unroll
   for (int u = 0; u < U; ++u) {
     const int kid = min(kbeg + u * 16 + slot, kclamp);
-    kr[u] = *reinterpret_cast<const uint4*>(kp + (int64_t)kid * tok_stride);
-    vr[u] = *reinterpret_cast<const uint4*>(vp + (int64_t)kid * tok_stride);
+    const int64_t off = row_off<PAGED>(kid, tok_stride, a);
+    kr[u] = *reinterpret_cast<const uint4*>(kp + off);
+    vr[u] = *reinterpret_cast<const uint4*>(vp + off);
   }
 
   const int64_t pos0 = a.pos0_dev[0];
@@ -180,7 +200,7 @@ __global__ __launch_bounds__(256) void decode_lanes_kernel(uint16_t* kc, uint16_
       if (c == G + 1) {  // V row: raw
         s_new[(NQ + t) * 16 + j] = raw;
         if (split == 0 && pos_ok)
-          *reinterpret_cast<uint4*>(vc + pos * tok_stride + (int64_t)kvh * head_stride + j * 8) = raw;
+          *reinterpret_cast<uint4*>(vc + row_off<PAGED>(pos, tok_stride, a) + (int64_t)kvh * head_stride + j * 8) = raw;
         continue;
       }
       float cs[8], sn[8];
@@ -192,7 +212,7 @@ __global__ __launch_bounds__(256) void decode_lanes_kernel(uint16_t* kc, uint16_
       } else {
         s_new[t * 16 + j] = ov;
         if (split == 0 && pos_ok)
-          *reinterpret_cast<uint4*>(kc + pos * tok_stride + (int64_t)kvh * head_stride + j * 8) = ov;
+          *reinterpret_cast<uint4*>(kc + row_off<PAGED>(pos, tok_stride, a) + (int64_t)kvh * head_stride + j * 8) = ov;
       }
     } else {
       const int t = row / G, g = row % G;
@@ -230,8 +250,9 @@ __global__ __launch_bounds__(256) void decode_lanes_kernel(uint16_t* kc, uint16_
 #pragma unroll
       for (int u = 0; u < U; ++u) {
         const int kid = min(k1 + u * 16 + slot, kend - 1);
-        kn[u] = *reinterpret_cast<const uint4*>(kp + (int64_t)kid * tok_stride);
-        vn[u] = *reinterpret_cast<const uint4*>(vp + (int64_t)kid * tok_stride);
+        const int64_t off = row_off<PAGED>(kid, tok_stride, a);
+        kn[u] = *reinterpret_cast<const uint4*>(kp + off);
+        vn[u] = *reinterpret_cast<const uint4*>(vp + off);
       }
     }
     float part[U * R];  // this lane's share of each score, index u * R + r
@@ -372,14 +393,19 @@ struct KVTile {
 
 // Loads of the tile at key k0 (k0 past the split: its first rows again, which
 // are cached).  Rows are clamped to kclamp, a row the split may read.
+template <bool PAGED>
 __device__ __forceinline__ KVTile fetch_tile(const uint16_t* kp, const uint16_t* vp, int tok_stride, int k0, int kbeg,
-                                             int kstat, int kclamp, int lrow) {
+                                             int kstat, int kclamp, int lrow, const DecodeTail& a) {
   const int base = k0 < kstat ? k0 : kbeg;
   const bool whole = base + kTile - 1 <= kclamp;  // wave-uniform: no row needs clamping
   const int64_t off0 = (int64_t)(base + lrow) * tok_stride, step = (int64_t)4 * tok_stride;
   KVTile t;
   auto ld = [&](int i, uint4& kd, uint4& vd) {
-    const int64_t off = whole ? off0 + i * step : (int64_t)min(base + lrow + 4 * i, kclamp) * tok_stride;
+    int64_t off;
+    if constexpr (PAGED)
+      off = row_off<true>(min(base + lrow + 4 * i, kclamp), tok_stride, a);
+    else
+      off = whole ? off0 + i * step : (int64_t)min(base + lrow + 4 * i, kclamp) * tok_stride;
     kd = *reinterpret_cast<const uint4*>(kp + off);
     vd = *reinterpret_cast<const uint4*>(vp + off);
   };
@@ -391,7 +417,7 @@ __device__ __forceinline__ KVTile fetch_tile(const uint16_t* kp, const uint16_t*
 // Grid (nkv, n_split): block (kvh, split), 4 wavefronts.  qsrc: fused, the
 // qkv rows (row stride qsrc_stride); unfused, the q rows [nq][nh][128]
 // (qsrc_stride = nh*128).
-template <int NQ, int G, bool FUSED>
+template <int NQ, int G, bool FUSED, bool PAGED>
 __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint16_t* vc, int tok_stride, int head_stride,
                                                         int chunk, int bound, const uint16_t* qsrc, int qsrc_stride,
                                                         int nh, const uint16_t* qn_w, const DecodeTail a) {
@@ -453,7 +479,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint1
   const uint16_t* kp = kc + (int64_t)kvh * head_stride + 8 * j;
   const uint16_t* vp = vc + (int64_t)kvh * head_stride + 8 * j;
   const int lrow = lane >> 4;  // this lane's first row of the tile; rows lrow + 4i
-  KVTile kv = fetch_tile(kp, vp, tok_stride, kbeg + kTile * wave, kbeg, kstat, kclamp, lrow);
+  KVTile kv = fetch_tile<PAGED>(kp, vp, tok_stride, kbeg + kTile * wave, kbeg, kstat, kclamp, lrow, a);
 
   const int64_t pos0 = a.pos0_dev[0];
 
@@ -470,7 +496,8 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint1
       if (c == G + 1) {  // V row: raw
         *reinterpret_cast<uint4*>(&s_new[(NQ + t) * 128 + j * 8]) = raw[ps];
         if (split == 0 && pos_ok)
-          *reinterpret_cast<uint4*>(vc + pos * tok_stride + (int64_t)kvh * head_stride + j * 8) = raw[ps];
+          *reinterpret_cast<uint4*>(vc + row_off<PAGED>(pos, tok_stride, a) + (int64_t)kvh * head_stride + j * 8) =
+              raw[ps];
         continue;
       }
       float cs[8], sn[8];
@@ -482,7 +509,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint1
       } else {
         *reinterpret_cast<uint4*>(&s_new[t * 128 + j * 8]) = ov;
         if (split == 0 && pos_ok)
-          *reinterpret_cast<uint4*>(kc + pos * tok_stride + (int64_t)kvh * head_stride + j * 8) = ov;
+          *reinterpret_cast<uint4*>(kc + row_off<PAGED>(pos, tok_stride, a) + (int64_t)kvh * head_stride + j * 8) = ov;
       }
     } else {
       *reinterpret_cast<uint4*>(&s_q[row * kQStride + j * 8]) = raw[ps];
@@ -536,7 +563,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint1
     stage_row(0, kv.k0, kv.v0); stage_row(1, kv.k1, kv.v1); stage_row(2, kv.k2, kv.v2); stage_row(3, kv.k3, kv.v3);
     stage_row(4, kv.k4, kv.v4); stage_row(5, kv.k5, kv.v5); stage_row(6, kv.k6, kv.v6); stage_row(7, kv.k7, kv.v7);
     // next tile (past the end: a re-read of cached rows)
-    kv = fetch_tile(kp, vp, tok_stride, k0 + 4 * kTile, kbeg, kstat, kclamp, lrow);
+    kv = fetch_tile<PAGED>(kp, vp, tok_stride, k0 + 4 * kTile, kbeg, kstat, kclamp, lrow, a);
     f32x16 s = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
@@ -785,6 +812,7 @@ struct DecodeArgs {
   int qsrc_stride, nh, nkv, n_split;
   const uint16_t* qn_w;
   bool lanes;  // the lane-parallel kernel (short chunks, one new token), else the MFMA kernel
+  bool paged;  // K/V rows through the page table in tail
   int U;       // key rows per slot per step of the lane-parallel kernel
   DecodeTail tail;
 };
@@ -804,27 +832,38 @@ static WsLayout ws_layout(int nq, int nh, int nkv, int n_split) {
   return w;
 }
 
-template <int NQ, int G, bool FUSED>
-static bool launch_split(const DecodeArgs& a, hipStream_t s) {
+template <int NQ, int G, bool FUSED, bool PAGED>
+static bool launch_split_p(const DecodeArgs& a, hipStream_t s) {
   if constexpr (NQ * G <= kMaxRows) {
     const dim3 grid(a.nkv, a.n_split);
     if constexpr (NQ == 1 && G <= kLanesMaxGroup) {
       if (a.lanes) {
         if (a.U == 4)
-          hipLaunchKernelGGL((decode_lanes_kernel<NQ, G, 4, FUSED>), grid, dim3(256), 0, s, a.kc, a.vc, a.tok_stride,
-                             a.head_stride, a.chunk, a.bound, a.qsrc, a.qsrc_stride, a.nh, a.qn_w, a.tail);
+          hipLaunchKernelGGL((decode_lanes_kernel<NQ, G, 4, FUSED, PAGED>), grid, dim3(256), 0, s, a.kc, a.vc,
+                             a.tok_stride, a.head_stride, a.chunk, a.bound, a.qsrc, a.qsrc_stride, a.nh, a.qn_w,
+                             a.tail);
         else
-          hipLaunchKernelGGL((decode_lanes_kernel<NQ, G, 2, FUSED>), grid, dim3(256), 0, s, a.kc, a.vc, a.tok_stride,
-                             a.head_stride, a.chunk, a.bound, a.qsrc, a.qsrc_stride, a.nh, a.qn_w, a.tail);
+          hipLaunchKernelGGL((decode_lanes_kernel<NQ, G, 2, FUSED, PAGED>), grid, dim3(256), 0, s, a.kc, a.vc,
+                             a.tok_stride, a.head_stride, a.chunk, a.bound, a.qsrc, a.qsrc_stride, a.nh, a.qn_w,
+                             a.tail);
         return true;
       }
     }
-    hipLaunchKernelGGL((decode_mfma_kernel<NQ, G, FUSED>), grid, dim3(256), 0, s, a.kc, a.vc, a.tok_stride,
+    hipLaunchKernelGGL((decode_mfma_kernel<NQ, G, FUSED, PAGED>), grid, dim3(256), 0, s, a.kc, a.vc, a.tok_stride,
                        a.head_stride, a.chunk, a.bound, a.qsrc, a.qsrc_stride, a.nh, a.qn_w, a.tail);
     return true;
   } else {
     return false;
   }
+}
+
+// The paged cache is served by the fused layer entry point only.
+template <int NQ, int G, bool FUSED>
+static bool launch_split(const DecodeArgs& a, hipStream_t s) {
+  if constexpr (FUSED) {
+    if (a.paged) return launch_split_p<NQ, G, true, true>(a, s);
+  }
+  return launch_split_p<NQ, G, FUSED, false>(a, s);
 }
 
 template <int NQ, int G>
@@ -1020,5 +1059,50 @@ extern "C" int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int 
   a.tail.kn_w = (const uint16_t*)kn_w;
   a.tail.rope_cs = (const uint16_t*)rope_cs;
   a.tail.eps = eps;
+  return launch_all(name, true, nq, a, (hipStream_t)stream);
+}
+
+extern "C" int solort_paged_decode_layer(const void* qkv, int64_t qkv_row_stride, int nq, int nh, int nkv, int hd,
+                                         const void* qn_w, const void* kn_w, float eps, const void* rope_cs,
+                                         const int64_t* pos0_dev, void* k_pages, void* v_pages, int64_t page_stride,
+                                         int64_t kv_tok_stride, int64_t kv_head_stride, int page_size,
+                                         int num_pages, const int32_t* page_table, int table_len, int bound,
+                                         float scale, void* ws, int n_split, void* out, int out_dtype,
+                                         solort_stream_t stream) {
+  const char* name = "paged_decode_layer";
+  if (page_size < 1 || page_size > (1 << 20) || (page_size & (page_size - 1)))
+    return set_error(SOLORT_EINVAL, "%s: page_size %d must be a power of two up to 2^20", name, page_size);
+  if (num_pages < 1 || table_len < 1 || (int64_t)table_len * page_size > kMaxI32)
+    return set_error(SOLORT_EINVAL, "%s: num_pages=%d table_len=%d page_size=%d", name, num_pages, table_len,
+                     page_size);
+  if (!page_table || ((uintptr_t)page_table & 3u))
+    return set_error(SOLORT_EINVAL, "%s: page_table must be a 4-byte aligned pointer", name);
+  if (page_stride < (int64_t)page_size * kv_tok_stride || page_stride % 8 != 0 ||
+      (int64_t)(num_pages - 1) * page_stride > ((int64_t)1 << 40))
+    return set_error(SOLORT_EINVAL, "%s: page_stride %lld must hold page_size rows and be a multiple of 8", name,
+                     (long long)page_stride);
+  if (kv_tok_stride < (int64_t)nkv * kv_head_stride && kv_head_stride < (int64_t)page_size * kv_tok_stride)
+    return set_error(SOLORT_EINVAL, "%s: token and head strides overlap", name);
+  DecodeArgs a = {};
+  // The logical capacity, table_len pages, plays the part of max_len.
+  int rc = prepare(name, nq, nh, nkv, hd, k_pages, v_pages, kv_tok_stride, kv_head_stride,
+                   (int64_t)table_len * page_size, pos0_dev, bound, scale, ws, n_split, out, out_dtype, a);
+  if (rc) return rc;
+  if (!qkv || !qn_w || !kn_w || !rope_cs) return set_error(SOLORT_EINVAL, "%s: null pointer", name);
+  if (!aligned16(qkv) || !aligned16(qn_w) || !aligned16(kn_w) || !aligned16(rope_cs))
+    return set_error(SOLORT_EINVAL, "%s: pointers must be 16-byte aligned", name);
+  if (qkv_row_stride < (int64_t)(nh + 2 * nkv) * hd || qkv_row_stride % 8 != 0 || qkv_row_stride > kMaxI32)
+    return set_error(SOLORT_EINVAL, "%s: qkv_row_stride %lld", name, (long long)qkv_row_stride);
+  a.qsrc = (const uint16_t*)qkv;
+  a.qsrc_stride = (int)qkv_row_stride;
+  a.qn_w = (const uint16_t*)qn_w;
+  a.tail.kn_w = (const uint16_t*)kn_w;
+  a.tail.rope_cs = (const uint16_t*)rope_cs;
+  a.tail.eps = eps;
+  a.paged = true;
+  a.tail.page_table = page_table;
+  a.tail.page_stride = page_stride;
+  a.tail.page_shift = __builtin_ctz((unsigned)page_size);
+  a.tail.num_pages = num_pages;
   return launch_all(name, true, nq, a, (hipStream_t)stream);
 }

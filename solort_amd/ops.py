@@ -250,6 +250,45 @@ def decode_layer(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps:
     _lib.check(rc, "decode_layer")
 
 
+def paged_decode_layer(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps: float, rope_cs: torch.Tensor,
+                       pos0: torch.Tensor, kv_pages: torch.Tensor, page_table: torch.Tensor, bound: int,
+                       scale: float, ws: torch.Tensor, n_split: int, out: torch.Tensor, nh: int, nkv: int) -> None:
+    """decode_layer over one layer of a paged KV cache kv_pages [num_pages, 2, page_size, nkv, 128] bf16
+    (the reference PagedKVCache's per-layer arena, kv_cache.py:71-100), through page_table int32
+    [>= ceil(bound / page_size)] (logical page -> physical page); see solort_paged_decode_layer."""
+    _on_gpu("qkv", qkv, torch.bfloat16)
+    _need(qkv.dim() == 2 and qkv.shape[1] == (nh + 2 * nkv) * HD and qkv.stride(1) == 1,
+          f"qkv must be [nq, {(nh + 2 * nkv) * HD}] with unit column stride")
+    nq = qkv.shape[0]
+    for name, w in (("qn_w", qn_w), ("kn_w", kn_w)):
+        _on_gpu(name, w, torch.bfloat16)
+        _need(w.shape == (HD,) and w.is_contiguous(), f"{name} must be [{HD}] contiguous")
+    _rope_rows_ok(rope_cs, nq)
+    _on_gpu("kv_pages", kv_pages, torch.bfloat16)
+    _need(kv_pages.dim() == 5 and kv_pages.shape[1] == 2 and kv_pages.shape[3] == nkv and kv_pages.shape[4] == HD
+          and kv_pages.stride(4) == 1, f"kv_pages must be [num_pages, 2, page_size, {nkv}, {HD}]")
+    num_pages, _, page_size = kv_pages.shape[:3]
+    _need(page_table.is_cuda and page_table.dtype == torch.int32 and page_table.dim() == 1
+          and page_table.is_contiguous(), "page_table must be a contiguous int32 vector on the device")
+    _need(page_table.numel() * page_size >= bound, f"page_table covers {page_table.numel() * page_size} < bound {bound}")
+    _need(pos0.is_cuda and pos0.dtype == torch.int64 and pos0.numel() >= 1, "pos0 must be int64 on the device")
+    _need(out.is_cuda and out.dtype in (torch.bfloat16, torch.float32), "out must be bf16 or fp32 on the device")
+    _need(out.shape == (nq, nh * HD) and out.is_contiguous() and out.data_ptr() % 16 == 0,
+          f"out must be [{nq}, {nh * HD}] contiguous and 16-byte aligned")
+    lib = _lib.load()
+    need = lib.solort_attn_workspace_bytes(nq, nh, nkv, HD, n_split)
+    _need(ws.is_cuda and ws.numel() * ws.element_size() >= need and ws.data_ptr() % 16 == 0,
+          f"workspace too small: need {need} bytes")
+    dt = DTYPE_F32 if out.dtype == torch.float32 else DTYPE_BF16
+    k_pages, v_pages = kv_pages[:, 0], kv_pages[:, 1]
+    rc = lib.solort_paged_decode_layer(
+        qkv.data_ptr(), qkv.stride(0), nq, nh, nkv, HD, qn_w.data_ptr(), kn_w.data_ptr(), float(eps),
+        rope_cs.data_ptr(), pos0.data_ptr(), k_pages.data_ptr(), v_pages.data_ptr(), kv_pages.stride(0),
+        kv_pages.stride(2), kv_pages.stride(3), int(page_size), int(num_pages), page_table.data_ptr(),
+        page_table.numel(), int(bound), float(scale), ws.data_ptr(), int(n_split), out.data_ptr(), dt, _stream(qkv))
+    _lib.check(rc, "paged_decode_layer")
+
+
 def prefill_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, scale: float,
                  out: torch.Tensor) -> None:
     """Causal GQA attention of T prompt rows (q [T, nh, 128]) over cache rows 0..T-1 into

@@ -141,6 +141,18 @@ def test_gemv_entry_points_reject_bad_arguments(lib):
     assert rc == EINVAL and "stride" in _err(lib)
 
 
+def test_paged_decode_rejects_bad_arguments(lib):
+    p = ctypes.c_void_p(4096)
+    args = lambda ps=16, pages=64, table=p, tlen=64, stride=2 * 16 * 1024: (  # noqa: E731
+        p, 6144, 1, 32, 8, 128, p, p, 1e-6, p, p, p, p, stride, 1024, 128, ps, pages, table, tlen, 1024, 0.088, p,
+        32, p, 0, None)
+    assert lib.solort_paged_decode_layer(*args(ps=12)) == EINVAL and "power of two" in _err(lib)
+    assert lib.solort_paged_decode_layer(*args(table=None)) == EINVAL and "page_table" in _err(lib)
+    assert lib.solort_paged_decode_layer(*args(stride=1000)) == EINVAL and "page_stride" in _err(lib)
+    assert lib.solort_paged_decode_layer(*args(tlen=32)) == EINVAL and "bound" in _err(lib)  # 512 rows < 1024
+    assert lib.solort_paged_decode_layer(*args(pages=0)) == EINVAL
+
+
 def test_torch_front_end_refuses_cpu_tensors():
     q = torch.zeros(1, 32, 128, dtype=torch.bfloat16)
     kc = torch.zeros(1024, 8, 128, dtype=torch.bfloat16)

@@ -362,3 +362,47 @@ def test_rmsnorm_linear_and_mlp_block_restatements():
     act = gu[:, :I] / (1 + np.exp(-gu[:, :I])) * gu[:, I:]
     want = x1 + act @ wdn.double().numpy().T
     assert np.abs(out - want).max() < 0.05 and np.abs(out - want).mean() < 5e-3
+
+
+# ---------------------------------------------------------------- paged KV cache restatement
+
+
+def test_paged_metadata_matches_reference_test_vectors():
+    """tests/test_kv_cache.py:8-18 (page_size 4, a 6-token sequence on pages [0, 1]) and :52-56."""
+    md = ref.metadata_for([0, 1], token_count=6, positions=[0, 3, 4, 5], page_size=4)
+    assert md == {"page_indptr": [0, 2], "page_indices": [0, 1], "last_page_len": [2], "slot_mapping": [0, 3, 4, 5]}
+    with pytest.raises(IndexError):
+        ref.slot_mapping([0], [4], 4)
+    assert [ref.pages_required(n, 4) for n in (0, 1, 4, 5, 8, 9)] == [0, 1, 1, 2, 2, 3]
+    assert [ref.last_page_len(n, 4) for n in (0, 1, 4, 6, 8)] == [0, 1, 4, 2, 4]
+
+
+def test_paged_slot_mapping_of_a_permuted_table():
+    table = [5, 2, 7]
+    assert ref.slot_mapping(table, list(range(12)), 4) == [20, 21, 22, 23, 8, 9, 10, 11, 28, 29, 30, 31]
+    rng = np.random.default_rng(3)
+    for ps in (1, 2, 16):
+        table = list(rng.permutation(40)[:9])
+        pos = list(range(9 * ps))
+        slots = ref.slot_mapping(table, pos, ps)
+        assert len(set(slots)) == len(slots)  # distinct positions never share a slot
+        assert all(s // ps == table[p // ps] and s % ps == p % ps for s, p in zip(slots, pos))
+
+
+def test_paged_store_and_gather_match_reference_test_vectors():
+    """tests/test_kv_cache.py:59-84 and :87-114: two layers, two pages of 4 rows, 2 heads of dim 4,
+    fp32; key = arange(24).reshape(1, 2, 3, 4) stored at slots [0, 1, 5] of layer 1."""
+    kv = torch.zeros(2, 2, 2, 4, 2, 4)
+    key = torch.arange(1 * 2 * 3 * 4, dtype=torch.float32).reshape(1, 2, 3, 4)
+    value = key + 100
+    slots = [0, 1, 5]
+    ref.paged_store(kv[1], slots, key[0].transpose(0, 1), value[0].transpose(0, 1))
+    ref.paged_store(kv[0], slots, (key + 200)[0].transpose(0, 1), (value + 200)[0].transpose(0, 1))
+    k_cache, v_cache = kv[:, :, 0], kv[:, :, 1]
+    assert torch.equal(k_cache[1, 0, 0], key[0, :, 0, :])
+    assert torch.equal(k_cache[1, 0, 1], key[0, :, 1, :])
+    assert torch.equal(v_cache[1, 1, 1], value[0, :, 2, :])
+    k_out, v_out = ref.paged_gather(kv[1], slots)
+    assert torch.equal(k_out, key[0].transpose(0, 1)) and torch.equal(v_out, value[0].transpose(0, 1))
+    k0, _ = ref.paged_gather(kv[0], slots)
+    assert torch.equal(k0, (key + 200)[0].transpose(0, 1)) and not torch.equal(k0, k_out)
