@@ -54,11 +54,12 @@ def parse() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-sweep", action="store_true", help="skip the per-bucket decode extras")
-    p.add_argument("--only", choices=("all", "decode", "prefill", "long", "verify", "gemv", "model"), default="all",
+    p.add_argument("--only", choices=("all", "decode", "prefill", "long", "verify", "gemv", "model", "paged"),
+                   default="all",
                    help="decode: the decode step and its kernel only; prefill: the prefill kernels only; "
                         "long: the Qwen3-8B KV 32768 decode only; verify: the speculative verify and argmax "
-                        "only; gemv: the decode-step GEMVs only; model: whole-model greedy decode only (for "
-                        "per-workload profiles)")
+                        "only; gemv: the decode-step GEMVs only; model: whole-model greedy decode only; paged: the "
+                        "paged-KV decode only (for per-workload profiles)")
     return p.parse_args()
 
 
@@ -111,6 +112,9 @@ def main() -> int:
         return 0
     if args.only == "gemv":
         print(json.dumps({"decode_gemv": gemv_extras(torch, ops, dev)}), flush=True)
+        return 0
+    if args.only == "paged":
+        print(json.dumps({"paged_decode_kv1024": paged_extras(torch, ops, runners, dev, sh)}), flush=True)
         return 0
     if args.only == "model":
         del runners
@@ -172,6 +176,7 @@ def main() -> int:
         result["extras"].update(verify_extras(torch, ops, wl, runners, dev, sh))
         result["extras"]["decode_8b_kv32768"] = long_decode_extras(torch, ops, wl, dev)
         result["extras"]["decode_gemv"] = gemv_extras(torch, ops, dev)
+        result["extras"]["paged_decode_kv1024"] = paged_extras(torch, ops, runners, dev, sh)
         result["extras"]["decode_model"] = model_extras(torch, dev)
     if args.only == "all":
         result["prefill"] = prefill_extras(torch, ops, runners, dev, sh)
@@ -310,6 +315,45 @@ def gemv_extras(torch, ops, dev, copies: int = 4) -> dict:
     out["layer_gemv_us"] = round(layer, 3)
     out["layer_torch_linear_us"] = round(sum(out[n]["torch_linear_us"] for n in ("qkv", "o_proj", "gate_up", "down")), 3)
     return out
+
+
+def paged_extras(torch, ops, runners, dev, sh, page_size: int = 16, bound: int = 1024) -> dict:
+    """Paged-KV decode at KV 1024: each runner layer's cache rows copied into a paged arena
+    [pages, 2, page_size, 8, 128] (the reference PagedKVCache layout) at a random block table (64 live
+    pages + 8 spare per layer, 1.36 GB in all), one solort_paged_decode_layer call per layer of every
+    set in one graph, HIP events around replays; next to the contiguous call of the same graph shape."""
+    from solort_amd.runner import decode_splits
+    ns = decode_splits(bound, sh.nkv)
+    n_log = bound // page_size
+    gen = torch.Generator().manual_seed(1013)
+    arenas = []
+    for r in runners:
+        per = []
+        for li in range(sh.layers):
+            table = torch.randperm(n_log + 8, generator=gen)[:n_log].to(torch.int32)
+            slots = torch.arange(bound)
+            pg = table.long()[slots // page_size]
+            kv = torch.empty(n_log + 8, 2, page_size, sh.nkv, 128, dtype=torch.bfloat16, device=dev)
+            kv[pg.to(dev), 0, (slots % page_size).to(dev)] = r.kc[li, :bound]
+            kv[pg.to(dev), 1, (slots % page_size).to(dev)] = r.vc[li, :bound]
+            per.append((kv, table.to(dev)))
+        arenas.append(per)
+    ws = ops.attn_workspace(1, sh.nh, sh.nkv, ns, dev)
+    out = torch.empty(1, sh.nh * 128, dtype=torch.bfloat16, device=dev)
+    calls = []
+    for r, per in zip(runners, arenas):
+        cs = ops.rope_rows(r.inv_freq, r.pos_buf, 1)
+        for li, (kv, table) in enumerate(per):
+            calls.append(lambda r=r, li=li, kv=kv, table=table, cs=cs: ops.paged_decode_layer(
+                r.qkv_dec[li], r.qn_w[li], r.kn_w[li], r.eps, cs, r.pos_buf, kv, table, bound, sh.scale, ws, ns, out,
+                sh.nh, sh.nkv))
+    us = _graph_us(torch, dev, calls, reps=4)
+    contiguous = time_decode_kernel(torch, ops, runners, bound, ns, sh, dev, reps=4)
+    del arenas
+    torch.cuda.empty_cache()
+    nbytes = decode_bytes(bound)
+    return {"page_size": page_size, "bound": bound, "n_split": ns, "us": round(us, 3),
+            "gbps": round(nbytes / (us * 1e-6) / 1e9, 1), "contiguous_us": round(contiguous, 3)}
 
 
 def model_extras(torch, dev, live: int = 960, n: int = 48) -> dict:
