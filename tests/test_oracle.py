@@ -297,7 +297,8 @@ def test_prefill_blockwise_equals_exact_without_rounding_and_close_with_it():
     orig = exact.bf16_round
     try:
         exact.bf16_round = lambda x: np.asarray(x, np.float64)
-        got = [exact.prefill_blockwise(q, k, v, SCALE, splits=sp, lazy=lz) for sp in (1, 2, 3) for lz in (0.0, 8.0)]
+        got = [exact.prefill_blockwise(q, k, v, SCALE, block=bk, splits=sp, lazy=lz)
+               for bk, sp in ((64, 1), (64, 2), (64, 3), (32, 4), (16, 5)) for lz in (0.0, 8.0)]
         # keys x8 (scores far above the lazy threshold) still merge back to exact attention
         k8 = k.copy()
         k8[::7] *= 8.0
