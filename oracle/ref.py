@@ -178,6 +178,26 @@ def decode_model_step(w: dict, tok: int, pos: int, kc: torch.Tensor, vc: torch.T
     return linear(rmsnorm(x, w["final_norm"], eps), w["lm_head"]).view(-1)
 
 
+
+def prefill_model(w: dict, ids: list[int], kc: torch.Tensor, vc: torch.Tensor, nh: int, nkv: int, eps: float = 1e-6,
+                  theta: float = 1e6) -> torch.Tensor:
+    """The prompt forward of a whole model, cuda_graph_executor.py:104-135, on the CPU in the weights'
+    dtype: embedding rows, per layer input norm + fused QKV, q/k norm + RoPE + KV write of rows
+    0..T-1 + causal grouped attention, o_proj + residual, post norm + gate/up + silu * up + down +
+    residual.  kc/vc [L, max_len, nkv, hd] are written in place.  Returns the logits [V] of the
+    last row (final norm and lm_head, :135 and :161)."""
+    hd = kc.shape[-1]
+    T = len(ids)
+    cos, sin = cos_sin(torch.arange(T), inv_freq(hd, theta), w["embed"].dtype)
+    x = w["embed"][torch.as_tensor(ids, dtype=torch.long)]
+    for li in range(kc.shape[0]):
+        qkv = linear(rmsnorm(x, w["in_ln"][li], eps), w["wqkv"][li])
+        q, k, v = prologue(qkv, w["qn"][li], w["kn"][li], eps, cos, sin, nh, nkv, hd)
+        write_kv(kc[li], vc[li], k, v, 0)
+        ctx = prefill_attn(q, k, v, hd ** -0.5)
+        x = decode_mlp_block(x, ctx, w["wo"][li], w["post_ln"][li], w["wgu"][li], w["wd"][li], eps)
+    return linear(rmsnorm(x[T - 1:], w["final_norm"], eps), w["lm_head"]).view(-1)
+
 # ---------------------------------------------------------------- paged KV cache (src/solort/cache/kv_cache.py)
 
 

@@ -21,9 +21,10 @@ from __future__ import annotations
 from dataclasses import dataclass
 
 import torch
+import torch.nn.functional as F
 
 from . import ops
-from .runner import DECODE_BUCKETS, HD, decode_splits
+from .runner import DECODE_BUCKETS, FUSED_PREFILL_MIN, HD, PREFILL_BUCKETS, decode_splits
 
 
 @dataclass(frozen=True)
@@ -73,6 +74,13 @@ class RandomQwen3:
         self.lm_head = self.embed if s.tie_embeddings else rnd(s.vocab, H)
 
 
+def _rmsnorm_rows(x: torch.Tensor, w: torch.Tensor, eps: float) -> torch.Tensor:
+    """cuda_graph_executor.py:25-28 over the rows of a prompt, as the reference's torch ops on the
+    device: fp32 upcast, x * rsqrt(mean(x^2) + eps), times w in fp32, cast back."""
+    xf = x.float()
+    return ((xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps)) * w.float()).to(x.dtype)
+
+
 class GraphQwen3Decode:
     """Greedy decode over a runner-owned bf16 KV cache, one captured graph per KV bucket."""
 
@@ -106,6 +114,17 @@ class GraphQwen3Decode:
         self.ws = ops.attn_workspace(1, s.nh, s.nkv, max(decode_splits(b, s.nkv) for b in self.buckets), self.dev)
         self.ws_arg = ops.gemv_argmax_workspace(s.vocab, self.dev) if fused_tail else ops.argmax_workspace(1, self.dev)
         self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        # prefill (cuda_graph_executor.py:83-85, :104-161): one graph per prompt bucket over the padded
+        # token buffer; the graph returns the last layer's hidden rows
+        self.pre_buckets = sorted(b for b in PREFILL_BUCKETS if b <= self.max_len)
+        pmax = max(self.pre_buckets)
+        self.pre_tok = torch.zeros(pmax, dtype=torch.long, device=self.dev)
+        self.cs_pre = torch.zeros(2 * pmax * (HD // 2), **bf)
+        self.q_pre = torch.zeros(min(pmax, FUSED_PREFILL_MIN), s.nh, HD, **bf)
+        self.ctx_pre = torch.zeros(pmax, s.nh * HD, **bf)
+        self.zero_pos = torch.zeros(1, dtype=torch.long, device=self.dev)
+        self._pre_graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self._pre_hidden: dict[int, torch.Tensor] = {}
 
     def start(self, token: int, pos: int) -> None:
         """The first input: token at position pos (rows 0..pos-1 of the cache hold the context)."""
@@ -156,6 +175,78 @@ class GraphQwen3Decode:
                 self._step(bound)
             self._graphs[bound] = g
         return self._graphs[bound]
+
+    def _prefill_forward(self, bound: int) -> torch.Tensor:
+        """cuda_graph_executor.py:104-135 over pre_tok[:bound] at positions 0..bound-1: the T-row
+        products as library GEMMs (hipBLASLt), the attention block (with the KV write of rows
+        0..bound-1) as solort_prefill_layer, or for short buckets the prologue then
+        solort_prefill_attn.  Returns the last layer's hidden rows [bound, hidden] (the final norm
+        is applied to the one row the lm_head reads)."""
+        s, w = self.s, self.w
+        cs = self.cs_pre[: 2 * bound * (HD // 2)].view(2, bound, HD // 2)
+        ops.rope_rows(self.inv_freq, self.zero_pos, bound, cs)                  # :111
+        x = w.embed.index_select(0, self.pre_tok[:bound])                       # :112
+        ctx = self.ctx_pre[:bound]
+        for li in range(s.layers):
+            qkv = F.linear(_rmsnorm_rows(x, w.in_ln[li], self.eps), w.wqkv[li])  # :114-115
+            if bound >= FUSED_PREFILL_MIN:                                       # :116-130
+                ops.prefill_layer(qkv, w.qn[li], w.kn[li], self.eps, cs, self.kc[li], self.vc[li], self.scale, ctx,
+                                  s.nh, s.nkv)
+            else:
+                ops.qknorm_rope_kvwrite_cs(qkv, w.qn[li], w.kn[li], self.eps, cs, None, self.q_pre[:bound],
+                                           self.kc[li], self.vc[li], s.nh, s.nkv)
+                ops.prefill_attn(self.q_pre[:bound], self.kc[li], self.vc[li], self.scale, ctx)
+            x = x + F.linear(ctx, w.wo[li])                                      # :131
+            gate, up = F.linear(_rmsnorm_rows(x, w.post_ln[li], self.eps), w.wgu[li]).split(s.inter, dim=-1)
+            x = x + F.linear(F.silu(gate) * up, w.wd[li])                        # :132-134
+        return x
+
+    def prefill(self, ids: torch.Tensor | list[int]) -> None:
+        """Graphed bucketed prefill (cuda_graph_executor.py:149-161) of a prompt of plen tokens: pads
+        it with token 0 to the first prompt bucket >= plen, replays that bucket's graph (cache rows
+        0..bucket-1 written; decode never reads the padding rows), then runs the final norm + lm_head +
+        greedy argmax on row plen-1 (the reference runs its lm_head eagerly for that one row, :161)
+        and leaves the first generated token as the next decode input at position plen, recorded
+        as tokens[0]."""
+        ids = torch.as_tensor(ids, dtype=torch.long).view(-1)
+        plen = int(ids.numel())
+        bound = next((b for b in self.pre_buckets if b >= plen), None)
+        if bound is None or plen < 1:
+            raise RuntimeError(f"prompt length {plen} outside the prefill buckets {self.pre_buckets}")
+        self.pre_tok[:plen].copy_(ids.to(self.dev))
+        self.pre_tok[plen:bound].zero_()
+        if bound not in self._pre_graphs:
+            self._prefill_forward(bound)  # eager once: the GEMM library initialises outside the capture
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._pre_hidden[bound] = self._prefill_forward(bound)
+            self._pre_graphs[bound] = graph
+        self._pre_graphs[bound].replay()
+        s, w = self.s, self.w
+        last = self._pre_hidden[bound][plen - 1]
+        self.pos.fill_(plen - 1)
+        self.step.zero_()
+        if self.fused_tail:
+            ops.gemv_argmax(w.lm_head, last, None, self.ws_arg, w.final_norm, self.eps, logits=self.logits.view(-1))
+            ops.greedy_advance(self.ws_arg, s.vocab, w.embed, self.x.view(-1), self.tok, self.tokens, self.step,
+                               self.pos)
+        else:
+            ops.gemv(w.lm_head, last, self.logits.view(-1), w.final_norm, self.eps)
+            ops.argmax_rows(self.logits, self.tok, self.ws_arg)
+            self.tokens.index_copy_(0, self.step, self.tok)
+            self.step.add_(1)
+            self.pos.add_(1)
+
+    def generate_from_prompt(self, ids: torch.Tensor | list[int], n: int) -> list[int]:
+        """Greedy continuation of a prompt: prefill, then n - 1 decode replays (one host
+        synchronisation); returns the n generated tokens."""
+        plen = len(ids)
+        if n < 1 or n > self.tokens.numel() or plen + n > self.max_len:
+            raise RuntimeError(f"cannot generate {n} tokens after a {plen}-token prompt (max_len {self.max_len})")
+        self.prefill(ids)
+        for i in range(n - 1):
+            self.graph(self.bucket_for(plen + i)).replay()
+        return self.tokens[:n].tolist()
 
     def generate(self, first_token: int, pos: int, n: int) -> list[int]:
         """Greedy tokens after `first_token` at position `pos` (rows 0..pos-1 of the cache hold the

@@ -105,3 +105,64 @@ def test_decode_steps_match_reference_ops(gpu, shape):
     kr = (kc.float() - kc32).abs().max().item()
     _say(f"  K rows written: device {kd:.3e}, bf16 reference {kr:.3e} from the fp32 model")
     assert kd <= 2.0 * kr + 2e-3
+
+
+@pytest.mark.parametrize("plen,max_len", [(37, 256), (300, 512)], ids=["bucket64", "bucket512-fused"])
+def test_prompt_prefill_then_decode_match_reference_ops(gpu, plen, max_len):
+    """Prompt prefill (cuda_graph_executor.py:104-161: library GEMMs around solort_prefill_layer or
+    the prologue + solort_prefill_attn) and the decode steps after it, against the CPU evaluations of
+    the same model in bf16 and fp32.  The first token's logits and the KV rows of the prompt are
+    held to the bf16 reference's own distance from the fp32 model (as the decode steps are); the
+    first token is the device argmax of its logits and becomes the decode input at position plen;
+    three teacher-forced decode steps follow on each side's own cache."""
+    shape = TINY_UNTIED
+    w = RandomQwen3(shape, gpu, seed=83)
+    m = GraphQwen3Decode(w, max_len)
+    g = torch.Generator().manual_seed(84)
+    ids = torch.randint(0, shape.vocab, (plen,), generator=g).tolist()
+    bf = {k: (v.cpu() if torch.is_tensor(v) else [t.cpu() for t in v]) for k, v in vars(w).items() if k != "shape"}
+    f32 = {k: (v.float() if torch.is_tensor(v) else [t.float() for t in v]) for k, v in bf.items()}
+    kv_shape = (shape.layers, max_len, shape.nkv, 128)
+    kc, vc = torch.zeros(kv_shape, dtype=torch.bfloat16), torch.zeros(kv_shape, dtype=torch.bfloat16)
+    kc32, vc32 = torch.zeros(kv_shape), torch.zeros(kv_shape)
+    m.prefill(ids)
+    torch.cuda.synchronize()
+    got = m.logits.view(-1).float().cpu()
+    want = ref.prefill_model(bf, ids, kc, vc, shape.nh, shape.nkv).float()
+    exact = ref.prefill_model(f32, ids, kc32, vc32, shape.nh, shape.nkv)
+    dg, dr = (got - exact).abs(), (want - exact).abs()
+    _say(f"  prefill T={plen}: to fp32 model device mean {dg.mean().item():.3e} max {dg.max().item():.3e} | "
+         f"bf16 reference mean {dr.mean().item():.3e} max {dr.max().item():.3e}")
+    assert dg.mean().item() <= 1.5 * dr.mean().item() + 2e-3 and dg.max().item() <= 2.0 * dr.max().item() + 2e-3
+    kd = (m.kc[:, :plen].float().cpu() - kc32[:, :plen]).abs().max().item()
+    kr = (kc[:, :plen].float() - kc32[:, :plen]).abs().max().item()
+    _say(f"  prompt K rows: device {kd:.3e}, bf16 reference {kr:.3e} from the fp32 model")
+    assert kd <= 2.0 * kr + 2e-3
+    tok = int(m.tok.item())
+    assert tok == int(torch.argmax(got).item()) and m.tokens[0].item() == tok
+    assert m.pos.item() == plen and m.step.item() == 1 and torch.equal(m.x.view(-1), w.embed[tok])
+    for i in range(3):  # decode after the prompt, teacher-forced with the device's tokens
+        pos = plen + i
+        m.graph(m.bucket_for(pos)).replay()
+        torch.cuda.synchronize()
+        got = m.logits.view(-1).float().cpu()
+        want = ref.decode_model_step(bf, tok, pos, kc, vc, m.bucket_for(pos), shape.nh, shape.nkv).float()
+        exact = ref.decode_model_step(f32, tok, pos, kc32, vc32, m.bucket_for(pos), shape.nh, shape.nkv)
+        dg, dr = (got - exact).abs(), (want - exact).abs()
+        _say(f"  decode pos {pos}: device mean {dg.mean().item():.3e} | bf16 reference mean {dr.mean().item():.3e}")
+        assert dg.mean().item() <= 1.5 * dr.mean().item() + 2e-3 and dg.max().item() <= 2.0 * dr.max().item() + 2e-3
+        tok = int(m.tok.item())
+        assert m.tokens[i + 1].item() == tok
+
+
+def test_generate_from_prompt_is_prefill_then_decode_replays(gpu):
+    """generate_from_prompt = prefill + n-1 decode replays, with either step tail (identical tokens),
+    and a second prompt on the same runner (captured graphs reused) repeats the first result."""
+    w = RandomQwen3(TINY_UNTIED, gpu, seed=85)
+    ids = list(range(3, 60, 2))
+    a = GraphQwen3Decode(w, 256).generate_from_prompt(ids, 10)
+    m = GraphQwen3Decode(w, 256, fused_tail=False)
+    b = m.generate_from_prompt(ids, 10)
+    c = m.generate_from_prompt(ids, 10)
+    _say(f"  tokens {a}")
+    assert a == b == c and len(set(a)) > 1

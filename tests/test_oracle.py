@@ -407,3 +407,30 @@ def test_paged_store_and_gather_match_reference_test_vectors():
     assert torch.equal(k_out, key[0].transpose(0, 1)) and torch.equal(v_out, value[0].transpose(0, 1))
     k0, _ = ref.paged_gather(kv[0], slots)
     assert torch.equal(k0, (key + 200)[0].transpose(0, 1)) and not torch.equal(k0, k_out)
+
+
+def test_prefill_model_equals_sequential_decode_steps():
+    """The prompt forward (causal SDPA over all rows, cuda_graph_executor.py:104-135) and T single-token
+    decode steps (masked grouped attention, :163-190) are the same function of the prompt: in fp32 the
+    last row's logits and every KV row agree to rounding.  Pins both whole-model restatements against
+    each other through different attention code."""
+    torch.manual_seed(0)
+    L, H, I, nh, nkv, V = 2, 256, 512, 4, 2, 300
+    width = (nh + 2 * nkv) * HD
+
+    def f(*s, std=0.02, mean=0.0):
+        return torch.randn(*s) * std + mean
+
+    w = {"embed": f(V, H, std=0.05), "in_ln": f(L, H, std=0.1, mean=1), "post_ln": f(L, H, std=0.1, mean=1),
+         "qn": f(L, HD, std=0.1, mean=1), "kn": f(L, HD, std=0.1, mean=1), "wqkv": [f(width, H) for _ in range(L)],
+         "wo": [f(H, nh * HD) for _ in range(L)], "wgu": [f(2 * I, H) for _ in range(L)],
+         "wd": [f(H, I) for _ in range(L)], "final_norm": f(H, std=0.1, mean=1), "lm_head": f(V, H)}
+    ids = [5, 17, 42, 7, 99, 3, 250, 11, 0, 64]
+    kc, vc = torch.zeros(L, 64, nkv, HD), torch.zeros(L, 64, nkv, HD)
+    lg = ref.prefill_model(w, ids, kc, vc, nh, nkv)
+    kc2, vc2 = torch.zeros_like(kc), torch.zeros_like(vc)
+    for p, t in enumerate(ids):
+        lg2 = ref.decode_model_step(w, t, p, kc2, vc2, 64, nh, nkv)
+    assert (lg - lg2).abs().max().item() < 1e-5
+    assert (kc - kc2).abs().max().item() < 1e-4 and (vc - vc2).abs().max().item() < 1e-4
+    assert torch.equal(vc[0], vc2[0])  # layer 0's V rows are the embedding's projection in both
