@@ -396,6 +396,21 @@ def model_extras(torch, dev, live: int = 960, n: int = 48) -> dict:
              "frac_hbm": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
              "first_tokens": m.tokens[:8].tolist()}
         if fused:
+            # time to first token: a prompt's prefill graph plus the last row's lm_head and argmax
+            ttft = {}
+            for plen in (128, 1024):
+                ids = torch.randint(0, s.vocab, (plen,), generator=torch.Generator().manual_seed(plen)).tolist()
+                m.prefill(ids)  # captures the bucket's graph
+                reps = []
+                for _ in range(3):
+                    torch.cuda.synchronize()
+                    e0.record(stream)
+                    m.prefill(ids)
+                    e1.record(stream)
+                    torch.cuda.synchronize()
+                    reps.append(e0.elapsed_time(e1))
+                ttft[str(plen)] = {"ms": round(min(reps), 3), "tokens_per_s": round(plen / min(reps) * 1e3, 1)}
+            r["prefill_ttft"] = ttft
             out.update(r)
         else:
             out["separate_tail"] = r
