@@ -198,6 +198,25 @@ def prefill_model(w: dict, ids: list[int], kc: torch.Tensor, vc: torch.Tensor, n
         x = decode_mlp_block(x, ctx, w["wo"][li], w["post_ln"][li], w["wgu"][li], w["wd"][li], eps)
     return linear(rmsnorm(x[T - 1:], w["final_norm"], eps), w["lm_head"]).view(-1)
 
+
+def verify_model(w: dict, toks: list[int], pos0: int, kc: torch.Tensor, vc: torch.Tensor, nh: int, nkv: int,
+                 eps: float = 1e-6, theta: float = 1e6) -> torch.Tensor:
+    """The speculative-verify forward of a whole model, cuda_graph_executor.py:245-268, on the CPU in
+    the weights' dtype: K+1 tokens at positions pos0..pos0+K, each layer writing their K/V rows and
+    attending every cache key <= its position (all max_len keys under the mask).  Returns the
+    logits [K+1, V]."""
+    hd = kc.shape[-1]
+    k1 = len(toks)
+    cos, sin = cos_sin(pos0 + torch.arange(k1), inv_freq(hd, theta), w["embed"].dtype)
+    x = w["embed"][torch.as_tensor(toks, dtype=torch.long)]
+    for li in range(kc.shape[0]):
+        qkv = linear(rmsnorm(x, w["in_ln"][li], eps), w["wqkv"][li])
+        q, k, v = prologue(qkv, w["qn"][li], w["kn"][li], eps, cos, sin, nh, nkv, hd)
+        write_kv(kc[li], vc[li], k, v, pos0)
+        ctx = verify_attn(q, kc[li], vc[li], pos0, hd ** -0.5)
+        x = decode_mlp_block(x, ctx, w["wo"][li], w["post_ln"][li], w["wgu"][li], w["wd"][li], eps)
+    return linear(rmsnorm(x, w["final_norm"], eps), w["lm_head"])
+
 # ---------------------------------------------------------------- paged KV cache (src/solort/cache/kv_cache.py)
 
 

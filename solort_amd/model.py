@@ -24,7 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from . import ops
-from .runner import DECODE_BUCKETS, FUSED_PREFILL_MIN, HD, PREFILL_BUCKETS, decode_splits
+from .runner import DECODE_BUCKETS, FUSED_PREFILL_MIN, HD, PREFILL_BUCKETS, decode_splits, verify_splits
 
 
 @dataclass(frozen=True)
@@ -85,11 +85,12 @@ class GraphQwen3Decode:
     """Greedy decode over a runner-owned bf16 KV cache, one captured graph per KV bucket."""
 
     def __init__(self, weights: RandomQwen3, max_len: int, eps: float = 1e-6, theta: float = 1e6,
-                 max_tokens: int = 4096, fused_tail: bool = True) -> None:
+                 max_tokens: int = 4096, fused_tail: bool = True, spec_k: int = 4) -> None:
         """fused_tail: the argmax folded into the lm_head launch and the token bookkeeping plus the
         next embedding row in one launch (solort_gemv_argmax + solort_greedy_advance); False runs
         the same step as the reference's separate ops (lm_head, argmax, token copy, counter adds,
-        embedding gather).  Both give the same tokens bit for bit."""
+        embedding gather).  Both give the same tokens bit for bit.  spec_k: draft tokens per
+        speculative round (the verify graph scores spec_k + 1 tokens)."""
         self.w = weights
         self.fused_tail = bool(fused_tail)
         s = self.s = weights.shape
@@ -125,6 +126,19 @@ class GraphQwen3Decode:
         self.zero_pos = torch.zeros(1, dtype=torch.long, device=self.dev)
         self._pre_graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self._pre_hidden: dict[int, torch.Tensor] = {}
+        # speculative verify (cuda_graph_executor.py:245-289, :463-482): spec_k + 1 tokens per
+        # graph, bucketed by key range like decode; acceptance on the device
+        self.k1 = int(spec_k) + 1
+        self.vtok = torch.zeros(self.k1, dtype=torch.long, device=self.dev)  # the input token, then the drafts
+        self.vpos0 = torch.zeros(1, dtype=torch.long, device=self.dev)
+        self.cs_ver = torch.zeros(2, self.k1, HD // 2, **bf)
+        self.ctx_ver = torch.zeros(self.k1, s.nh * HD, **bf)
+        self.tok_ver = torch.zeros(self.k1, dtype=torch.long, device=self.dev)
+        self.acc_ver = torch.zeros(2, dtype=torch.long, device=self.dev)
+        self.ws_ver = ops.attn_workspace(self.k1, s.nh, s.nkv, max(verify_splits(b) for b in self.buckets), self.dev)
+        self.ws_argv = ops.argmax_workspace(self.k1, self.dev)
+        self._ver_graphs: dict[int, torch.cuda.CUDAGraph] = {}
+        self._ver_logits: dict[int, torch.Tensor] = {}
 
     def start(self, token: int, pos: int) -> None:
         """The first input: token at position pos (rows 0..pos-1 of the cache hold the context)."""
@@ -247,6 +261,83 @@ class GraphQwen3Decode:
         for i in range(n - 1):
             self.graph(self.bucket_for(plen + i)).replay()
         return self.tokens[:n].tolist()
+
+    def _verify_forward(self, bound: int) -> torch.Tensor:
+        """cuda_graph_executor.py:245-268 for the k1 tokens in vtok at vpos0..vpos0+k1-1: library GEMMs
+        on the k1 rows around solort_decode_layer (nq = k1: prologue, KV write, causal attention over
+        the bucket), the logits [k1, V], their argmax (:475) and the accepted-prefix rule (:476-481)
+        into acc_ver = [a, tg[a]]."""
+        s, w = self.s, self.w
+        ops.rope_rows(self.inv_freq, self.vpos0, self.k1, self.cs_ver)          # :248
+        x = w.embed.index_select(0, self.vtok)                                  # :249
+        for li in range(s.layers):
+            qkv = F.linear(_rmsnorm_rows(x, w.in_ln[li], self.eps), w.wqkv[li])  # :252-253
+            ops.decode_layer(qkv, w.qn[li], w.kn[li], self.eps, self.cs_ver, self.vpos0, self.kc[li], self.vc[li],
+                             bound, self.scale, self.ws_ver, verify_splits(bound), self.ctx_ver, s.nh, s.nkv)
+            x = x + F.linear(self.ctx_ver, w.wo[li])                            # :264
+            gate, up = F.linear(_rmsnorm_rows(x, w.post_ln[li], self.eps), w.wgu[li]).split(s.inter, dim=-1)
+            x = x + F.linear(F.silu(gate) * up, w.wd[li])                       # :265-267
+        logits = F.linear(_rmsnorm_rows(x, w.final_norm, self.eps), w.lm_head)   # :268
+        ops.argmax_rows(logits, self.tok_ver, self.ws_argv)
+        if self.k1 > 1:
+            ops.accept_prefix(self.tok_ver, self.vtok[1:], self.acc_ver)
+        return logits
+
+    def verify(self, pos0: int) -> torch.Tensor:
+        """Replays the verify graph of the bucket holding positions pos0..pos0+k1-1 over the tokens
+        already in vtok; tok_ver then holds the k1 argmax tokens and acc_ver [a, tg[a]].  Returns the
+        logits [k1, V] (the graph's buffer)."""
+        if not 0 <= pos0 <= self.max_len - self.k1:
+            raise RuntimeError(f"verify positions {pos0}..{pos0 + self.k1 - 1} exceed max_len {self.max_len}")
+        bound = self.bucket_for(pos0 + self.k1 - 1)
+        self.vpos0.fill_(int(pos0))
+        if bound not in self._ver_graphs:
+            self._verify_forward(bound)  # eager once: the GEMM library initialises outside the capture
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                self._ver_logits[bound] = self._verify_forward(bound)
+            self._ver_graphs[bound] = graph
+        self._ver_graphs[bound].replay()
+        return self._ver_logits[bound]
+
+    def speculative_round(self, draft: "GraphQwen3Decode", last_token: int, pos: int) -> list[int]:
+        """One exact greedy speculative round, cuda_graph_executor.py:463-482: the draft model decodes
+        k = k1 - 1 tokens from last_token at pos (its own graphs and cache), this model scores
+        [last_token, drafts] at pos..pos+k in one verify replay, and the accepted drafts plus the
+        token after them are returned (one host synchronisation).  With every draft accepted the
+        draft also decodes its last draft at pos+k, so its cache stays whole (:479)."""
+        k = self.k1 - 1
+        if draft.k1 != self.k1 or draft.max_len < pos + k + 1:
+            raise RuntimeError("draft model does not match the verify width or is too short")
+        draft.start(last_token, pos)
+        for i in range(k):
+            draft.graph(draft.bucket_for(pos + i)).replay()
+        self.vtok[0].fill_(int(last_token))
+        self.vtok[1:].copy_(draft.tokens[:k])
+        self.verify(pos)
+        got = torch.cat([self.acc_ver, self.vtok[1:]]).tolist()  # the one synchronisation
+        a, nxt, drafts = got[0], got[1], got[2:]
+        if a == k:
+            draft.start(drafts[k - 1], pos + k)
+            draft.graph(draft.bucket_for(pos + k)).replay()
+        return drafts[:a] + [nxt]
+
+    def generate_speculative(self, draft: "GraphQwen3Decode", ids: list[int], n: int) -> tuple[list[int], list[int]]:
+        """Greedy continuation of a prompt by speculative rounds: both models prefill the prompt,
+        then rounds run until n tokens are out (the last round's extra tokens are dropped).
+        Returns the tokens and the accepted-draft count of every round."""
+        plen = len(ids)
+        if plen + n + self.k1 > min(self.max_len, draft.max_len):
+            raise RuntimeError(f"{plen} + {n} tokens and a round of {self.k1} exceed max_len")
+        self.prefill(ids)
+        draft.prefill(ids)
+        out = [int(self.tok.item())]
+        accepted = []
+        while len(out) < n:
+            toks = self.speculative_round(draft, out[-1], plen + len(out) - 1)
+            accepted.append(len(toks) - 1)
+            out += toks
+        return out[:n], accepted
 
     def generate(self, first_token: int, pos: int, n: int) -> list[int]:
         """Greedy tokens after `first_token` at position `pos` (rows 0..pos-1 of the cache hold the

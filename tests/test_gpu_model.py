@@ -166,3 +166,76 @@ def test_generate_from_prompt_is_prefill_then_decode_replays(gpu):
     c = m.generate_from_prompt(ids, 10)
     _say(f"  tokens {a}")
     assert a == b == c and len(set(a)) > 1
+
+
+def test_verify_graph_matches_reference_ops(gpu):
+    """The whole-model verify graph (cuda_graph_executor.py:245-268 with the argmax and acceptance of
+    :475-481): its logits against the CPU evaluations in bf16 and fp32 (the decode steps' bar), its
+    argmax tokens the argmax of its logits, and acc_ver the first-mismatch rule applied on the host."""
+    shape = TINY_UNTIED
+    p0 = 90
+    w, m = _model(gpu, p0, shape)
+    bf = {k: (v.cpu() if torch.is_tensor(v) else [t.cpu() for t in v]) for k, v in vars(w).items() if k != "shape"}
+    f32 = {k: (v.float() if torch.is_tensor(v) else [t.float() for t in v]) for k, v in bf.items()}
+    kc, vc = m.kc.cpu(), m.vc.cpu()
+    kc32, vc32 = kc.float(), vc.float()
+    g = torch.Generator().manual_seed(87)
+    for rnd in range(3):
+        toks = torch.randint(0, shape.vocab, (m.k1,), generator=g).tolist()
+        pos0 = p0 + rnd * m.k1
+        m.vtok.copy_(torch.tensor(toks, device=gpu))
+        logits = m.verify(pos0).float().cpu()
+        torch.cuda.synchronize()
+        want = ref.verify_model(bf, toks, pos0, kc, vc, shape.nh, shape.nkv).float()
+        exact = ref.verify_model(f32, toks, pos0, kc32, vc32, shape.nh, shape.nkv)
+        dg, dr = (logits - exact).abs(), (want - exact).abs()
+        _say(f"  verify at {pos0}: device mean {dg.mean().item():.3e} max {dg.max().item():.3e} | "
+             f"bf16 reference mean {dr.mean().item():.3e} max {dr.max().item():.3e}")
+        assert dg.mean().item() <= 1.5 * dr.mean().item() + 2e-3 and dg.max().item() <= 2.0 * dr.max().item() + 2e-3
+        tg = m.tok_ver.tolist()
+        assert tg == logits.argmax(-1).tolist()
+        a, nxt = ref.accept_prefix(torch.tensor(tg), torch.tensor(toks[1:]))
+        assert m.acc_ver.tolist() == [a, nxt]
+    kd = (m.kc[:, : p0 + 3 * m.k1].float().cpu() - kc32[:, : p0 + 3 * m.k1]).abs().max().item()
+    kr = (kc[:, : p0 + 3 * m.k1].float() - kc32[:, : p0 + 3 * m.k1]).abs().max().item()
+    assert kd <= 2.0 * kr + 2e-3
+
+
+@pytest.mark.parametrize("draft_seed", [None, 99], ids=["draft-same-weights", "draft-other-weights"])
+def test_speculative_generation(gpu, draft_seed):
+    """Greedy speculative rounds (cuda_graph_executor.py:463-482) after a prompt prefill: every
+    emitted token is the fp32 model's argmax at its position (teacher-forced on the CPU with the
+    emitted tokens) wherever that argmax leads the runner-up by more than 0.05, the target cache
+    rows hold the emitted sequence's K rows, and a draft with the target's weights has most of its
+    drafts accepted while a draft with other weights has almost none."""
+    shape = TINY_UNTIED
+    w = RandomQwen3(shape, gpu, seed=86)
+    target = GraphQwen3Decode(w, 256)
+    draft = GraphQwen3Decode(w if draft_seed is None else RandomQwen3(shape, gpu, seed=draft_seed), 256)
+    ids = torch.randint(0, shape.vocab, (20,), generator=torch.Generator().manual_seed(88)).tolist()
+    n = 24
+    toks, accepted = target.generate_speculative(draft, ids, n)
+    _say(f"  tokens {toks}\n  accepted per round {accepted}")
+    bf = {k: (v.cpu() if torch.is_tensor(v) else [t.cpu() for t in v]) for k, v in vars(w).items() if k != "shape"}
+    f32 = {k: (v.float() if torch.is_tensor(v) else [t.float() for t in v]) for k, v in bf.items()}
+    kc32 = torch.zeros(shape.layers, 256, shape.nkv, 128)
+    vc32 = torch.zeros_like(kc32)
+    lg = ref.prefill_model(f32, ids, kc32, vc32, shape.nh, shape.nkv)
+    checked = 0
+    for i in range(n):
+        top2 = torch.topk(lg, 2).values
+        if (top2[0] - top2[1]).item() > 0.05:
+            assert toks[i] == int(lg.argmax().item()), i
+            checked += 1
+        if i + 1 < n:
+            lg = ref.decode_model_step(f32, toks[i], len(ids) + i, kc32, vc32, target.bucket_for(len(ids) + i),
+                                       shape.nh, shape.nkv)
+    P = len(ids) + n - 1
+    kd = (target.kc[:, :P].float().cpu() - kc32[:, :P]).abs().max().item()
+    _say(f"  {checked} of {n} tokens checked against the fp32 argmax; cache K rows to fp32 {kd:.3e}")
+    assert checked >= n // 2 and kd <= 6e-2
+    k = target.k1 - 1
+    if draft_seed is None:
+        assert sum(accepted) >= 0.6 * k * len(accepted)
+    else:
+        assert sum(accepted) <= 0.2 * k * len(accepted)

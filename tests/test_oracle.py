@@ -433,3 +433,27 @@ def test_prefill_model_equals_sequential_decode_steps():
         lg2 = ref.decode_model_step(w, t, p, kc2, vc2, 64, nh, nkv)
     assert (lg - lg2).abs().max().item() < 1e-5
     assert (kc - kc2).abs().max().item() < 1e-4 and (vc - vc2).abs().max().item() < 1e-4
+
+
+def test_verify_model_equals_sequential_decode_steps():
+    """The K+1-token verify forward (mask key <= position over all max_len keys, :245-268) equals K+1
+    single-token decode steps (:163-190) over the same cache, in fp32 to rounding."""
+    torch.manual_seed(1)
+    L, H, I, nh, nkv, V = 2, 256, 512, 4, 2, 300
+    width = (nh + 2 * nkv) * HD
+
+    def f(*s, std=0.02, mean=0.0):
+        return torch.randn(*s) * std + mean
+
+    w = {"embed": f(V, H, std=0.05), "in_ln": f(L, H, std=0.1, mean=1), "post_ln": f(L, H, std=0.1, mean=1),
+         "qn": f(L, HD, std=0.1, mean=1), "kn": f(L, HD, std=0.1, mean=1), "wqkv": [f(width, H) for _ in range(L)],
+         "wo": [f(H, nh * HD) for _ in range(L)], "wgu": [f(2 * I, H) for _ in range(L)],
+         "wd": [f(H, I) for _ in range(L)], "final_norm": f(H, std=0.1, mean=1), "lm_head": f(V, H)}
+    kc = torch.randn(L, 64, nkv, HD)
+    vc = torch.randn_like(kc)
+    kc2, vc2 = kc.clone(), vc.clone()
+    toks = [3, 9, 27, 81, 243]
+    lg = ref.verify_model(w, toks, 20, kc, vc, nh, nkv)
+    for i, t in enumerate(toks):
+        assert (lg[i] - ref.decode_model_step(w, t, 20 + i, kc2, vc2, 64, nh, nkv)).abs().max().item() < 1e-5
+    assert (kc - kc2).abs().max().item() < 1e-4 and (vc - vc2).abs().max().item() < 1e-4
