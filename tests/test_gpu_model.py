@@ -23,6 +23,9 @@ TINY = ModelShape("tiny", hidden=512, inter=1024, nh=4, nkv=2, layers=2, vocab=4
 # untied one walks through varied tokens
 TINY_UNTIED = ModelShape("tiny-untied", hidden=512, inter=1024, nh=8, nkv=2, layers=3, vocab=4096,
                          tie_embeddings=False)
+# the Qwen3-4B widths (hidden, intermediate, heads, vocabulary, tied embedding) with two layers
+QWEN3_4B_2L = ModelShape("qwen3-4b-2layers", hidden=2560, inter=9728, nh=32, nkv=8, layers=2, vocab=151936,
+                         tie_embeddings=True)
 
 
 def _say(msg):
@@ -62,7 +65,7 @@ def test_decode_graph_replays_equal_eager_steps(gpu):
     _say(f"  tokens {toks}")
 
 
-@pytest.mark.parametrize("shape", [TINY, TINY_UNTIED], ids=lambda s: s.name)
+@pytest.mark.parametrize("shape", [TINY, TINY_UNTIED, QWEN3_4B_2L], ids=lambda s: s.name)
 def test_decode_steps_match_reference_ops(gpu, shape):
     """Each step's logits against two CPU evaluations of cuda_graph_executor.py:163-190 fed the same
     tokens: the reference's bf16 arithmetic, and the same weights and cache in fp32 (no intermediate
