@@ -210,6 +210,28 @@ int solort_paged_decode_layer(const void* qkv, int64_t qkv_row_stride, int nq, i
                               int n_split, void* out, int out_dtype, solort_stream_t stream);
 
 /*
+ * Slot-mapped row copies for the paged arena (layout as in
+ * solort_paged_decode_layer).  store: K/V row t of the contiguous rows
+ * (k_rows/v_rows, token stride row_tok_stride, head stride row_head_stride)
+ * -> physical slot slot_mapping[t] (page slot / page_size, row
+ * slot % page_size), the reference's store_layer_tokens
+ * (src/solort/cache/kv_cache.py:191-230; slots from its slot_mapping,
+ * :131-145).  gather: slot slot_mapping[t] -> row t, its gather_layer_tokens
+ * (:232-256).  slot_mapping int64 [T]; a slot outside [0, num_pages *
+ * page_size) is skipped by store and reads as zeros in gather.  A prompt
+ * reaches the pages by solort_prefill_layer into T contiguous rows, then
+ * store.
+ */
+int solort_paged_kv_store(const void* k_rows, const void* v_rows, int64_t row_tok_stride, int64_t row_head_stride,
+                          int T, int nkv, int hd, const int64_t* slot_mapping, void* k_pages, void* v_pages,
+                          int64_t page_stride, int64_t kv_tok_stride, int64_t kv_head_stride, int page_size,
+                          int num_pages, solort_stream_t stream);
+int solort_paged_kv_gather(const void* k_pages, const void* v_pages, int64_t page_stride, int64_t kv_tok_stride,
+                           int64_t kv_head_stride, int page_size, int num_pages, const int64_t* slot_mapping, int T,
+                           int nkv, int hd, void* k_rows, void* v_rows, int64_t row_tok_stride,
+                           int64_t row_head_stride, solort_stream_t stream);
+
+/*
  * Causal grouped-query prefill attention on bf16 MFMA.
  * Replaces cuda_graph_executor.py:124-130: SDPA(q, repeat_interleave(k, g),
  * repeat_interleave(v, g), is_causal=True, scale) over T prompt rows at

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before ours)
 
 LIB_PATH = Path(__file__).resolve().parent / "libsolort_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 # name -> (restype, argtypes); mirrors include/solort_hip.h
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -60,6 +60,16 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p,
          c_void_p, c_int64, c_int64, c_int64, c_int, c_int, c_void_p, c_int, c_int, c_float, c_void_p, c_int,
          c_void_p, c_int, c_void_p],
+    ),
+    "solort_paged_kv_store": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
+         c_int64, c_int, c_int, c_void_p],
+    ),
+    "solort_paged_kv_gather": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int, c_int, c_void_p, c_int, c_int, c_int, c_void_p,
+         c_void_p, c_int64, c_int64, c_void_p],
     ),
     "solort_prefill_layer": (
         c_int,

@@ -26,6 +26,6 @@ int check_launch(const char* what) {
 
 }  // namespace solort
 
-extern "C" int solort_abi_version(void) { return 7; }
+extern "C" int solort_abi_version(void) { return 8; }
 
 extern "C" const char* solort_last_error(void) { return g_err; }

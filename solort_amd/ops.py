@@ -289,6 +289,52 @@ def paged_decode_layer(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor
     _lib.check(rc, "paged_decode_layer")
 
 
+def _paged_arena(kv_pages: torch.Tensor) -> tuple[int, int, int]:
+    _on_gpu("kv_pages", kv_pages, torch.bfloat16)
+    _need(kv_pages.dim() == 5 and kv_pages.shape[1] == 2 and kv_pages.shape[4] == HD and kv_pages.stride(4) == 1,
+          f"kv_pages must be [num_pages, 2, page_size, nkv, {HD}]")
+    return kv_pages.shape[0], kv_pages.shape[2], kv_pages.shape[3]
+
+
+def _slot_rows(k_rows: torch.Tensor, v_rows: torch.Tensor, slot_mapping: torch.Tensor, nkv: int) -> int:
+    for name, t in (("k_rows", k_rows), ("v_rows", v_rows)):
+        _on_gpu(name, t, torch.bfloat16)
+        _need(t.dim() == 3 and t.shape[1] == nkv and t.shape[2] == HD and t.stride(2) == 1,
+              f"{name} must be [T, {nkv}, {HD}] with unit dim stride")
+    _need(v_rows.shape == k_rows.shape and v_rows.stride() == k_rows.stride(), "k_rows and v_rows must match")
+    T = k_rows.shape[0]
+    _need(slot_mapping.is_cuda and slot_mapping.dtype == torch.int64 and slot_mapping.is_contiguous()
+          and slot_mapping.numel() == T, f"slot_mapping must be int64 [{T}] on the device")
+    return T
+
+
+def paged_kv_store(k_rows: torch.Tensor, v_rows: torch.Tensor, slot_mapping: torch.Tensor,
+                   kv_pages: torch.Tensor) -> None:
+    """Rows k_rows/v_rows [T, nkv, 128] -> physical slots slot_mapping [T] of the paged arena kv_pages
+    [num_pages, 2, page_size, nkv, 128] (store_layer_tokens, kv_cache.py:191-230); see
+    solort_paged_kv_store."""
+    num_pages, page_size, nkv = _paged_arena(kv_pages)
+    T = _slot_rows(k_rows, v_rows, slot_mapping, nkv)
+    rc = _lib.load().solort_paged_kv_store(
+        k_rows.data_ptr(), v_rows.data_ptr(), k_rows.stride(0), k_rows.stride(1), T, nkv, HD, slot_mapping.data_ptr(),
+        kv_pages[:, 0].data_ptr(), kv_pages[:, 1].data_ptr(), kv_pages.stride(0), kv_pages.stride(2),
+        kv_pages.stride(3), page_size, num_pages, _stream(kv_pages))
+    _lib.check(rc, "paged_kv_store")
+
+
+def paged_kv_gather(kv_pages: torch.Tensor, slot_mapping: torch.Tensor, k_rows: torch.Tensor,
+                    v_rows: torch.Tensor) -> None:
+    """Physical slots slot_mapping [T] of kv_pages -> rows k_rows/v_rows [T, nkv, 128]
+    (gather_layer_tokens, kv_cache.py:232-256); see solort_paged_kv_gather."""
+    num_pages, page_size, nkv = _paged_arena(kv_pages)
+    T = _slot_rows(k_rows, v_rows, slot_mapping, nkv)
+    rc = _lib.load().solort_paged_kv_gather(
+        kv_pages[:, 0].data_ptr(), kv_pages[:, 1].data_ptr(), kv_pages.stride(0), kv_pages.stride(2),
+        kv_pages.stride(3), page_size, num_pages, slot_mapping.data_ptr(), T, nkv, HD, k_rows.data_ptr(),
+        v_rows.data_ptr(), k_rows.stride(0), k_rows.stride(1), _stream(kv_pages))
+    _lib.check(rc, "paged_kv_gather")
+
+
 def prefill_attn(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, scale: float,
                  out: torch.Tensor) -> None:
     """Causal GQA attention of T prompt rows (q [T, nh, 128]) over cache rows 0..T-1 into

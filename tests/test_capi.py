@@ -153,6 +153,20 @@ def test_paged_decode_rejects_bad_arguments(lib):
     assert lib.solort_paged_decode_layer(*args(pages=0)) == EINVAL
 
 
+def test_paged_kv_copies_reject_bad_arguments(lib):
+    p = ctypes.c_void_p(4096)
+    st = lambda T=4, hd=128, slots=p, ps=16, stride=32768: lib.solort_paged_kv_store(  # noqa: E731
+        p, p, 1024, 128, T, 8, hd, slots, p, p, stride, 1024, 128, ps, 8, None)
+    assert st(hd=64) == EINVAL and "head_dim" in _err(lib)
+    assert st(slots=None) == EINVAL and "null" in _err(lib)
+    assert st(stride=1000) == EINVAL and "page" in _err(lib)
+    assert st(ps=0) == EINVAL
+    assert st(T=0) == 0  # nothing to copy
+    rc = lib.solort_paged_kv_gather(p, p, 32768, 1024, 128, 16, 8, ctypes.c_void_p(4100), 4, 8, 128, p, p, 1024, 128,
+                                    None)
+    assert rc == EINVAL and "aligned" in _err(lib)
+
+
 def test_torch_front_end_refuses_cpu_tensors():
     q = torch.zeros(1, 32, 128, dtype=torch.bfloat16)
     kc = torch.zeros(1024, 8, 128, dtype=torch.bfloat16)

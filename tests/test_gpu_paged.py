@@ -156,3 +156,82 @@ def test_paged_decode_against_reference_ops(gpu):
     assert torch.equal(k_g[case.pos], torch.from_numpy(kx[0]).to(torch.bfloat16))
     assert torch.equal(v_g[case.pos], torch.from_numpy(vx[0]).to(torch.bfloat16))
     assert (k_g[case.pos].float() - kc_r[case.pos].float()).abs().max().item() <= 2 ** -7 * 4
+
+
+def test_paged_kv_store_and_gather_match_reference(gpu):
+    """solort_paged_kv_store / _gather against the oracle's restatement of store_layer_tokens and
+    gather_layer_tokens (kv_cache.py:191-256; pinned on the reference's own test vectors): bit-exact
+    arena after the store, the rows back from the gather, rows of other slots untouched, and slots
+    outside the pool skipped by the store and read as zeros by the gather."""
+    T, nkv, ps, pages = 37, 8, 16, 6
+    g = torch.Generator().manual_seed(90)
+    table = torch.randperm(pages, generator=g)[:3].tolist()
+    slots = ref.slot_mapping(table, list(range(T)), ps)
+    k = torch.randn(T, nkv, HD, generator=g).to(torch.bfloat16)
+    v = torch.randn(T, nkv, HD, generator=g).to(torch.bfloat16)
+    arena = torch.randn(pages, 2, ps, nkv, HD, generator=g).to(torch.bfloat16)
+    want = arena.clone()
+    ref.paged_store(want, slots, k, v)
+    kv = arena.to(gpu)
+    sm = torch.tensor(slots, dtype=torch.long, device=gpu)
+    ops.paged_kv_store(k.to(gpu), v.to(gpu), sm, kv)
+    kg = torch.zeros(T, nkv, HD, dtype=torch.bfloat16, device=gpu)
+    vg = torch.zeros_like(kg)
+    ops.paged_kv_gather(kv, sm, kg, vg)
+    torch.cuda.synchronize()
+    assert torch.equal(kv.cpu(), want)
+    assert torch.equal(kg.cpu(), k) and torch.equal(vg.cpu(), v)
+    bad = torch.tensor([-1, pages * ps, slots[5]], dtype=torch.long, device=gpu)
+    kv2 = kv.clone()
+    ops.paged_kv_store((k[:3] + 1).to(gpu), (v[:3] + 1).to(gpu), bad, kv2)
+    kb, vb = torch.ones(3, nkv, HD, dtype=torch.bfloat16, device=gpu), torch.ones(3, nkv, HD, dtype=torch.bfloat16,
+                                                                                  device=gpu)
+    ops.paged_kv_gather(kv2, bad, kb, vb)
+    torch.cuda.synchronize()
+    changed = (kv2 != kv).reshape(pages, 2, ps, -1).any(-1)
+    assert changed.sum().item() == 2 and changed[slots[5] // ps, :, slots[5] % ps].all()  # only slot[5], K and V
+    assert (kb[:2] == 0).all() and (vb[:2] == 0).all() and torch.equal(kb[2].cpu(), k[2] + 1)
+
+
+def test_paged_prompt_then_decode_equals_contiguous(gpu):
+    """A prompt placed in pages the way the reference's paged path would (solort_prefill_layer into
+    contiguous rows, then solort_paged_kv_store through the sequence's slot mapping) followed by
+    paged decode steps gives the contiguous path's outputs and cache rows bit for bit."""
+    sh = wl.QWEN3_4B
+    T, ps, bound, steps = 300, 16, 512, 3
+    g = torch.Generator().manual_seed(91)
+    ifr = ops.inv_freq(HD, wl.THETA, gpu)
+    qn = (1 + 0.1 * torch.randn(HD, generator=g)).to(torch.bfloat16).to(gpu)
+    kn = (1 + 0.1 * torch.randn(HD, generator=g)).to(torch.bfloat16).to(gpu)
+    qkv = torch.randn(T, sh.qkv_width, generator=g).to(torch.bfloat16).to(gpu)
+    kc = torch.zeros(bound, sh.nkv, HD, dtype=torch.bfloat16, device=gpu)
+    vc = torch.zeros_like(kc)
+    cs = ops.rope_rows(ifr, torch.zeros(1, dtype=torch.long, device=gpu), T)
+    ctx = torch.empty(T, sh.nh * HD, dtype=torch.bfloat16, device=gpu)
+    ops.prefill_layer(qkv, qn, kn, wl.EPS, cs, kc, vc, sh.scale, ctx, sh.nh, sh.nkv)
+    n_log = bound // ps
+    table = torch.randperm(n_log + 4, generator=g)[:n_log].to(torch.int32)
+    kv = torch.zeros(n_log + 4, 2, ps, sh.nkv, HD, dtype=torch.bfloat16, device=gpu)
+    sm = torch.tensor(ref.slot_mapping(table.tolist(), list(range(T)), ps), dtype=torch.long, device=gpu)
+    ops.paged_kv_store(kc[:T], vc[:T], sm, kv)
+    table = table.to(gpu)
+    ns = decode_splits(bound, sh.nkv)
+    ws_a = ops.attn_workspace(1, sh.nh, sh.nkv, ns, gpu)
+    ws_b = ops.attn_workspace(1, sh.nh, sh.nkv, ns, gpu)
+    for i in range(steps):
+        pos = torch.tensor([T + i], dtype=torch.long, device=gpu)
+        q1 = torch.randn(1, sh.qkv_width, generator=g).to(torch.bfloat16).to(gpu)
+        c1 = ops.rope_rows(ifr, pos, 1)
+        out_a = torch.empty(1, sh.nh * HD, dtype=torch.float32, device=gpu)
+        out_b = torch.empty_like(out_a)
+        ops.decode_layer(q1, qn, kn, wl.EPS, c1, pos, kc, vc, bound, sh.scale, ws_a, ns, out_a, sh.nh, sh.nkv)
+        ops.paged_decode_layer(q1, qn, kn, wl.EPS, c1, pos, kv, table, bound, sh.scale, ws_b, ns, out_b, sh.nh, sh.nkv)
+        torch.cuda.synchronize()
+        assert torch.equal(out_a, out_b), i
+    sm_all = torch.tensor(ref.slot_mapping(table.cpu().tolist(), list(range(T + steps)), ps), dtype=torch.long,
+                          device=gpu)
+    kg = torch.empty(T + steps, sh.nkv, HD, dtype=torch.bfloat16, device=gpu)
+    vg = torch.empty_like(kg)
+    ops.paged_kv_gather(kv, sm_all, kg, vg)
+    torch.cuda.synchronize()
+    assert torch.equal(kg, kc[:T + steps]) and torch.equal(vg, vc[:T + steps])
