@@ -54,12 +54,14 @@ def parse() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-sweep", action="store_true", help="skip the per-bucket decode extras")
-    p.add_argument("--only", choices=("all", "decode", "prefill", "long", "verify", "gemv", "model", "paged"),
+    p.add_argument("--only", choices=("all", "decode", "prefill", "long", "verify", "gemv", "model", "paged",
+                                      "torchref"),
                    default="all",
                    help="decode: the decode step and its kernel only; prefill: the prefill kernels only; "
                         "long: the Qwen3-8B KV 32768 decode only; verify: the speculative verify and argmax "
                         "only; gemv: the decode-step GEMVs only; model: whole-model greedy decode only; paged: the "
-                        "paged-KV decode only (for per-workload profiles)")
+                        "paged-KV decode only; torchref: the reference's torch decode ops on this GPU only (for "
+                        "per-workload profiles)")
     return p.parse_args()
 
 
@@ -112,6 +114,10 @@ def main() -> int:
         return 0
     if args.only == "gemv":
         print(json.dumps({"decode_gemv": gemv_extras(torch, ops, dev)}), flush=True)
+        return 0
+    if args.only == "torchref":
+        print(json.dumps({"torch_reference_decode": torch_reference_extras(torch, runners, dev, sh, bound)}),
+              flush=True)
         return 0
     if args.only == "paged":
         print(json.dumps({"paged_decode_kv1024": paged_extras(torch, ops, runners, dev, sh)}), flush=True)
@@ -177,6 +183,7 @@ def main() -> int:
         result["extras"]["decode_8b_kv32768"] = long_decode_extras(torch, ops, wl, dev)
         result["extras"]["decode_gemv"] = gemv_extras(torch, ops, dev)
         result["extras"]["paged_decode_kv1024"] = paged_extras(torch, ops, runners, dev, sh)
+        result["extras"]["torch_reference_decode"] = torch_reference_extras(torch, runners, dev, sh, bound)
         result["extras"]["decode_model"] = model_extras(torch, dev)
     if args.only == "all":
         result["prefill"] = prefill_extras(torch, ops, runners, dev, sh)
@@ -560,6 +567,75 @@ def prefill_extras(torch, ops, runners, dev, sh) -> dict:
                        "frac_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4),
                        "step_us_per_layer": round(step_us, 3), "flop": fl}
     return out
+
+
+def torch_reference_extras(torch, runners, dev, sh, bound: int) -> dict:
+    """The reference's own decode-attention ops (cuda_graph_executor.py:164, :168, :173-184) as torch
+    kernels on this GPU, for context: per layer the q/k split, two per-head RMSNorms (:25-28), two
+    RoPEs (:100-102), the two KV index_copy_ writes, the grouped score matmul, scale, mask, softmax
+    and the P V matmul, in bf16.  The transposed K^T and the permuted V views are made contiguous
+    before their batched products (batched bf16 products on transposed views are unsafe on this
+    device); that adds two copies per layer.  One graph per KV set replays the 36 layers, rotated
+    over the sets, HIP events around the replays."""
+    F = torch.nn.functional
+    nh, nkv, hd, g = sh.nh, sh.nkv, 128, sh.nh // sh.nkv
+    eps, scale = 1e-6, 128 ** -0.5
+
+    def rmsnorm(x, w):
+        xf = x.float()
+        return ((xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps)) * w.float()).to(x.dtype)
+
+    def rope(x, cos, sin):
+        d = x.shape[-1] // 2
+        return x * cos + torch.cat([-x[..., d:], x[..., :d]], -1) * sin
+
+    arange = torch.arange(bound, device=dev)
+    graphs = []
+    for r in runners:
+        pos_buf = r.pos_buf
+        inv = r.inv_freq
+
+        def step(r=r, pos_buf=pos_buf, inv=inv):
+            freqs = pos_buf.float().view(-1, 1) * inv.view(1, -1)                     # :95-98
+            emb = torch.cat([freqs, freqs], -1)
+            cos, sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+            nkeep = (arange > pos_buf).view(1, 1, bound)                              # :168
+            for li in range(sh.layers):
+                q, k, v = r.qkv_dec[li].split([nh * hd, nkv * hd, nkv * hd], dim=-1)  # :173-175
+                q = q.view(1, nh, hd).transpose(0, 1)
+                k = k.view(1, nkv, hd).transpose(0, 1)
+                v = v.view(1, nkv, hd).transpose(0, 1)
+                q = rope(rmsnorm(q, r.qn_w[li]), cos, sin)                             # :176-177
+                k = rope(rmsnorm(k, r.kn_w[li]), cos, sin)
+                r.kc[li].index_copy_(0, pos_buf, k.transpose(0, 1))                   # :178-179
+                r.vc[li].index_copy_(0, pos_buf, v.transpose(0, 1))
+                qg = q.reshape(nkv, g, hd)                                            # :180-184
+                kt = r.kc[li, :bound].permute(1, 2, 0).contiguous()
+                vb = r.vc[li, :bound].permute(1, 0, 2).contiguous()
+                sc = (torch.matmul(qg, kt) * scale).masked_fill(nkeep, float("-inf"))
+                torch.matmul(torch.softmax(sc, -1).to(torch.bfloat16), vb).reshape(1, nh * hd)
+
+        for _ in range(2):
+            step()  # eager first: the BLAS initialises outside the capture
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step()
+        graphs.append(graph)
+    stream = torch.cuda.current_stream(dev)
+    for gr in graphs:
+        gr.replay()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 3
+    e0.record(stream)
+    for _ in range(reps):
+        for gr in graphs:
+            gr.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / (reps * len(graphs) * sh.layers)
+    return {"us_per_layer": round(us, 3), "bound": bound,
+            "note": "reference decode-attention torch ops on this GPU, graphed; K^T and V made contiguous"}
 
 
 def cpu_baseline(budget_s: float, live: int) -> dict:
