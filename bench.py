@@ -423,6 +423,14 @@ def model_extras(torch, dev, live: int = 960, n: int = 48) -> dict:
             out["separate_tail"] = r
         del m, g
         torch.cuda.empty_cache()
+    kc = torch.zeros(s.layers, 1024, s.nkv, 128, dtype=torch.bfloat16, device=dev)
+    vc = torch.zeros_like(kc)
+    kc[:, :live].copy_(ctx_k)
+    vc[:, :live].copy_(ctx_v)
+    ref_ms = torch_reference_model_ms(torch, w, kc, vc, live, n)
+    out["torch_reference"] = {"ms_per_token": round(ref_ms, 4), "tokens_per_s": round(1e3 / ref_ms, 1),
+                              "note": "the reference's decode step as torch ops on this GPU, graphed; K^T and V "
+                                      "made contiguous for the batched attention products"}
     return out
 
 
@@ -569,6 +577,76 @@ def prefill_extras(torch, ops, runners, dev, sh) -> dict:
     return out
 
 
+def _ref_rmsnorm(x, w, eps: float = 1e-6):
+    """cuda_graph_executor.py:25-28 (torch ops)."""
+    xf = x.float()
+    return ((xf * xf.square().mean(-1, keepdim=True).add(eps).rsqrt()) * w.float()).to(x.dtype)
+
+
+def _ref_rope(x, cos, sin):
+    """cuda_graph_executor.py:100-102 (torch ops)."""
+    import torch
+    d = x.shape[-1] // 2
+    return x * cos + torch.cat([-x[..., d:], x[..., :d]], -1) * sin
+
+
+def torch_reference_model_ms(torch, w, kc, vc, live: int, n: int, bound: int = 1024) -> float:
+    """The reference's whole greedy decode step (cuda_graph_executor.py:163-206: embedding, per layer
+    input norm, QKV product, q/k norm + RoPE, KV write, grouped attention, o_proj, post norm,
+    gate/up, SiLU, down; final norm, lm_head, argmax into the token buffer) as torch ops on this GPU,
+    graphed as the reference's _capture does, over the given weights and caches.  The batched
+    attention products get contiguous K^T and V (batched bf16 products on transposed views are
+    unsafe on this device).  Returns ms per token over n replays from position `live`."""
+    F = torch.nn.functional
+    s = w.shape
+    nh, nkv, hd, g = s.nh, s.nkv, 128, s.nh // s.nkv
+    dev = kc.device
+    tok_buf = torch.tensor([11], dtype=torch.long, device=dev)
+    pos_buf = torch.tensor([live], dtype=torch.long, device=dev)
+    inv = 1.0 / (1e6 ** (torch.arange(0, hd, 2, device=dev).float() / hd))
+    arange = torch.arange(bound, device=dev)
+
+    def step():
+        freqs = pos_buf.float().view(-1, 1) * inv.view(1, -1)
+        emb = torch.cat([freqs, freqs], -1)
+        cos, sin = emb.cos().to(torch.bfloat16), emb.sin().to(torch.bfloat16)
+        x = w.embed[tok_buf]
+        nkeep = (arange > pos_buf).view(1, 1, bound)
+        for li in range(s.layers):
+            qkv = _ref_rmsnorm(x, w.in_ln[li]) @ w.wqkv[li].T
+            q, k, v = qkv.split([nh * hd, nkv * hd, nkv * hd], dim=-1)
+            q = _ref_rope(_ref_rmsnorm(q.view(1, nh, hd).transpose(0, 1), w.qn[li]), cos, sin)
+            k = _ref_rope(_ref_rmsnorm(k.view(1, nkv, hd).transpose(0, 1), w.kn[li]), cos, sin)
+            kc[li].index_copy_(0, pos_buf, k.transpose(0, 1))
+            vc[li].index_copy_(0, pos_buf, v.view(1, nkv, hd))
+            kt = kc[li, :bound].permute(1, 2, 0).contiguous()
+            vb = vc[li, :bound].permute(1, 0, 2).contiguous()
+            sc = (torch.matmul(q.reshape(nkv, g, hd), kt) * hd ** -0.5).masked_fill(nkeep, float("-inf"))
+            ctx = torch.matmul(torch.softmax(sc, -1).to(torch.bfloat16), vb).reshape(1, nh * hd)
+            x = x + ctx @ w.wo[li].T
+            gate, up = (_ref_rmsnorm(x, w.post_ln[li]) @ w.wgu[li].T).split([s.inter, s.inter], dim=-1)
+            x = x + (F.silu(gate) * up) @ w.wd[li].T
+        lg = (_ref_rmsnorm(x, w.final_norm) @ w.lm_head.T).float()
+        tok_buf.copy_(lg.argmax(-1))
+        pos_buf.add_(1)
+
+    for _ in range(2):
+        step()  # eager first: the BLAS initialises outside the capture
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        step()
+    pos_buf.fill_(live)
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(stream)
+    for _ in range(n):
+        graph.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / n
+
+
 def torch_reference_extras(torch, runners, dev, sh, bound: int) -> dict:
     """The reference's own decode-attention ops (cuda_graph_executor.py:164, :168, :173-184) as torch
     kernels on this GPU, for context: per layer the q/k split, two per-head RMSNorms (:25-28), two
@@ -577,17 +655,9 @@ def torch_reference_extras(torch, runners, dev, sh, bound: int) -> dict:
     before their batched products (batched bf16 products on transposed views are unsafe on this
     device); that adds two copies per layer.  One graph per KV set replays the 36 layers, rotated
     over the sets, HIP events around the replays."""
-    F = torch.nn.functional
     nh, nkv, hd, g = sh.nh, sh.nkv, 128, sh.nh // sh.nkv
-    eps, scale = 1e-6, 128 ** -0.5
-
-    def rmsnorm(x, w):
-        xf = x.float()
-        return ((xf * torch.rsqrt(xf.square().mean(-1, keepdim=True) + eps)) * w.float()).to(x.dtype)
-
-    def rope(x, cos, sin):
-        d = x.shape[-1] // 2
-        return x * cos + torch.cat([-x[..., d:], x[..., :d]], -1) * sin
+    scale = 128 ** -0.5
+    rmsnorm, rope = _ref_rmsnorm, _ref_rope
 
     arange = torch.arange(bound, device=dev)
     graphs = []
