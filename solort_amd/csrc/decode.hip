@@ -137,7 +137,8 @@ __global__ __launch_bounds__(256) void decode_lanes_kernel(uint16_t* kc, uint16_
   __shared__ __align__(16) float s_s[R * KPI];       // its masked scores [row][key] (log2 units), then p
 
   const int tid = threadIdx.x, j = tid & 15, slot = tid >> 4, wave = tid >> 6, lane = tid & 63;
-  const int kvh = blockIdx.x, split = blockIdx.y, nkv = gridDim.x, NS = gridDim.y;
+  const int kvh = blockIdx.x, split = blockIdx.y, NS = gridDim.y;
+  const int nkv = nh / G;  // = gridDim.x, without the hidden-argument load
   const int kbeg = min(split * chunk, bound);
   const int kstat = min(kbeg + chunk, bound);
 
@@ -435,7 +436,8 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint1
 
   const int tid = threadIdx.x, j = tid & 15, slot = tid >> 4, wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, hi = lane >> 5;
-  const int kvh = blockIdx.x, split = blockIdx.y, nkv = gridDim.x, NS = gridDim.y;
+  const int kvh = blockIdx.x, split = blockIdx.y, NS = gridDim.y;
+  const int nkv = nh / G;  // = gridDim.x, without the hidden-argument load
   const int kbeg = min(split * chunk, bound);
   const int kstat = min(kbeg + chunk, bound);
   const int kclamp = kstat > kbeg ? kstat - 1 : (kbeg > 0 ? kbeg - 1 : 0);  // a row this split may read

@@ -45,12 +45,15 @@ __device__ __forceinline__ float wave_sum64(float v) {
 // rounded to bf16 as F.silu on a bf16 tensor.
 __device__ __forceinline__ float silu_bf16(float g) { return rbf(g / (1.0f + __expf(-g))); }
 
+// The arguments the first loads need lead (w .. norm_w: 13 dwords), so they
+// arrive preloaded in SGPRs and the weight stream starts without waiting for
+// the kernel-argument fetch.
 template <int R, int U, int EPI, bool NORM>
 __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ w, int64_t w_stride, int n_out,
-                                                   int K, const uint16_t* __restrict__ x,
+                                                   int K, int64_t inter, const uint16_t* __restrict__ x,
                                                    const uint16_t* __restrict__ norm_w, float eps,
-                                                   const uint16_t* res, int64_t inter, uint16_t* out,
-                                                   uint64_t* arg_ws, int64_t* arg_idx) {
+                                                   const uint16_t* res, uint16_t* out, uint64_t* arg_ws,
+                                                   int64_t* arg_idx) {
   extern __shared__ uint4 sx[];  // x as K / 8 chunks of 16 bytes
   __shared__ float s_red[4];
   __shared__ uint64_t s_key[4];
@@ -314,8 +317,8 @@ int launch_gemv(const char* name, const void* w, int64_t w_row_stride, int n_out
   const int U = (R == 4 || cpl % 5 == 0 || cpl < 5) ? 5 : (R == 1 && cpl > 8 && cpl <= 20 ? 20 : 8);
 #define SOLORT_GEMV_U(RR, UU, EE, NN)                                                                         \
   hipLaunchKernelGGL((gemv_kernel<RR, UU, EE, NN>), dim3((unsigned)blocks), dim3(256), lds, s,               \
-                     (const uint16_t*)w, w_row_stride, n_out, k, (const uint16_t*)x, (const uint16_t*)norm_w,   \
-                     eps, (const uint16_t*)res, inter, (uint16_t*)out, arg_ws, arg_idx)
+                     (const uint16_t*)w, w_row_stride, n_out, k, inter, (const uint16_t*)x,                    \
+                     (const uint16_t*)norm_w, eps, (const uint16_t*)res, (uint16_t*)out, arg_ws, arg_idx)
 #define SOLORT_GEMV(RR, EE, NN)                              \
   do {                                                       \
     if (U == 5) SOLORT_GEMV_U(RR, 5, EE, NN);                \

@@ -19,28 +19,50 @@
 
 namespace solort {
 
+// rope_src: TABLE, the step's cos/sin rows rope_cs [2][T][64] bf16; else
+// inv_freq [64] fp32.  The arguments the first loads need lead (qkv ..
+// rope_src: 14 dwords), so they arrive preloaded in SGPRs.
 template <bool TABLE>
 __global__ __launch_bounds__(256) void qknorm_rope_kvwrite_kernel(
-    const uint16_t* __restrict__ qkv, int64_t qkv_stride, int T, int nh, int nkv,
-    const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w, float eps,
-    const float* __restrict__ inv_freq, const uint16_t* __restrict__ rope_cs, int64_t pos_limit,
-    const int64_t* __restrict__ pos0_dev, uint16_t* __restrict__ q_out, uint16_t* __restrict__ kc,
-    uint16_t* __restrict__ vc, int64_t tok_stride, int64_t head_stride, int row0) {
+    const uint16_t* __restrict__ qkv, int64_t qkv_stride, int T, int nh, int nkv, int row0,
+    const uint16_t* __restrict__ qn_w, const uint16_t* __restrict__ kn_w, const void* __restrict__ rope_src,
+    float eps, int64_t pos_limit, const int64_t* __restrict__ pos0_dev, uint16_t* __restrict__ q_out,
+    uint16_t* __restrict__ kc, uint16_t* __restrict__ vc, int64_t tok_stride, int64_t head_stride) {
   // Block = one token; the 16 slots of 16 lanes take its head rows row0 ..
   // (row0 = nh: the K and V rows only, q_out unused).
   const int tid = threadIdx.x, j = tid & 15, slot = tid >> 4;
   const int t = blockIdx.x;
   const int heads = nh + 2 * nkv;
+  // This slot's rows hs = slot + 16 p, all loaded before any is computed (a
+  // load issued after the previous row's math would add a memory latency per
+  // row); past the last row the loads re-read it and are not used.  These
+  // loads (and, TABLE, the cos/sin rows) need only preloaded arguments and go
+  // out before the position, which the writes need, is read.
+  constexpr int kMaxPass = 6;  // heads <= 96
+  uint4 cs_raw{}, sn_raw{};
+  if constexpr (TABLE) {  // rope_cs [2][T][64]: this lane's 8 cos then sin values of row t
+    const uint16_t* rope_cs = reinterpret_cast<const uint16_t*>(rope_src);
+    cs_raw = *reinterpret_cast<const uint4*>(rope_cs + (int64_t)t * 64 + (j & 7) * 8);
+    sn_raw = *reinterpret_cast<const uint4*>(rope_cs + ((int64_t)T + t) * 64 + (j & 7) * 8);
+  }
+  const uint4 wq = *reinterpret_cast<const uint4*>(qn_w + j * 8), wk = *reinterpret_cast<const uint4*>(kn_w + j * 8);
+  uint4 raws[kMaxPass];
+#pragma unroll
+  for (int p = 0; p < kMaxPass; ++p)
+    raws[p] = *reinterpret_cast<const uint4*>(qkv + (int64_t)t * qkv_stride +
+                                              min(row0 + slot + 16 * p, heads - 1) * SOLORT_HD + j * 8);
+  __builtin_amdgcn_sched_barrier(0);
+
   const int64_t pos = (pos0_dev ? pos0_dev[0] : 0) + t;
   const bool pos_ok = pos >= 0 && pos < pos_limit;
   float c[8], s[8];
-  if constexpr (TABLE) {  // rope_cs [2][T][64]: this lane's 8 cos then sin values of row t
-    unpack8(*reinterpret_cast<const uint4*>(rope_cs + (int64_t)t * 64 + (j & 7) * 8), c);
-    unpack8(*reinterpret_cast<const uint4*>(rope_cs + ((int64_t)T + t) * 64 + (j & 7) * 8), s);
+  if constexpr (TABLE) {
+    unpack8(cs_raw, c);
+    unpack8(sn_raw, s);
   } else {  // the token's 128 cos/sin values, one per thread, through LDS
     __shared__ float s_cs[64], s_sn[64];
     if (tid < 128) {
-      const float ang = rope_angle(pos, inv_freq[tid >> 1]);
+      const float ang = rope_angle(pos, reinterpret_cast<const float*>(rope_src)[tid >> 1]);
       if (tid & 1) s_sn[tid >> 1] = rope_sin(ang);
       else s_cs[tid >> 1] = rope_cos(ang);
     }
@@ -51,16 +73,6 @@ __global__ __launch_bounds__(256) void qknorm_rope_kvwrite_kernel(
       s[i] = s_sn[(j & 7) * 8 + i];
     }
   }
-  // This slot's rows hs = slot + 16 p, all loaded before any is computed (a
-  // load issued after the previous row's math would add a memory latency per
-  // row); past the last row the loads re-read it and are not used.
-  constexpr int kMaxPass = 6;  // heads <= 96
-  const uint4 wq = *reinterpret_cast<const uint4*>(qn_w + j * 8), wk = *reinterpret_cast<const uint4*>(kn_w + j * 8);
-  uint4 raws[kMaxPass];
-#pragma unroll
-  for (int p = 0; p < kMaxPass; ++p)
-    raws[p] = *reinterpret_cast<const uint4*>(qkv + (int64_t)t * qkv_stride +
-                                              min(row0 + slot + 16 * p, heads - 1) * SOLORT_HD + j * 8);
 #pragma unroll
   for (int p = 0; p < kMaxPass; ++p) {  // whole 16-lane groups take a row
     const int hs = row0 + slot + 16 * p;
@@ -115,9 +127,9 @@ extern "C" int solort_qknorm_rope_kvwrite(const void* qkv, int64_t qkv_row_strid
                           k_cache, v_cache, kv_tok_stride, kv_head_stride, max_len);
   if (rc || T == 0) return rc;
   hipLaunchKernelGGL(qknorm_rope_kvwrite_kernel<false>, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)qkv, qkv_row_stride, T, nh, nkv, (const uint16_t*)qn_w,
-                     (const uint16_t*)kn_w, eps, inv_freq, (const uint16_t*)nullptr, max_len, pos0_dev,
-                     (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, kv_tok_stride, kv_head_stride, 0);
+                     (const uint16_t*)qkv, qkv_row_stride, T, nh, nkv, 0, (const uint16_t*)qn_w,
+                     (const uint16_t*)kn_w, (const void*)inv_freq, eps, max_len, pos0_dev, (uint16_t*)q_out,
+                     (uint16_t*)k_cache, (uint16_t*)v_cache, kv_tok_stride, kv_head_stride);
   return check_launch("qknorm_rope_kvwrite");
 }
 
@@ -130,9 +142,9 @@ extern "C" int solort_qknorm_rope_kvwrite_cs(const void* qkv, int64_t qkv_row_st
                           q_out, k_cache, v_cache, kv_tok_stride, kv_head_stride, max_len);
   if (rc || T == 0) return rc;
   hipLaunchKernelGGL(qknorm_rope_kvwrite_kernel<true>, dim3((unsigned)T), dim3(256), 0, (hipStream_t)stream,
-                     (const uint16_t*)qkv, qkv_row_stride, T, nh, nkv, (const uint16_t*)qn_w,
-                     (const uint16_t*)kn_w, eps, (const float*)nullptr, (const uint16_t*)rope_cs, max_len, pos0_dev,
-                     (uint16_t*)q_out, (uint16_t*)k_cache, (uint16_t*)v_cache, kv_tok_stride, kv_head_stride, 0);
+                     (const uint16_t*)qkv, qkv_row_stride, T, nh, nkv, 0, (const uint16_t*)qn_w,
+                     (const uint16_t*)kn_w, rope_cs, eps, max_len, pos0_dev, (uint16_t*)q_out, (uint16_t*)k_cache,
+                     (uint16_t*)v_cache, kv_tok_stride, kv_head_stride);
   return check_launch("qknorm_rope_kvwrite_cs");
 }
 
@@ -143,8 +155,8 @@ int solort::launch_kv_rows_cs(const void* qkv, int64_t qkv_row_stride, int T, in
                               float eps, const void* rope_cs, void* k_cache, void* v_cache, int64_t kv_tok_stride,
                               int64_t kv_head_stride, int64_t max_len, hipStream_t stream) {
   hipLaunchKernelGGL(qknorm_rope_kvwrite_kernel<true>, dim3((unsigned)T), dim3(256), 0, stream, (const uint16_t*)qkv,
-                     qkv_row_stride, T, nh, nkv, (const uint16_t*)kn_w, (const uint16_t*)kn_w, eps,
-                     (const float*)nullptr, (const uint16_t*)rope_cs, max_len, (const int64_t*)nullptr,
-                     (uint16_t*)nullptr, (uint16_t*)k_cache, (uint16_t*)v_cache, kv_tok_stride, kv_head_stride, nh);
+                     qkv_row_stride, T, nh, nkv, nh, (const uint16_t*)kn_w, (const uint16_t*)kn_w, rope_cs, eps,
+                     max_len, (const int64_t*)nullptr, (uint16_t*)nullptr, (uint16_t*)k_cache, (uint16_t*)v_cache,
+                     kv_tok_stride, kv_head_stride);
   return check_launch("prefill_layer (K/V rows)");
 }
