@@ -29,8 +29,8 @@ HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
 # HBM bytes per launch of the decode split kernel at KV 1024 (decode_lanes_kernel<1,4,2,true>),
 # from rocprofv3 --pmc FETCH_SIZE (x1.999: a 64 MiB copy reads 32786 KiB on it) plus
-# WRITE_SIZE (x1.000): (2102.5 * 1.999 + 524.0) KiB.  Re-measured whenever that kernel changes.
-DECODE_KERNEL_TRAFFIC = int((2102.5 * 1.999 + 524.0) * 1024)
+# WRITE_SIZE (x1.000): (2103.0 * 1.999 + 524.0) KiB.  Re-measured whenever that kernel changes.
+DECODE_KERNEL_TRAFFIC = int((2103.0 * 1.999 + 524.0) * 1024)
 
 
 def decode_bytes(live: int, nh: int = 32, nkv: int = 8, hd: int = 128) -> int:
