@@ -28,7 +28,10 @@
 //     8j..8j+7); the query group sits in registers as bf16 pairs, a score is
 //     four bf16 pair dot products reduced over the slot with DPP, and scores
 //     and V rows go through LDS so that each wavefront accumulates its own
-//     query row (two output dims per lane).
+//     query row (two output dims per lane).  For the fused layer on a
+//     contiguous cache whose strides fit 16 bits (in 16-byte units), the same
+//     body runs as decode_lanes_packed_kernel, whose packed arguments keep
+//     every pointer the first loads need among the preloaded dwords.
 //   - decode_mfma_kernel, for long chunks and several new tokens: each
 //     wavefront takes 32-key tiles (kbeg + 32w + 128i), stages K and V
 //     through its LDS tile with whole-row loads, and computes S^T = K q^T and
@@ -125,9 +128,10 @@ __device__ __forceinline__ void store_out2(void* out, int out_f32, int nh, int k
 // fused, the qkv rows (row stride qsrc_stride); unfused, the q rows
 // [nq][nh][128] (qsrc_stride = nh*128).
 template <int NQ, int G, int U, bool FUSED, bool PAGED>
-__global__ __launch_bounds__(256) void decode_lanes_kernel(uint16_t* kc, uint16_t* vc, int tok_stride, int head_stride,
-                                                     int chunk, int bound, const uint16_t* qsrc, int qsrc_stride,
-                                                     int nh, const uint16_t* qn_w, const DecodeTail a) {
+__device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, int tok_stride, int head_stride,
+                                                  int chunk, int bound, const uint16_t* qsrc, int qsrc_stride,
+                                                  int nh, const uint16_t* qn_w, const uint16_t* kn_w,
+                                                  const uint16_t* rope_cs, const DecodeTail& a) {
   constexpr int R = NQ * G;            // query rows sharing one KV head
   constexpr int KPI = 16 * U;          // keys per iteration (16 slots x U)
   constexpr int RPW = (R + 3) / 4;     // output rows per wavefront
@@ -157,9 +161,9 @@ __global__ __launch_bounds__(256) void decode_lanes_kernel(uint16_t* kc, uint16_
       const int hs = c < G ? kvh * G + c : (c == G ? nh + kvh : nh + nkv + kvh);
       raw0 = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + hs * SOLORT_HD + j * 8);
       wq0 = *reinterpret_cast<const uint4*>(qn_w + j * 8);
-      wk0 = *reinterpret_cast<const uint4*>(a.kn_w + j * 8);
-      c0 = *reinterpret_cast<const uint4*>(a.rope_cs + t * 64 + (j & 7) * 8);
-      s0 = *reinterpret_cast<const uint4*>(a.rope_cs + (NQ + t) * 64 + (j & 7) * 8);
+      wk0 = *reinterpret_cast<const uint4*>(kn_w + j * 8);
+      c0 = *reinterpret_cast<const uint4*>(rope_cs + t * 64 + (j & 7) * 8);
+      s0 = *reinterpret_cast<const uint4*>(rope_cs + (NQ + t) * 64 + (j & 7) * 8);
     } else {
       const int t = row / G, g = row % G;
       raw0 = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + (kvh * G + g) * SOLORT_HD + j * 8);
@@ -181,6 +185,7 @@ __global__ __launch_bounds__(256) void decode_lanes_kernel(uint16_t* kc, uint16_
     kr[u] = *reinterpret_cast<const uint4*>(kp + off);
     vr[u] = *reinterpret_cast<const uint4*>(vp + off);
   }
+  __builtin_amdgcn_sched_barrier(0);  // every K/V load issues before the position is read
 
   const int64_t pos0 = a.pos0_dev[0];
 
@@ -195,8 +200,8 @@ __global__ __launch_bounds__(256) void decode_lanes_kernel(uint16_t* kc, uint16_
       if (row != slot) {  // rows past the first (verify): loaded here
         const int hs = c < G ? kvh * G + c : (c == G ? nh + kvh : nh + nkv + kvh);
         raw = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + hs * SOLORT_HD + j * 8);
-        c8 = *reinterpret_cast<const uint4*>(a.rope_cs + t * 64 + (j & 7) * 8);
-        s8 = *reinterpret_cast<const uint4*>(a.rope_cs + (NQ + t) * 64 + (j & 7) * 8);
+        c8 = *reinterpret_cast<const uint4*>(rope_cs + t * 64 + (j & 7) * 8);
+        s8 = *reinterpret_cast<const uint4*>(rope_cs + (NQ + t) * 64 + (j & 7) * 8);
       }
       if (c == G + 1) {  // V row: raw
         s_new[(NQ + t) * 16 + j] = raw;
@@ -364,6 +369,32 @@ __global__ __launch_bounds__(256) void decode_lanes_kernel(uint16_t* kc, uint16_
       if (lane == 0) *reinterpret_cast<float2*>(a.ws_ml + pr * 2) = make_float2(M[i], Ls);
     }
   }
+}
+
+// Arguments as the entry points pass them: the leading 14 dwords arrive
+// preloaded in SGPRs; kn_w and rope_cs travel in the tail.
+template <int NQ, int G, int U, bool FUSED, bool PAGED>
+__global__ __launch_bounds__(256) void decode_lanes_kernel(uint16_t* kc, uint16_t* vc, int tok_stride, int head_stride,
+                                                     int chunk, int bound, const uint16_t* qsrc, int qsrc_stride,
+                                                     int nh, const uint16_t* qn_w, const DecodeTail a) {
+  decode_lanes_body<NQ, G, U, FUSED, PAGED>(kc, vc, tok_stride, head_stride, chunk, bound, qsrc, qsrc_stride, nh,
+                                            qn_w, a.kn_w, a.rope_cs, a);
+}
+
+// One new token, fused, contiguous cache: every pointer the first loads need
+// fits the 14 preloaded dwords, so no load waits for the kernel-argument
+// fetch.  strides8 = tok_stride / 8 | (head_stride / 8) << 16; geom =
+// (chunk / 16 - 1) | nh << 2 | bound << 13 (chunk <= 64, nh < 2048, bound <
+// 2^19).  The qkv row stride is not needed for one token.
+template <int G, int U>
+__global__ __launch_bounds__(256) void decode_lanes_packed_kernel(uint16_t* kc, uint16_t* vc, unsigned strides8,
+                                                            unsigned geom, const uint16_t* qkv,
+                                                            const uint16_t* qn_w, const uint16_t* kn_w,
+                                                            const uint16_t* rope_cs, const DecodeTail a) {
+  const int tok_stride = (int)(strides8 & 0xffffu) * 8, head_stride = (int)(strides8 >> 16) * 8;
+  const int chunk = ((int)(geom & 3u) + 1) * 16, nh = (int)((geom >> 2) & 2047u), bound = (int)(geom >> 13);
+  decode_lanes_body<1, G, U, true, false>(kc, vc, tok_stride, head_stride, chunk, bound, qkv, 0, nh, qn_w, kn_w,
+                                          rope_cs, a);
 }
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -839,6 +870,20 @@ static bool launch_split_p(const DecodeArgs& a, hipStream_t s) {
   if constexpr (NQ * G <= kMaxRows) {
     const dim3 grid(a.nkv, a.n_split);
     if constexpr (NQ == 1 && G <= kLanesMaxGroup) {
+      if constexpr (FUSED && !PAGED) {
+        // The packed-argument kernel when the layout fits its fields.
+        if (a.lanes && a.tok_stride < (1 << 19) && a.head_stride < (1 << 19) && a.nh < 2048 && a.bound < (1 << 19)) {
+          const unsigned strides8 = (unsigned)(a.tok_stride / 8) | (unsigned)(a.head_stride / 8) << 16;
+          const unsigned geom = (unsigned)(a.chunk / 16 - 1) | (unsigned)a.nh << 2 | (unsigned)a.bound << 13;
+          if (a.U == 4)
+            hipLaunchKernelGGL((decode_lanes_packed_kernel<G, 4>), grid, dim3(256), 0, s, a.kc, a.vc, strides8, geom,
+                               a.qsrc, a.qn_w, a.tail.kn_w, a.tail.rope_cs, a.tail);
+          else
+            hipLaunchKernelGGL((decode_lanes_packed_kernel<G, 2>), grid, dim3(256), 0, s, a.kc, a.vc, strides8, geom,
+                               a.qsrc, a.qn_w, a.tail.kn_w, a.tail.rope_cs, a.tail);
+          return true;
+        }
+      }
       if (a.lanes) {
         if (a.U == 4)
           hipLaunchKernelGGL((decode_lanes_kernel<NQ, G, 4, FUSED, PAGED>), grid, dim3(256), 0, s, a.kc, a.vc,

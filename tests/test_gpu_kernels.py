@@ -355,6 +355,42 @@ def test_decode_layer_repeated_calls_reuse_workspace(gpu):
         assert torch.equal(outs[i], outs[i - 4])
 
 
+@pytest.mark.parametrize("live,n_split", [(1024, 32), (256, 8)])
+def test_decode_layer_head_major_cache_equals_token_major(gpu, live, n_split):
+    """A head-major cache ([nkv][8192][128] storage: head stride 2^20 elements, past the 16-bit
+    stride fields of the packed-argument kernel, so the launch takes the general one) gives the
+    same KV bits and output bits as the token-major [max_len][nkv][128] cache."""
+    case = wl.decode_case(1, live=live, layers=1)
+    dev = gpu
+    sh = case.shape
+    _say(f"[head-major {sh.name} pos={case.pos} bound={case.bound} n_split={n_split}]")
+    ifr = _ifr(dev)
+    pos = torch.tensor([case.pos], dtype=torch.long, device=dev)
+    qkv = case.qkv[0].to(dev)
+    qn, kn = case.qn_w[0].to(dev), case.kn_w[0].to(dev)
+    kc_t, vc_t = case.kc[0].to(dev), case.vc[0].to(dev)
+    rows = 8192
+    k_store = torch.zeros(sh.nkv, rows, HD, dtype=torch.bfloat16, device=dev)
+    v_store = torch.zeros_like(k_store)
+    k_store[:, :case.max_len] = kc_t.permute(1, 0, 2)
+    v_store[:, :case.max_len] = vc_t.permute(1, 0, 2)
+    kc_h = k_store[:, :case.max_len].permute(1, 0, 2)
+    vc_h = v_store[:, :case.max_len].permute(1, 0, 2)
+    assert kc_h.stride() == (HD, rows * HD, 1)
+    ws = ops.attn_workspace(1, sh.nh, sh.nkv, n_split, dev)
+    cs = ops.rope_rows(ifr, pos, 1)
+    for dt in (torch.bfloat16, torch.float32):
+        out_t = torch.empty(1, sh.nh * HD, dtype=dt, device=dev)
+        out_h = torch.empty_like(out_t)
+        ops.decode_layer(qkv, qn, kn, wl.EPS, cs, pos, kc_t, vc_t, case.bound, sh.scale, ws, n_split, out_t,
+                         sh.nh, sh.nkv)
+        ops.decode_layer(qkv, qn, kn, wl.EPS, cs, pos, kc_h, vc_h, case.bound, sh.scale, ws, n_split, out_h,
+                         sh.nh, sh.nkv)
+        torch.cuda.synchronize()
+        assert torch.equal(out_t, out_h), f"outputs differ ({dt})"
+        assert torch.equal(kc_t, kc_h) and torch.equal(vc_t, vc_h), "KV rows differ"
+
+
 def test_device_rope_table_equals_torch_table(gpu):
     """The library's cos/sin kernel reproduces torch's table (the reference's expression) bit for bit
     for every position of the longest cache served (32768)."""
