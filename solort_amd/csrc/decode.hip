@@ -38,7 +38,9 @@
 //     O^T += V^T P^T on v_mfma_f32_32x32x16_bf16 with the query rows (at most
 //     32) as the N dimension; V^T comes from transposing LDS reads and P
 //     enters as bf16 high and low parts (~16 bits), with a lazily moved
-//     softmax maximum.  The wavefronts merge in LDS at the end.
+//     softmax maximum.  The wavefronts merge in LDS at the end.  Fused, on a
+//     contiguous cache with packed qkv rows, the same body runs as
+//     decode_mfma_packed_kernel (packed arguments, as above).
 // Output: with one split the block writes the answer; otherwise its partial
 // (running max in log2 units, sum, unnormalised output).  Combine kernel:
 // merges the partials of each KV head (log-sum-exp); the kernel boundary
@@ -450,9 +452,10 @@ __device__ __forceinline__ KVTile fetch_tile(const uint16_t* kp, const uint16_t*
 // qkv rows (row stride qsrc_stride); unfused, the q rows [nq][nh][128]
 // (qsrc_stride = nh*128).
 template <int NQ, int G, bool FUSED, bool PAGED>
-__global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint16_t* vc, int tok_stride, int head_stride,
-                                                        int chunk, int bound, const uint16_t* qsrc, int qsrc_stride,
-                                                        int nh, const uint16_t* qn_w, const DecodeTail a) {
+__device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int tok_stride, int head_stride,
+                                                 int chunk, int bound, const uint16_t* qsrc, int qsrc_stride,
+                                                 int nh, const uint16_t* qn_w, const uint16_t* kn_w,
+                                                 const uint16_t* rope_cs, const DecodeTail& a) {
   constexpr int R = NQ * G;  // query rows sharing one KV head (<= 32)
   constexpr int NROWS = FUSED ? NQ * (G + 2) : R;
   static_assert(R <= 32, "at most 32 query rows per KV head");
@@ -490,8 +493,8 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint1
       const int t = row / (G + 2), c = row % (G + 2);
       const int hs = c < G ? kvh * G + c : (c == G ? nh + kvh : nh + nkv + kvh);
       raw[ps] = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + hs * SOLORT_HD + j * 8);
-      cr[ps] = *reinterpret_cast<const uint4*>(a.rope_cs + t * 64 + (j & 7) * 8);
-      sr[ps] = *reinterpret_cast<const uint4*>(a.rope_cs + (NQ + t) * 64 + (j & 7) * 8);
+      cr[ps] = *reinterpret_cast<const uint4*>(rope_cs + t * 64 + (j & 7) * 8);
+      sr[ps] = *reinterpret_cast<const uint4*>(rope_cs + (NQ + t) * 64 + (j & 7) * 8);
     } else {
       const int t = row / G, g = row % G;
       raw[ps] = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + (kvh * G + g) * SOLORT_HD + j * 8);
@@ -499,7 +502,7 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint1
   }
   if constexpr (FUSED) {
     wq0 = *reinterpret_cast<const uint4*>(qn_w + j * 8);
-    wk0 = *reinterpret_cast<const uint4*>(a.kn_w + j * 8);
+    wk0 = *reinterpret_cast<const uint4*>(kn_w + j * 8);
   }
   __builtin_amdgcn_sched_barrier(0);  // keep these loads ahead of the K/V loads
 
@@ -752,6 +755,32 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint1
         make_float2(m == -INFINITY ? m : m * qs, lsum);
 }
 
+// Arguments as the entry points pass them: the leading 14 dwords arrive
+// preloaded in SGPRs; kn_w and rope_cs travel in the tail.
+template <int NQ, int G, bool FUSED, bool PAGED>
+__global__ __launch_bounds__(256, 2) void decode_mfma_kernel(uint16_t* kc, uint16_t* vc, int tok_stride, int head_stride,
+                                                        int chunk, int bound, const uint16_t* qsrc, int qsrc_stride,
+                                                        int nh, const uint16_t* qn_w, const DecodeTail a) {
+  decode_mfma_body<NQ, G, FUSED, PAGED>(kc, vc, tok_stride, head_stride, chunk, bound, qsrc, qsrc_stride, nh, qn_w,
+                                        a.kn_w, a.rope_cs, a);
+}
+
+// Fused, contiguous cache, packed qkv rows: every pointer the first loads
+// need fits the 14 preloaded dwords.  strides8 = tok_stride / 8 |
+// (head_stride / 8) << 16; geom = (chunk / 32 - 1) | nh << 5 | bound << 16
+// (chunk <= 1024, nh < 2048, bound < 2^16); the qkv row stride is
+// (nh + 2 nkv) * 128.
+template <int NQ, int G>
+__global__ __launch_bounds__(256, 2) void decode_mfma_packed_kernel(uint16_t* kc, uint16_t* vc, unsigned strides8,
+                                                               unsigned geom, const uint16_t* qkv,
+                                                               const uint16_t* qn_w, const uint16_t* kn_w,
+                                                               const uint16_t* rope_cs, const DecodeTail a) {
+  const int tok_stride = (int)(strides8 & 0xffffu) * 8, head_stride = (int)(strides8 >> 16) * 8;
+  const int chunk = ((int)(geom & 31u) + 1) * 32, nh = (int)((geom >> 5) & 2047u), bound = (int)(geom >> 16);
+  decode_mfma_body<NQ, G, true, false>(kc, vc, tok_stride, head_stride, chunk, bound, qkv,
+                                       (nh + 2 * (nh / G)) * SOLORT_HD, nh, qn_w, kn_w, rope_cs, a);
+}
+
 // The log-sum-exp combine of the n_split partials of each KV head.  Grid
 // (nkv, column blocks): block = (KV head, 32 float4 columns of its [R][128]
 // output); thread = (column, split group sg of 8): it merges splits sg,
@@ -893,6 +922,17 @@ static bool launch_split_p(const DecodeArgs& a, hipStream_t s) {
           hipLaunchKernelGGL((decode_lanes_kernel<NQ, G, 2, FUSED, PAGED>), grid, dim3(256), 0, s, a.kc, a.vc,
                              a.tok_stride, a.head_stride, a.chunk, a.bound, a.qsrc, a.qsrc_stride, a.nh, a.qn_w,
                              a.tail);
+        return true;
+      }
+    }
+    if constexpr (FUSED && !PAGED) {
+      // The packed-argument kernel when the layout fits its fields.
+      if (a.tok_stride < (1 << 19) && a.head_stride < (1 << 19) && a.nh < 2048 && a.bound < (1 << 16) &&
+          a.chunk <= 1024 && a.qsrc_stride == (a.nh + 2 * a.nkv) * SOLORT_HD) {
+        const unsigned strides8 = (unsigned)(a.tok_stride / 8) | (unsigned)(a.head_stride / 8) << 16;
+        const unsigned geom = (unsigned)(a.chunk / 32 - 1) | (unsigned)a.nh << 5 | (unsigned)a.bound << 16;
+        hipLaunchKernelGGL((decode_mfma_packed_kernel<NQ, G>), grid, dim3(256), 0, s, a.kc, a.vc, strides8, geom,
+                           a.qsrc, a.qn_w, a.tail.kn_w, a.tail.rope_cs, a.tail);
         return true;
       }
     }

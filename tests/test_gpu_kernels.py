@@ -355,21 +355,22 @@ def test_decode_layer_repeated_calls_reuse_workspace(gpu):
         assert torch.equal(outs[i], outs[i - 4])
 
 
-@pytest.mark.parametrize("live,n_split", [(1024, 32), (256, 8)])
-def test_decode_layer_head_major_cache_equals_token_major(gpu, live, n_split):
-    """A head-major cache ([nkv][8192][128] storage: head stride 2^20 elements, past the 16-bit
-    stride fields of the packed-argument kernel, so the launch takes the general one) gives the
-    same KV bits and output bits as the token-major [max_len][nkv][128] cache."""
-    case = wl.decode_case(1, live=live, layers=1)
+@pytest.mark.parametrize("index,live,n_split", [(1, 1024, 32), (1, 256, 8), (4, None, 32)])
+def test_decode_layer_head_major_cache_equals_token_major(gpu, index, live, n_split):
+    """A head-major cache ([nkv][rows][128] storage with rows >= 8192: head stride >= 2^20 elements,
+    past the 16-bit stride fields of the packed-argument kernels, so the launch takes the general
+    one) gives the same KV bits and output bits as the token-major [max_len][nkv][128] cache, for the
+    lane kernel (one token) and the MFMA kernel (verify, 5 tokens)."""
+    case = wl.decode_case(index, live=live, layers=1)
     dev = gpu
     sh = case.shape
-    _say(f"[head-major {sh.name} pos={case.pos} bound={case.bound} n_split={n_split}]")
+    _say(f"[head-major {sh.name} pos={case.pos} nq={case.nq} bound={case.bound} n_split={n_split}]")
     ifr = _ifr(dev)
     pos = torch.tensor([case.pos], dtype=torch.long, device=dev)
     qkv = case.qkv[0].to(dev)
     qn, kn = case.qn_w[0].to(dev), case.kn_w[0].to(dev)
     kc_t, vc_t = case.kc[0].to(dev), case.vc[0].to(dev)
-    rows = 8192
+    rows = max(8192, 2 * case.max_len)
     k_store = torch.zeros(sh.nkv, rows, HD, dtype=torch.bfloat16, device=dev)
     v_store = torch.zeros_like(k_store)
     k_store[:, :case.max_len] = kc_t.permute(1, 0, 2)
@@ -377,10 +378,10 @@ def test_decode_layer_head_major_cache_equals_token_major(gpu, live, n_split):
     kc_h = k_store[:, :case.max_len].permute(1, 0, 2)
     vc_h = v_store[:, :case.max_len].permute(1, 0, 2)
     assert kc_h.stride() == (HD, rows * HD, 1)
-    ws = ops.attn_workspace(1, sh.nh, sh.nkv, n_split, dev)
-    cs = ops.rope_rows(ifr, pos, 1)
+    ws = ops.attn_workspace(case.nq, sh.nh, sh.nkv, n_split, dev)
+    cs = ops.rope_rows(ifr, pos, case.nq)
     for dt in (torch.bfloat16, torch.float32):
-        out_t = torch.empty(1, sh.nh * HD, dtype=dt, device=dev)
+        out_t = torch.empty(case.nq, sh.nh * HD, dtype=dt, device=dev)
         out_h = torch.empty_like(out_t)
         ops.decode_layer(qkv, qn, kn, wl.EPS, cs, pos, kc_t, vc_t, case.bound, sh.scale, ws, n_split, out_t,
                          sh.nh, sh.nkv)
@@ -389,6 +390,38 @@ def test_decode_layer_head_major_cache_equals_token_major(gpu, live, n_split):
         torch.cuda.synchronize()
         assert torch.equal(out_t, out_h), f"outputs differ ({dt})"
         assert torch.equal(kc_t, kc_h) and torch.equal(vc_t, vc_h), "KV rows differ"
+
+
+@pytest.mark.parametrize("index,live,n_split", [(1, 1024, 32), (4, None, 32)])
+def test_decode_layer_padded_qkv_rows_equal_packed(gpu, index, live, n_split):
+    """qkv rows with a padded row stride (the general MFMA kernel: its packed variant assumes packed
+    rows) give the same KV bits and output bits as packed rows."""
+    case = wl.decode_case(index, live=live, layers=1)
+    dev = gpu
+    sh = case.shape
+    _say(f"[padded qkv {sh.name} pos={case.pos} nq={case.nq} bound={case.bound} n_split={n_split}]")
+    ifr = _ifr(dev)
+    pos = torch.tensor([case.pos], dtype=torch.long, device=dev)
+    qkv = case.qkv[0].to(dev)
+    store = torch.zeros(case.nq, sh.qkv_width + 64, dtype=torch.bfloat16, device=dev)
+    store[:, :sh.qkv_width] = qkv
+    qkv_p = store[:, :sh.qkv_width]
+    assert qkv_p.stride(0) == sh.qkv_width + 64
+    qn, kn = case.qn_w[0].to(dev), case.kn_w[0].to(dev)
+    kc_a, vc_a = case.kc[0].to(dev), case.vc[0].to(dev)
+    kc_b, vc_b = kc_a.clone(), vc_a.clone()
+    ws = ops.attn_workspace(case.nq, sh.nh, sh.nkv, n_split, dev)
+    cs = ops.rope_rows(ifr, pos, case.nq)
+    for dt in (torch.bfloat16, torch.float32):
+        out_a = torch.empty(case.nq, sh.nh * HD, dtype=dt, device=dev)
+        out_b = torch.empty_like(out_a)
+        ops.decode_layer(qkv, qn, kn, wl.EPS, cs, pos, kc_a, vc_a, case.bound, sh.scale, ws, n_split, out_a,
+                         sh.nh, sh.nkv)
+        ops.decode_layer(qkv_p, qn, kn, wl.EPS, cs, pos, kc_b, vc_b, case.bound, sh.scale, ws, n_split, out_b,
+                         sh.nh, sh.nkv)
+        torch.cuda.synchronize()
+        assert torch.equal(out_a, out_b), f"outputs differ ({dt})"
+        assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b), "KV rows differ"
 
 
 def test_device_rope_table_equals_torch_table(gpu):
