@@ -27,7 +27,7 @@ import time
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
-# HBM bytes per launch of the decode split kernel at KV 1024 (decode_lanes_kernel<1,4,2,true>),
+# HBM bytes per launch of the decode split kernel at KV 1024 (decode_lanes_packed_kernel<4,2>),
 # from rocprofv3 --pmc FETCH_SIZE (x1.999: a 64 MiB copy reads 32786 KiB on it) plus
 # WRITE_SIZE (x1.000): (2103.0 * 1.999 + 524.0) KiB.  Re-measured whenever that kernel changes.
 DECODE_KERNEL_TRAFFIC = int((2103.0 * 1.999 + 524.0) * 1024)
@@ -172,7 +172,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": DECODE_KERNEL_TRAFFIC if live == 1024 else None,
-                     "kernel": "solort_decode_layer = decode_lanes_kernel<1,4,2,fused> + combine_kernel<1,4>",
+                     "kernel": "solort_decode_layer = decode_lanes_packed_kernel<4,2> + combine_kernel<1,4>",
                      "kernel_us": round(kern_us, 3),
                      "algorithmic_bytes": kbytes},
     }
