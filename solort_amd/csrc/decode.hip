@@ -520,12 +520,23 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
   const int64_t pos0 = a.pos0_dev[0];
 
   // 3. q rows (and, fused, the new tokens' K/V rows) into LDS; rows R..31 of
-  //    the q tile are zero.
+  //    the q tile are zero.  Fused: every pass's row is normalised first,
+  //    without branches (V rows and idle slots too, unused), so the passes'
+  //    reduction chains overlap; then the rows are stored.
+  if constexpr (FUSED) {
+    uint4 ov[NPASS];
 #pragma unroll
-  for (int ps = 0; ps < NPASS; ++ps) {
-    const int row = slot + 16 * ps;
-    if (row >= NROWS) break;
-    if constexpr (FUSED) {
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int c = min(slot + 16 * ps, NROWS - 1) % (G + 2);
+      float cs[8], sn[8];
+      unpack8(cr[ps], cs);
+      unpack8(sr[ps], sn);
+      ov[ps] = qknorm_rope_row(raw[ps], c < G ? wq0 : wk0, cs, sn, a.eps, j);
+    }
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int row = slot + 16 * ps;
+      if (row >= NROWS) break;
       const int t = row / (G + 2), c = row % (G + 2);
       const int64_t pos = pos0 + t;
       const bool pos_ok = pos >= 0 && pos < a.pos_limit;
@@ -534,20 +545,20 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
         if (split == 0 && pos_ok)
           *reinterpret_cast<uint4*>(vc + row_off<PAGED>(pos, tok_stride, a) + (int64_t)kvh * head_stride + j * 8) =
               raw[ps];
-        continue;
-      }
-      float cs[8], sn[8];
-      unpack8(cr[ps], cs);
-      unpack8(sr[ps], sn);
-      const uint4 ov = qknorm_rope_row(raw[ps], c < G ? wq0 : wk0, cs, sn, a.eps, j);
-      if (c < G) {
-        *reinterpret_cast<uint4*>(&s_q[(t * G + c) * kQStride + j * 8]) = ov;
+      } else if (c < G) {
+        *reinterpret_cast<uint4*>(&s_q[(t * G + c) * kQStride + j * 8]) = ov[ps];
       } else {
-        *reinterpret_cast<uint4*>(&s_new[t * 128 + j * 8]) = ov;
+        *reinterpret_cast<uint4*>(&s_new[t * 128 + j * 8]) = ov[ps];
         if (split == 0 && pos_ok)
-          *reinterpret_cast<uint4*>(kc + row_off<PAGED>(pos, tok_stride, a) + (int64_t)kvh * head_stride + j * 8) = ov;
+          *reinterpret_cast<uint4*>(kc + row_off<PAGED>(pos, tok_stride, a) + (int64_t)kvh * head_stride + j * 8) =
+              ov[ps];
       }
-    } else {
+    }
+  } else {
+#pragma unroll
+    for (int ps = 0; ps < NPASS; ++ps) {
+      const int row = slot + 16 * ps;
+      if (row >= NROWS) break;
       *reinterpret_cast<uint4*>(&s_q[row * kQStride + j * 8]) = raw[ps];
     }
   }
