@@ -424,6 +424,56 @@ def test_decode_layer_padded_qkv_rows_equal_packed(gpu, index, live, n_split):
         assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b), "KV rows differ"
 
 
+@pytest.mark.parametrize("group,nq", [(1, 1), (8, 1), (1, 5), (8, 4)])
+def test_decode_layer_query_groups_1_and_8(gpu, group, nq):
+    """Query groups 1 and 8 (the split kernels serve 1, 2, 4 and 8; the Qwen3 shapes use 2 and 4):
+    the fused layer equals the two-launch path bit for bit (KV rows and output) and the
+    reference's bf16 ops within the bf16 bar, for one new token (lane kernel) and for several
+    (MFMA kernel)."""
+    dev = gpu
+    nkv, max_len, bound, n_split, pos0 = 4, 512, 512, 16, 300
+    nh = nkv * group
+    width = (nh + 2 * nkv) * HD
+    scale = HD ** -0.5
+    g = torch.Generator().manual_seed(4000 + 10 * group + nq)
+    kc0 = torch.zeros(max_len, nkv, HD)
+    vc0 = torch.zeros(max_len, nkv, HD)
+    kc0[:pos0] = torch.randn(pos0, nkv, HD, generator=g)
+    vc0[:pos0] = torch.randn(pos0, nkv, HD, generator=g)
+    kc0, vc0 = kc0.to(torch.bfloat16), vc0.to(torch.bfloat16)
+    qkv_c = torch.randn(nq, width, generator=g).to(torch.bfloat16)
+    qn_c = (1 + 0.1 * torch.randn(HD, generator=g)).to(torch.bfloat16)
+    kn_c = (1 + 0.1 * torch.randn(HD, generator=g)).to(torch.bfloat16)
+    _say(f"[group {group} nh={nh} nkv={nkv} nq={nq} pos0={pos0} bound={bound} n_split={n_split}]")
+    ifr = _ifr(dev)
+    pos = torch.tensor([pos0], dtype=torch.long, device=dev)
+    qkv, qn, kn = qkv_c.to(dev), qn_c.to(dev), kn_c.to(dev)
+    kc_a, vc_a = kc0.to(dev), vc0.to(dev)
+    kc_b, vc_b = kc_a.clone(), vc_a.clone()
+    q = torch.empty(nq, nh, HD, dtype=torch.bfloat16, device=dev)
+    ws = ops.attn_workspace(nq, nh, nkv, n_split, dev)
+    out_a = torch.empty(nq, nh * HD, dtype=torch.bfloat16, device=dev)
+    out_b = torch.empty_like(out_a)
+    ops.qknorm_rope_kvwrite(qkv, qn, kn, wl.EPS, ifr, pos, q, kc_a, vc_a, nh, nkv)
+    (ops.decode_attn if nq == 1 else ops.verify_attn)(q, kc_a, vc_a, pos, bound, scale, ws, n_split, out_a)
+    ops.decode_layer(qkv, qn, kn, wl.EPS, ops.rope_rows(ifr, pos, nq), pos, kc_b, vc_b, bound, scale, ws, n_split,
+                     out_b, nh, nkv)
+    torch.cuda.synchronize()
+    assert torch.equal(kc_a, kc_b) and torch.equal(vc_a, vc_b), "KV rows differ"
+    assert torch.equal(out_a, out_b), "outputs differ"
+    cos, sin = _tables(dev, max_len)
+    rows = torch.arange(pos0, pos0 + nq)
+    c, sn = cos.cpu()[rows], sin.cpu()[rows]
+    qr, kr, vr = ref.prologue(qkv_c, qn_c, kn_c, wl.EPS, torch.cat([c, c], -1), torch.cat([sn, sn], -1), nh, nkv)
+    kc_r, vc_r = kc0.clone(), vc0.clone()
+    ref.write_kv(kc_r, vc_r, kr, vr, pos0)
+    if nq == 1:
+        want = ref.decode_attn(qr, kc_r, vc_r, pos0, bound, scale)
+    else:
+        want = ref.verify_attn(qr, kc_r, vc_r, pos0, scale)
+    _check_bf16(out_b, want, f"  group {group} nq={nq} bf16 vs reference ops")
+
+
 def test_device_rope_table_equals_torch_table(gpu):
     """The library's cos/sin kernel reproduces torch's table (the reference's expression) bit for bit
     for every position of the longest cache served (32768)."""
