@@ -27,10 +27,11 @@ import time
 
 HBM_PEAK_GBS = 8000.0
 BF16_PEAK_TFLOPS = 2500.0
-# HBM bytes per launch of the decode split kernel at KV 1024 (decode_lanes_packed_kernel<4,2>),
-# from rocprofv3 --pmc FETCH_SIZE (x1.999: a 64 MiB copy reads 32786 KiB on it) plus
-# WRITE_SIZE (x1.000): (2103.0 * 1.999 + 524.0) KiB.  Re-measured whenever that kernel changes.
-DECODE_KERNEL_TRAFFIC = int((2103.0 * 1.999 + 524.0) * 1024)
+# The split kernel of one Qwen3-4B decode-attention call at KV 1024 (32 q / 8 kv heads, 32 splits).
+DECODE_KERNEL = "decode_lanes_packed_kernel<4, 2>"
+# The 64 MiB device copy bench.py issues outside its timed regions: the reference that scales the
+# FETCH_SIZE / WRITE_SIZE counters into bytes.
+CALIB_BYTES = 64 << 20
 
 
 def decode_bytes(live: int, nh: int = 32, nkv: int = 8, hd: int = 128) -> int:
@@ -54,13 +55,16 @@ def parse() -> argparse.Namespace:
     p.add_argument("--cpu-seconds", type=float, default=10.0, help="budget of the CPU baseline sample")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--no-sweep", action="store_true", help="skip the per-bucket decode extras")
+    p.add_argument("--no-traffic", action="store_true",
+                   help="skip the in-run HBM traffic measurement (two short rocprofv3 --pmc passes)")
     p.add_argument("--only", choices=("all", "decode", "prefill", "long", "verify", "gemv", "model", "paged",
-                                      "torchref"),
+                                      "torchref", "floor", "cpu"),
                    default="all",
                    help="decode: the decode step and its kernel only; prefill: the prefill kernels only; "
                         "long: the Qwen3-8B KV 32768 decode only; verify: the speculative verify and argmax "
                         "only; gemv: the decode-step GEMVs only; model: whole-model greedy decode only; paged: the "
-                        "paged-KV decode only; torchref: the reference's torch decode ops on this GPU only (for "
+                        "paged-KV decode only; torchref: the reference's torch decode ops on this GPU only; "
+                        "floor: the launch and streaming floor probes only; cpu: the CPU baselines only (for "
                         "per-workload profiles)")
     return p.parse_args()
 
@@ -71,10 +75,13 @@ def main() -> int:
         print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no multi-GPU path; "
               "each GPU would run its own KV heads or key splits (see DESIGN.md).", file=sys.stderr)
         return 2
+    if args.only == "cpu":
+        print(json.dumps({"cpu_baseline": cpu_baseline(args.cpu_seconds, args.live)}), flush=True)
+        return 0
 
     import torch
 
-    from solort_amd import ops
+    from solort_amd import _lib, ops
     from solort_amd import workloads as wl
     from solort_amd.runner import GraphQwen3Attention, decode_splits
 
@@ -122,6 +129,9 @@ def main() -> int:
     if args.only == "paged":
         print(json.dumps({"paged_decode_kv1024": paged_extras(torch, ops, runners, dev, sh)}), flush=True)
         return 0
+    if args.only == "floor":
+        print(json.dumps({"floor": floor_extras(torch, ops, runners, dev, sh)}), flush=True)
+        return 0
     if args.only == "model":
         del runners
         torch.cuda.empty_cache()
@@ -142,12 +152,14 @@ def main() -> int:
 
     # ---------------------------------------------------------------- decode kernel alone (roofline)
     ns = decode_splits(bound, sh.nkv)
+    lib = _lib.load()
+    single = lib.solort_combine_mode(-1) == 1
     kern_us = time_decode_kernel(torch, ops, runners, bound, ns, sh, dev, reps=4)
     kbytes = decode_bytes(live, sh.nh, sh.nkv)
     achieved = kbytes / (kern_us * 1e-6) / 1e9
     # A plain 64 MiB device copy, outside every timed region: the reference point that scales the
     # FETCH_SIZE / WRITE_SIZE hardware counters of a profiling run into bytes.
-    calib_src = torch.empty(64 << 20, dtype=torch.uint8, device=dev)
+    calib_src = torch.empty(CALIB_BYTES, dtype=torch.uint8, device=dev)
     torch.empty_like(calib_src).copy_(calib_src)
     torch.cuda.synchronize()
 
@@ -171,14 +183,18 @@ def main() -> int:
         "decode_gbps": round(kbytes / (us_per_layer * 1e-6) / 1e9, 1),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
-                     "traffic": DECODE_KERNEL_TRAFFIC if live == 1024 else None,
-                     "kernel": "solort_decode_layer = decode_lanes_packed_kernel<4,2> + combine_kernel<1,4>",
+                     "traffic": None,
+                     "kernel": (f"solort_decode_layer = {DECODE_KERNEL} (split-KV attention with the "
+                                "single-launch combine)" if single else
+                                f"solort_decode_layer = {DECODE_KERNEL} + combine_kernel<1, 4>"),
                      "kernel_us": round(kern_us, 3),
-                     "algorithmic_bytes": kbytes},
+                     "algorithmic_bytes": kbytes,
+                     "single_launch_combine": single},
     }
 
     if not args.no_sweep and args.only == "all":
         result["extras"] = extras(torch, ops, wl, runners, dev, sh)
+        result["extras"]["floor"] = floor_extras(torch, ops, runners, dev, sh)
         result["extras"].update(verify_extras(torch, ops, wl, runners, dev, sh))
         result["extras"]["decode_8b_kv32768"] = long_decode_extras(torch, ops, wl, dev)
         result["extras"]["decode_gemv"] = gemv_extras(torch, ops, dev)
@@ -186,12 +202,16 @@ def main() -> int:
         result["extras"]["torch_reference_decode"] = torch_reference_extras(torch, runners, dev, sh, bound)
         result["extras"]["decode_model"] = model_extras(torch, dev)
     if args.only == "all":
-        result["prefill"] = prefill_extras(torch, ops, runners, dev, sh)
-        p1024 = result["prefill"].get("1024")
-        if p1024:
-            result["prefill_tflops"] = p1024["tflops"]
+        by_t = prefill_extras(torch, ops, runners, dev, sh)
+        result["prefill"] = {"T": 1024, **by_t["1024"], "by_T": by_t}
+        result["prefill_tflops"] = by_t["1024"]["tflops"]
 
-    if not args.no_cpu and args.only == "all":
+    if not args.no_traffic and args.only == "all" and live == 1024:
+        tr = measure_traffic(DECODE_KERNEL)
+        result["roofline"]["traffic"] = tr.get("bytes")
+        result["roofline"]["traffic_detail"] = tr
+
+    if not args.no_cpu and args.only in ("all", "cpu"):
         result["cpu_baseline"] = cpu_baseline(args.cpu_seconds, live)
 
     print(json.dumps(result), flush=True)
@@ -230,21 +250,123 @@ def time_decode_kernel(torch, ops, runners, bound, ns, sh, dev, reps=3, pos=None
 
 
 def extras(torch, ops, wl, runners, dev, sh) -> dict:
-    """Decode attention call times per bucket (same rotation), and a split-count sweep at KV 1024."""
+    """Decode attention call times per bucket (same rotation), with the split combine in the same
+    launch (the default where the placement check passed) and as a second launch; and a split-count
+    sweep at KV 1024."""
+    from solort_amd import _lib
     from solort_amd.runner import decode_splits
 
-    out: dict = {"decode_call_us": {}, "n_split_sweep_kv1024": {}}
+    lib = _lib.load()
+    default_mode = lib.solort_combine_mode(-1)
+    out: dict = {"decode_call_us": {}, "n_split_sweep_kv1024": {}, "single_launch_combine": default_mode == 1}
     for live in (128, 256, 512, 1024):
         ns = decode_splits(live, sh.nkv)
         pos = torch.tensor([live - 1], dtype=torch.long, device=dev)
         us = time_decode_kernel(torch, ops, runners, live, ns, sh, dev, reps=3, pos=pos)
+        lib.solort_combine_mode(0)
+        us2 = time_decode_kernel(torch, ops, runners, live, ns, sh, dev, reps=3, pos=pos)
+        lib.solort_combine_mode(1)
         gbs = decode_bytes(live) / (us * 1e-6) / 1e9
         out["decode_call_us"][str(live)] = {"us": round(us, 3), "gbps": round(gbs, 1),
-                                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "n_split": ns}
+                                            "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "n_split": ns,
+                                            "two_launch_us": round(us2, 3)}
     pos = torch.tensor([1023], dtype=torch.long, device=dev)
     for ns in (8, 16, 32, 64, 128):
         us = time_decode_kernel(torch, ops, runners, 1024, ns, sh, dev, reps=3, pos=pos)
         out["n_split_sweep_kv1024"][str(ns)] = round(us, 3)
+    lib.solort_combine_mode(default_mode)
+    return out
+
+
+def floor_extras(torch, ops, runners, dev, sh) -> dict:
+    """The launch and streaming floor a decode-attention call at KV 1024 is compared with, measured
+    the way the call is (HIP events around replays of one graph holding 288 launches):
+      empty_node_us      an empty kernel (1 workgroup) per graph node
+      read_4mib_us       one launch streaming 4 MiB (the call's K and V bytes) with the call's 256
+                         workgroups, one 16-byte load in flight per thread; and with 512 workgroups
+                         x 2 loads in flight (the best shape found)
+      read_4mib_then_32wg_us  the same read followed by a dependent 32-workgroup launch reading
+                         512 KiB (the two-launch combine's shape)
+    Sources rotate over 144 distinct 4 MiB slices of the rotated KV caches (576 MiB, beyond the 256
+    MB Infinity Cache), as the decode calls do."""
+    from solort_amd import _lib
+
+    lib = _lib.load()
+    slices = []
+    for r in runners:
+        flat = r.kc.view(-1)
+        n4 = flat.numel() * 2 // (4 << 20)
+        slices += [flat[i * (2 << 20):(i + 1) * (2 << 20)] for i in range(n4)]
+    slices = slices[:288]
+    sink = torch.zeros(1024, dtype=torch.int32, device=dev)
+    small = torch.zeros(512 << 10, dtype=torch.uint8, device=dev)
+
+    def empty(n_wg=1):  # on the current stream: the capture stream inside a graph capture
+        _lib.check(lib.solort_probe_empty(n_wg, torch.cuda.current_stream(dev).cuda_stream), "probe_empty")
+
+    def read(src_ptr, nbytes, n_wg, inflight):
+        _lib.check(lib.solort_probe_read(src_ptr, nbytes, n_wg, inflight, sink.data_ptr(),
+                                         torch.cuda.current_stream(dev).cuda_stream), "probe_read")
+
+    res = {"empty_node_us": round(_graph_us(torch, dev, [empty] * 288, reps=4), 3)}
+    res["read_4mib_us"] = round(_graph_us(
+        torch, dev, [lambda x=x: read(x.data_ptr(), 4 << 20, 256, 1) for x in slices], reps=4), 3)
+    res["read_4mib_512wg_x2_us"] = round(_graph_us(
+        torch, dev, [lambda x=x: read(x.data_ptr(), 4 << 20, 512, 2) for x in slices], reps=4), 3)
+    res["read_4mib_then_32wg_us"] = round(_graph_us(
+        torch, dev, [lambda x=x: (read(x.data_ptr(), 4 << 20, 256, 1), read(small.data_ptr(), 512 << 10, 32, 4))
+                     for x in slices], reps=4), 3)
+    res["slices"] = len(slices)
+    return res
+
+
+def measure_traffic(kernel: str, timeout_s: int = 120) -> dict:
+    """HBM bytes per launch of `kernel`, measured in this run: two rocprofv3 --pmc passes (FETCH_SIZE,
+    then WRITE_SIZE) over `bench.py --only decode`, each counter scaled by what it reads for the
+    64 MiB device copy that run issues (CALIB_BYTES read and written).  Returns the bytes and the
+    raw figures, or the reason they are missing."""
+    import csv
+    import shutil
+    import subprocess
+    import tempfile
+
+    prof = shutil.which("rocprofv3") or "/opt/rocm/bin/rocprofv3"
+    if not os.path.exists(prof):
+        return {"bytes": None, "reason": "rocprofv3 not found"}
+    here = os.path.dirname(os.path.abspath(__file__))
+    env = {**os.environ, "TMPDIR": "/tmp"}
+    out = {"kernel": kernel, "calibration": "64 MiB device copy"}
+    for counter in ("FETCH_SIZE", "WRITE_SIZE"):
+        d = tempfile.mkdtemp(prefix=f"solort_pmc_{counter.lower()}_", dir="/tmp")
+        cmd = [prof, "--pmc", counter, "--output-format", "csv", "-d", d, "-o", "p", "--",
+               sys.executable, os.path.join(here, "bench.py"), "--only", "decode", "--steps", "10", "--warmup", "2",
+               "--no-cpu", "--no-traffic"]
+        try:
+            subprocess.run(cmd, cwd="/tmp", env=env, stdout=subprocess.DEVNULL, stderr=subprocess.DEVNULL,
+                           timeout=timeout_s)
+        except subprocess.TimeoutExpired:
+            return {"bytes": None, "reason": f"rocprofv3 --pmc {counter} timed out"}
+        files = [os.path.join(r, f) for r, _, fs in os.walk(d) for f in fs if f.endswith("counter_collection.csv")]
+        if not files:
+            return {"bytes": None, "reason": f"no counter output for {counter}"}
+        vals, calib = [], []
+        with open(files[0], newline="") as f:
+            rows = sorted((r for r in csv.DictReader(f) if r["Counter_Name"] == counter),
+                          key=lambda r: int(r["Dispatch_Id"]))
+        for row in rows:
+            name, v = row["Kernel_Name"], float(row["Counter_Value"])
+            if kernel in name:
+                vals.append(v)
+            elif "copyBuffer" in name:
+                calib.append(v)
+        shutil.rmtree(d, ignore_errors=True)
+        if not vals or not calib:
+            return {"bytes": None, "reason": f"{counter}: kernel or calibration copy not found in the profile"}
+        kib = statistics.mean(vals)
+        factor = (CALIB_BYTES / 1024) / calib[-1]  # the run's last device copy is the calibration copy
+        out[counter] = {"kib_raw": round(kib, 1), "dispatches": len(vals), "calib_kib_raw": calib[-1],
+                        "factor": round(factor, 4), "bytes": int(kib * factor * 1024)}
+    out["bytes"] = out["FETCH_SIZE"]["bytes"] + out["WRITE_SIZE"]["bytes"]
     return out
 
 
@@ -708,9 +830,32 @@ def torch_reference_extras(torch, runners, dev, sh, bound: int) -> dict:
             "note": "reference decode-attention torch ops on this GPU, graphed; K^T and V made contiguous"}
 
 
+def _median_us(fn, budget_s: float, warm: int = 5, min_runs: int = 20, max_runs: int = 200) -> tuple[float, int]:
+    """Median wall time (us) of fn() over at least min_runs timed runs after `warm` untimed ones,
+    continuing up to max_runs while the budget lasts (perf_counter_ns around each run)."""
+    for _ in range(warm):
+        fn()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    while len(times) < min_runs or (time.perf_counter() < t_end and len(times) < max_runs):
+        t0 = time.perf_counter_ns()
+        fn()
+        times.append((time.perf_counter_ns() - t0) / 1e3)
+    return statistics.median(times), len(times)
+
+
 def cpu_baseline(budget_s: float, live: int) -> dict:
-    """The oracle's fp32 torch restatement of the reference's decode attention block
-    (prologue + KV write + grouped attention, 36 layers) on the host cores."""
+    """The oracle's fp32 torch restatement of the reference path (cuda_graph_executor.py; the
+    reference's own method is synchronize + perf_counter over N replays, scripts/microbench_decode.py:
+    30-35) on the host cores, per BASELINE config, on the same seeded inputs as the GPU workloads:
+      config 1  Qwen3-0.6B decode, all 28 layers, 513 keys (bucket 1024), in full
+      config 2  Qwen3-4B decode, 36 layers, KV 128 / 256 / 512 / 1024 (`value`: KV `live`)
+      config 3  Qwen3-4B prefill T = 512: prologue + KV write + causal attention, 6 of the 36 layers
+      config 4  Qwen3-8B decode at KV 32768, 2 of the 36 layers (4.3 GB of fp32 cache per 16 layers)
+      config 5  Qwen3-4B verify: 5 tokens at 2048.. over the max-4096 cache, 6 of the 36 layers; and
+                the greedy argmax of the [5, 151936] logits
+    Each figure is the median of at least 20 runs after 5 warm-ups, per layer where the config has
+    layers."""
     import torch
 
     from oracle import ref
@@ -718,29 +863,84 @@ def cpu_baseline(budget_s: float, live: int) -> dict:
 
     cores = len(os.sched_getaffinity(0))
     torch.set_num_threads(cores)
-    sh = wl.QWEN3_4B
-    case = wl.decode_case(1, live=live, layers=sh.layers, dtype=torch.float32)
-    cos, sin = ref.cos_sin(torch.tensor([case.pos]), ref.inv_freq(128, wl.THETA), torch.float32)
-    times = []
-    t_end = time.perf_counter() + budget_s
-    n = 0
-    while n < 5 or (time.perf_counter() < t_end and n < 200):
-        t0 = time.perf_counter_ns()
-        ref.decode_layers(case.qkv, case.qn_w, case.kn_w, wl.EPS, cos, sin, case.kc, case.vc, case.pos,
-                          case.bound, sh.nh, sh.nkv, sh.scale)
-        times.append((time.perf_counter_ns() - t0) / 1e3)
-        n += 1
-    steady = times[2:] if len(times) > 4 else times
-    us_layer = statistics.median(steady) / sh.layers
     model = ""
     try:
         with open("/proc/cpuinfo") as f:
             model = next((ln.split(":", 1)[1].strip() for ln in f if ln.startswith("model name")), "")
     except OSError:
         pass
-    return {"value": round(us_layer, 2), "unit": "us/layer", "cores": cores, "kind": "port",
-            "sample": f"{len(times)} decode steps (36 layers, Qwen3-4B, KV live {live}) in fp32 torch on "
-                      f"{cores} threads of '{model}'; median per step / 36"}
+    per = budget_s / 8
+    f32 = torch.float32
+    inv = ref.inv_freq(128, wl.THETA)
+
+    def decode_fn(case):
+        sh = case.shape
+        cos, sin = ref.cos_sin(torch.tensor([case.pos]), inv, f32)
+        return lambda: ref.decode_layers(case.qkv, case.qn_w, case.kn_w, wl.EPS, cos, sin, case.kc, case.vc,
+                                         case.pos, case.bound, sh.nh, sh.nkv, sh.scale)
+
+    configs: dict = {}
+    c1 = wl.decode_case(0, dtype=f32)
+    us, n = _median_us(decode_fn(c1), per)
+    configs["1"] = {"us_per_layer": round(us / c1.shape.layers, 2), "us_per_step": round(us, 1), "runs": n,
+                    "workload": "Qwen3-0.6B decode, 28 layers, 513 keys (bucket 1024), fp32"}
+    c2 = {}
+    for L in wl.DECODE_LIVE:
+        case = wl.decode_case(1, live=L, dtype=f32)
+        us, n = _median_us(decode_fn(case), per / 2)
+        c2[str(L)] = {"us_per_layer": round(us / case.shape.layers, 2), "runs": n}
+        del case
+    configs["2"] = {"by_live": c2, "workload": "Qwen3-4B decode, 36 layers, fp32"}
+
+    nl = 6  # layers timed for configs 3 and 5 (each layer is the same work)
+    pc = wl.prefill_case(512, layers=nl, dtype=f32)
+    sh = pc.shape
+    cos, sin = ref.cos_sin(torch.arange(pc.T), inv, f32)
+    kc = torch.zeros(nl, pc.max_len, sh.nkv, 128)
+    vc = torch.zeros_like(kc)
+
+    def prefill():
+        for li in range(nl):
+            q, k, v = ref.prologue(pc.qkv[li], pc.qn_w[li], pc.kn_w[li], wl.EPS, cos, sin, sh.nh, sh.nkv)
+            ref.write_kv(kc[li], vc[li], k, v, 0)
+            ref.prefill_attn(q, k, v, sh.scale)
+
+    us, n = _median_us(prefill, per)
+    configs["3"] = {"us_per_layer": round(us / nl, 2), "runs": n,
+                    "workload": f"Qwen3-4B prefill T=512: prologue + KV write + causal attention, {nl} layers, fp32"}
+    del pc, kc, vc
+
+    c4 = wl.decode_case(3, layers=2, dtype=f32)
+    us, n = _median_us(decode_fn(c4), per)
+    configs["4"] = {"us_per_layer": round(us / 2, 2), "runs": n,
+                    "workload": "Qwen3-8B decode at KV 32768, 2 layers, fp32"}
+    del c4
+
+    c5 = wl.decode_case(4, layers=nl, dtype=f32)
+    sh = c5.shape
+    cos, sin = ref.cos_sin(c5.pos + torch.arange(c5.nq), inv, f32)
+
+    def verify():
+        for li in range(nl):
+            q, k, v = ref.prologue(c5.qkv[li], c5.qn_w[li], c5.kn_w[li], wl.EPS, cos, sin, sh.nh, sh.nkv)
+            ref.write_kv(c5.kc[li], c5.vc[li], k, v, c5.pos)
+            ref.verify_attn(q, c5.kc[li], c5.vc[li], c5.pos, sh.scale)
+
+    us, n = _median_us(verify, per)
+    logits = c5.logits.float()
+    aus, an = _median_us(lambda: ref.argmax(logits), per / 4)
+    configs["5"] = {"us_per_layer": round(us / nl, 2), "runs": n, "argmax_us": round(aus, 2),
+                    "argmax_runs": an,
+                    "workload": f"Qwen3-4B verify, 5 tokens at 2048 over the max-4096 cache, {nl} layers, fp32; "
+                                "argmax of [5, 151936] fp32 logits"}
+    del c5
+
+    head = c2.get(str(live), c2["1024"])
+    return {"value": head["us_per_layer"], "unit": "us/layer", "cores": cores, "kind": "port",
+            "sample": f"config 2 (Qwen3-4B decode, 36 layers, KV {live}) in fp32 torch on {cores} threads of "
+                      f"'{model}': median of {head['runs']} steps after 5 warm-ups, per layer; the other "
+                      "configs under `configs`",
+            "cpu_model": model, "configs": configs}
 
 
 if __name__ == "__main__":

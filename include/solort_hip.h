@@ -6,8 +6,9 @@
  * _GraphQwen3Runner (src/solort/model/cuda_graph_executor.py); it has no FFI.
  * Each entry point below replaces one block of that inline code and is cited
  * to it.  Plain pointers and sizes only: every buffer is owned by the caller,
- * nothing here allocates, frees, synchronises or reads device memory back, so
- * every call can be recorded into a hipGraph.  The position of the token(s)
+ * and apart from the one-time solort_init nothing here allocates, frees,
+ * synchronises or reads device memory back, so every call can be recorded
+ * into a hipGraph.  The position of the token(s)
  * is read on the device from `pos0_dev`, exactly like the reference's
  * `pos_buf` (cuda_graph_executor.py:71), so one captured graph serves every
  * position inside its bucket.
@@ -50,8 +51,32 @@ typedef void* solort_stream_t;
 /* Version of this ABI; bumped when a signature changes. */
 int solort_abi_version(void);
 
+/* 64-bit hash of the sources the library was built from (its HIP sources and
+ * headers), so a loader can refuse a library built from other sources. */
+uint64_t solort_source_id(void);
+
 /* Message of the last failed call on this thread ("" if none). */
 const char* solort_last_error(void);
+
+/*
+ * Per-device set-up (no counterpart in the reference, whose attention is
+ * inline torch code): call once per device, with that device current and
+ * outside graph capture (it launches a probe, synchronises and allocates a
+ * few KB that it frees).  It checks that workgroup b of a launch always runs
+ * on the XCD (L2 domain) of workgroup b % 8, the round-robin placement of
+ * MI355X, which the single-launch split combine relies on (see
+ * solort_decode_attn).  Without it, or if the check fails, every split call
+ * combines in a second launch.
+ */
+int solort_init(void);
+
+/*
+ * Split-combine mode of the current device: mode 1 = one launch where
+ * eligible (needs solort_init), 0 = always a second launch, -1 = query only.
+ * Returns the mode in effect (1 only when solort_init's check passed).  Both
+ * modes give the same bits.
+ */
+int solort_combine_mode(int mode);
 
 /*
  * Per-head QK-RMSNorm + RoPE prologue with the in-place KV-cache write.
@@ -116,19 +141,26 @@ int solort_rope_rows(const float* inv_freq, int half_dim, const int64_t* pos0_de
                      solort_stream_t stream);
 
 /* Workspace bytes needed by solort_decode_attn / solort_verify_attn /
- * solort_decode_layer for `nq` query tokens and `n_split` key splits: the
- * splits' partial results (per KV head and split: running max and sum, and
- * the unnormalised [nq * group][128] output, fp32).  The caller allocates it
- * once and reuses it; its contents need no initialisation.  A workspace sized
- * for (nq, n_split) serves any call with the same nh/nkv and no larger nq or
- * n_split.  Calls that overlap in time must not share a workspace. */
+ * solort_decode_layer for `nq` query tokens and `n_split` key splits: 16 KB
+ * of per-KV-head tickets of the single-launch combine, then the splits'
+ * partial results (per KV head and split: running max and sum, and the
+ * unnormalised [nq * group][128] output, fp32).  The caller allocates it
+ * once, zero-fills it once and reuses it (the kernels leave the tickets at
+ * zero).  A workspace sized for (nq, n_split) serves any call with the same
+ * nh/nkv and no larger nq or n_split.  Calls that overlap in time must not
+ * share a workspace. */
 size_t solort_attn_workspace_bytes(int nq, int nh, int nkv, int hd, int n_split);
 
 /*
  * Grouped-query attention of `nq` new tokens over the static KV cache, split
- * across `n_split` workgroups per KV head (flash-decoding), followed by the
- * log-sum-exp combine of the splits in a second launch on the same stream
- * (none when n_split is 1).
+ * across `n_split` workgroups per KV head (flash-decoding), and the
+ * log-sum-exp combine of the splits (none when n_split is 1).  The combine
+ * runs inside the same launch -- the last split of each KV head to finish
+ * merges the head's partials, which meet in the L2 of the XCD all of that
+ * head's splits run on -- for long chunks: when solort_init's placement check
+ * passed, nkv is a multiple of 8, n_split <= 32, nq * (nh / nkv) <= 8 and
+ * each split covers at least 512 keys; otherwise (where a second launch is
+ * cheaper) as a second launch on the same stream.
  * Replaces the decode block cuda_graph_executor.py:168, :180-184 (nq = 1:
  * softmax(q K^T * scale, keys > pos masked) V over the bucket) and the verify
  * block :247-250, :261-263 (nq = K+1, query t at position pos0+t sees keys
@@ -238,8 +270,10 @@ int solort_paged_kv_gather(const void* k_pages, const void* v_pages, int64_t pag
  * positions 0..T-1, with K/V read from cache rows 0..T-1 (written first by
  * solort_qknorm_rope_kvwrite, as the reference writes them at :122-123).
  * q   [T, nh, 128] bf16; out [T, nh * 128] bf16 or fp32.  T <= max_len.
- * Query groups g = nh / nkv of 1, 2 or 4.  Probabilities enter the second
- * matrix product rounded to bf16 (accumulation and softmax are fp32).
+ * Query groups g = nh / nkv of 1, 2 or 4.  Accumulation and softmax are
+ * fp32; with a bf16 output the probabilities enter the second matrix product
+ * rounded to bf16, with an fp32 output as bf16 high + low parts (~16 bits),
+ * which keeps it within 1e-4 of exact attention over the same bf16 q/K/V.
  */
 int solort_prefill_attn(const void* q, int T, int nh, int nkv, int hd, const void* k_cache,
                         const void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride,
@@ -342,6 +376,21 @@ size_t solort_argmax_workspace_bytes(int rows);
  */
 int solort_argmax_rows(const void* logits, int dtype, int rows, int64_t vocab, int64_t row_stride,
                        int64_t* out_idx, void* ws, solort_stream_t stream);
+
+/*
+ * Device probes (no counterpart in the reference): the launch and streaming
+ * floor a latency-bound call on this device is compared with.
+ * probe_placement: out[2b] = XCD index, out[2b + 1] = HW_ID register of
+ *   workgroup b of an n_wg-workgroup launch (out: 2 * n_wg words).
+ * probe_empty: an empty kernel of n_wg workgroups of 64 threads.
+ * probe_read: streams nbytes (a multiple of 16) from src with n_wg
+ *   workgroups of 256 threads, in_flight (1, 2 or 4) 16-byte loads in flight
+ *   per thread; workgroup b writes one word to sink[b] (sink: n_wg words).
+ */
+int solort_probe_placement(uint32_t* out, int n_wg, solort_stream_t stream);
+int solort_probe_empty(int n_wg, solort_stream_t stream);
+int solort_probe_read(const void* src, int64_t nbytes, int n_wg, int in_flight, uint32_t* sink,
+                      solort_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -101,6 +101,19 @@ def attn_fp64(q: np.ndarray, keys: np.ndarray, vals: np.ndarray, scale: float) -
     return p @ np.asarray(vals, np.float64)
 
 
+def causal_attn_fp64(q: np.ndarray, keys: np.ndarray, vals: np.ndarray, scale: float) -> np.ndarray:
+    """Top-left causal attention in fp64, one head: row t of q [T,hd] attends keys/vals 0..t
+    (cuda_graph_executor.py:124-130, SDPA is_causal=True over positions 0..T-1).  Returns [T,hd]."""
+    q = np.asarray(q, np.float64)
+    T = q.shape[0]
+    s = (q @ np.asarray(keys, np.float64)[:T].T) * scale
+    s[np.triu_indices(T, 1)] = -np.inf
+    s -= s.max(axis=-1, keepdims=True)
+    p = np.exp(s)
+    p /= p.sum(axis=-1, keepdims=True)
+    return p @ np.asarray(vals, np.float64)[:T]
+
+
 def causal_decode_fp64(q: np.ndarray, kc_l: np.ndarray, vc_l: np.ndarray, pos0: int, scale: float) -> np.ndarray:
     """Query t (q [nq,nh,hd]) at position pos0+t attends cache rows 0..pos0+t of its KV head h // g.
 

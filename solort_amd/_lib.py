@@ -15,12 +15,18 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before ours)
 
 LIB_PATH = Path(__file__).resolve().parent / "libsolort_hip.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 # name -> (restype, argtypes); mirrors include/solort_hip.h
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "solort_abi_version": (c_int, []),
+    "solort_source_id": (ctypes.c_uint64, []),
     "solort_last_error": (ctypes.c_char_p, []),
+    "solort_init": (c_int, []),
+    "solort_combine_mode": (c_int, [c_int]),
+    "solort_probe_placement": (c_int, [c_void_p, c_int, c_void_p]),
+    "solort_probe_empty": (c_int, [c_int, c_void_p]),
+    "solort_probe_read": (c_int, [c_void_p, c_int64, c_int, c_int, c_void_p, c_void_p]),
     "solort_qknorm_rope_kvwrite": (
         c_int,
         [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p,
@@ -96,12 +102,39 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
 }
 
 _lib: ctypes.CDLL | None = None
+_init_devices: set[int] = set()
+
+
+def _source_id() -> int | None:
+    """The hash the build compiles into the library, over the sources present next to this
+    package (None when they are not shipped)."""
+    from . import build
+    if not build.CSRC.is_dir():
+        return None
+    return build.source_id()
+
+
+def _init_device(lib: ctypes.CDLL) -> None:
+    """solort_init once per device, outside graph capture (it synchronises): checks the
+    workgroup placement the single-launch split combine relies on."""
+    if not torch.cuda.is_available():
+        return
+    dev = torch.cuda.current_device()
+    if dev in _init_devices or torch.cuda.is_current_stream_capturing():
+        return
+    rc = lib.solort_init()
+    if rc != 0:
+        raise RuntimeError(f"solort_init failed ({rc}): {lib.solort_last_error().decode(errors='replace')}")
+    _init_devices.add(dev)
 
 
 def load() -> ctypes.CDLL:
-    """Loads (once) and returns the library; raises RuntimeError if it is missing."""
+    """Loads (once) and returns the library, initialised for the current device; raises
+    RuntimeError if it is missing, of another ABI, or built from other sources."""
     global _lib
     if _lib is not None:
+        if torch.cuda.is_available() and torch.cuda.current_device() not in _init_devices:
+            _init_device(_lib)
         return _lib
     if not LIB_PATH.exists():
         raise RuntimeError(
@@ -115,6 +148,11 @@ def load() -> ctypes.CDLL:
     ver = lib.solort_abi_version()
     if ver != ABI_VERSION:
         raise RuntimeError(f"{LIB_PATH} has ABI {ver}, expected {ABI_VERSION}; rebuild it")
+    sid = _source_id()
+    if sid is not None and lib.solort_source_id() != sid:
+        raise RuntimeError(f"{LIB_PATH} was built from other sources than those in {LIB_PATH.parent / 'csrc'}; "
+                           "rebuild it (python -m solort_amd.build)")
+    _init_device(lib)
     _lib = lib
     return lib
 

@@ -45,16 +45,31 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
+def source_id() -> int:
+    """64-bit hash of every source the library is built from (csrc/*.hip, csrc/*.h,
+    include/*.h): compiled into the library and compared by the loader, which refuses
+    a library built from other sources."""
+    import hashlib
+    h = hashlib.sha256()
+    files = sorted([*CSRC.glob("*.hip"), *CSRC.glob("*.h"), *(PKG.parent / "include").glob("*.h")])
+    for f in files:
+        h.update(f.name.encode())
+        h.update(b"\0")
+        h.update(f.read_bytes())
+        h.update(b"\0")
+    return int.from_bytes(h.digest()[:8], "little")
+
+
 # Per-source extra flags.  prefill.hip: MFMA results stay in architectural
 # VGPRs, where the softmax reads and rescales them, instead of AGPRs that
 # every VALU access would first have to copy out.
 EXTRA_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
-def _compile(src: Path) -> Path:
+def _compile(src: Path, sid: int) -> Path:
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), "-I", str(PKG.parent / "include"), "-c",
-           str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), f"-DSOLORT_SOURCE_ID={sid}ULL", "-I",
+           str(PKG.parent / "include"), "-c", str(src), "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")
@@ -66,8 +81,9 @@ def build(verbose: bool = False) -> Path:
     OBJ_DIR.mkdir(exist_ok=True)
     srcs = sources()
     jobs = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
+    sid = source_id()
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(_compile, srcs))
+        objs = list(ex.map(lambda f: _compile(f, sid), srcs))
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -26,6 +26,18 @@ int check_launch(const char* what) {
 
 }  // namespace solort
 
-extern "C" int solort_abi_version(void) { return 8; }
+extern "C" int solort_abi_version(void) { return 9; }
+
+#ifndef SOLORT_SOURCE_ID
+#define SOLORT_SOURCE_ID 0ULL
+#endif
+extern "C" uint64_t solort_source_id(void) { return SOLORT_SOURCE_ID; }
+
+extern "C" int solort_init(void) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return solort::set_error((int)e, "init: no device: %s", hipGetErrorString(e));
+  return solort::verify_xcd_placement(dev);
+}
 
 extern "C" const char* solort_last_error(void) { return g_err; }

@@ -21,6 +21,13 @@ int check_prologue(const char* name, const void* qkv, int64_t qkv_row_stride, in
                    const void* qn_w, const void* kn_w, const void* rope_src, const void* q_out, const void* k_cache,
                    const void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride, int64_t max_len);
 
+// probe.hip: runs the workgroup-placement probe on device `dev` (current)
+// and records whether workgroup b always runs on the XCD of workgroup b % 8;
+// synchronous.  0 or the error code.
+int verify_xcd_placement(int dev);
+// probe.hip: whether that check passed on device `dev`.
+bool xcd_round_robin(int dev);
+
 // prologue.hip: QK-RMSNorm + RoPE of the K rows and the cache write of the K
 // and V rows of T tokens at positions 0..T-1 (no q rows), cos/sin from a
 // solort_rope_rows table; arguments already validated.

@@ -76,6 +76,9 @@ struct DecodeTail {
   int64_t page_stride;
   int page_shift;
   int num_pages;
+  // Single-launch combine (null: the combine kernel runs as a second launch): per KV head a
+  // 64-bit ticket, 128 bytes apart, zero between launches.
+  unsigned long long* tickets;
 };
 
 // Element offset of the cache row at position t (head 0, dim 0).  Paged: a
@@ -123,6 +126,169 @@ __device__ __forceinline__ void store_out2(void* out, int out_f32, int nh, int k
     *reinterpret_cast<float2*>(reinterpret_cast<float*>(out) + oi) = make_float2(o0, o1);
   else
     *reinterpret_cast<uint32_t*>(reinterpret_cast<uint16_t*>(out) + oi) = f2bf(o0) | (f2bf(o1) << 16);
+}
+
+// ---------------------------------------------------------------- split combine
+// The log-sum-exp combine of the n_split partials of one KV head: thread =
+// (float4 column c of the head's [R][128] output, split group sg of 8) merges
+// splits sg, sg + 8, ... on its own (up to kCombB loads in flight per batch),
+// then the 8 split groups meet once in LDS.  The combine kernel runs 32
+// columns per workgroup; the single-launch combine (the last split of the
+// head to finish) runs all of the head's columns at once.  Both use these
+// functions, so both give the same bits.
+
+constexpr int kCombB = 8;  // splits per thread per batch (combine kernel)
+
+struct CombAcc {
+  float m, l;  // max (log2 units) and sum of the merged splits
+  float4 o;    // their unnormalised output column
+};
+
+__device__ __forceinline__ CombAcc comb_init() { return CombAcc{-INFINITY, 0.f, make_float4(0.f, 0.f, 0.f, 0.f)}; }
+
+// Folds a batch of B partials (max -inf: an empty or absent split) into acc.
+// Branch-free, so that the compiler keeps every load of the batch ahead of
+// it: with no split seen yet (mb = -inf) all weights are 0 and acc stays
+// (m = -inf, l = 0, o = 0).
+template <int B>
+__device__ __forceinline__ void comb_merge(CombAcc& acc, const float2 (&ml)[B], const float4 (&ov)[B]) {
+  float mb = acc.m;
+#pragma unroll
+  for (int k = 0; k < B; ++k) mb = fmaxf(mb, ml[k].x);
+  const float mr = mb == -INFINITY ? 0.f : mb;  // reference for the weights
+  const float sc = fast_exp2(acc.m - mr);       // acc.m = -inf gives 0
+  acc.l *= sc;
+  acc.o.x *= sc; acc.o.y *= sc; acc.o.z *= sc; acc.o.w *= sc;
+#pragma unroll
+  for (int k = 0; k < B; ++k) {
+    const float w = (ml[k].x == -INFINITY) ? 0.f : fast_exp2(ml[k].x - mr);
+    acc.l = fmaf(w, ml[k].y, acc.l);
+    acc.o = f4fma(w, ov[k], acc.o);
+  }
+  acc.m = mb;
+}
+
+// The 8 split groups of one column, [8][n_cols] in LDS (s_m, s_l, s_o), folded
+// in group order; returns the normalised column.
+__device__ __forceinline__ float4 comb_final(const float* s_m, const float* s_l, const float4* s_o, int n_cols,
+                                             int c) {
+  float Mx = -INFINITY;
+#pragma unroll
+  for (int g = 0; g < 8; ++g) Mx = fmaxf(Mx, s_m[g * n_cols + c]);
+  float Ls = 0.f;
+  float4 Os = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (Mx != -INFINITY) {
+#pragma unroll
+    for (int g = 0; g < 8; ++g) {
+      const float mg = s_m[g * n_cols + c];
+      const float w = (mg == -INFINITY) ? 0.f : fast_exp2(mg - Mx);
+      Ls = fmaf(w, s_l[g * n_cols + c], Ls);
+      Os = f4fma(w, s_o[g * n_cols + c], Os);
+    }
+  }
+  const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+  Os.x *= inv; Os.y *= inv; Os.z *= inv; Os.w *= inv;
+  return Os;
+}
+
+// Loads that miss the CU's L1 and hit the XCD's L2 (cache policy sc0): the
+// partials of the other splits of a head were stored by other CUs of the same
+// XCD during this launch.
+__device__ __forceinline__ float4 ld_l2_f4(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 1));
+}
+__device__ __forceinline__ float2 ld_l2_f2(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 1));
+}
+
+constexpr int kFuseMaxSplit = 32;   // single-launch combine: splits per head (4 per split group)
+constexpr int kFuseMaxRows = 8;     // ... query rows per KV head
+constexpr int kFuseMinChunk = 512;  // ... and keys per split (the MFMA split kernel's long chunks)
+
+// Bytes of LDS the single-launch combine of R rows needs: [8][32 R] max, sum, output.
+constexpr int fuse_lds_bytes(int R) { return R <= kFuseMaxRows ? 8 * 32 * R * (4 + 4 + 16) : 0; }
+
+// The end of a split block in single-launch mode, after its partial is
+// stored: the block takes the head's ticket; the last split of the head to
+// arrive merges all of its partials and writes the head's output rows.
+//
+// Every split of a head runs on one XCD: blocks (kvh, split) have linear
+// index kvh + nkv * split, nkv is a multiple of 8, and workgroup b runs on
+// the XCD of workgroup b % 8 (round-robin dispatch, checked by solort_init).
+// So the partials meet in that XCD's L2: each block waits until its stores
+// are acknowledged (by the L2), then adds to the ticket; the last one reads
+// the partials past its L1.  No cache writeback or invalidate is needed.
+// The ticket adds 1 << (8 xcc) per block, so the last block also sees that
+// every split ran on its own XCD; if not (placement other than checked), it
+// writes NaN rather than a result built from partials it cannot see.  It
+// then clears the ticket for the next launch.  lds: fuse_lds_bytes(R) bytes.
+template <int R>
+__device__ __forceinline__ void single_launch_combine(const DecodeTail& a, int kvh, int NS, int nh, int G,
+                                                      uint8_t* lds) {
+  static_assert(R <= kFuseMaxRows, "single-launch combine serves at most 8 rows per KV head");
+  constexpr int C = R * 32;  // float4 columns of the head's output
+  constexpr int NB = kFuseMaxSplit / 8;
+  __shared__ int s_last;
+  const int tid = threadIdx.x;
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial stores are in the L2
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t xcc = __builtin_amdgcn_s_getreg(20 | (0 << 6) | ((16 - 1) << 11)) & 7u;
+    unsigned long long* t = a.tickets + (size_t)kvh * 16;
+    const unsigned long long mine = 1ull << (8 * xcc);
+    const unsigned long long now =
+        __hip_atomic_fetch_add(t, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + mine;
+    unsigned total = 0;
+#pragma unroll
+    for (int x = 0; x < 8; ++x) total += (unsigned)(now >> (8 * x)) & 0xffu;
+    const bool last = total == (unsigned)NS;
+    const bool same = ((now >> (8 * xcc)) & 0xffu) == (unsigned long long)NS;
+    if (last) __hip_atomic_store(t, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = last ? (same ? 1 : 2) : 0;
+  }
+  __syncthreads();
+  const int last = s_last;
+  if (last == 0) return;
+  const int c = tid & 31, sg = tid >> 5;
+  const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_o + (size_t)kvh * NS * C * 4, (short)0, NS * C * 16, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
+      a.ws_ml + (size_t)kvh * NS * R * 2, (short)0, NS * R * 8, 0x00020000);
+  float* s_m = reinterpret_cast<float*>(lds);
+  float* s_l = s_m + 8 * C;
+  float4* s_o = reinterpret_cast<float4*>(s_l + 8 * C);
+  // All loads first, unconditionally (splits past NS lie past the buffer
+  // ranges and read as zeros): column 32 p + c (row p) of splits sg + 8 k.
+  float2 ml[R][NB];
+  float4 ov[R][NB];
+#pragma unroll
+  for (int p = 0; p < R; ++p)
+#pragma unroll
+    for (int k = 0; k < NB; ++k) {
+      const int s = sg + 8 * k;
+      ml[p][k] = ld_l2_f2(rm, (s * R + p) * 8);
+      ov[p][k] = ld_l2_f4(ro, (s * C + 32 * p + c) * 16);
+    }
+#pragma unroll
+  for (int p = 0; p < R; ++p)
+#pragma unroll
+    for (int k = 0; k < NB; ++k)
+      if (sg + 8 * k >= NS) ml[p][k].x = -INFINITY;  // an absent split
+#pragma unroll
+  for (int p = 0; p < R; ++p) {
+    CombAcc acc = comb_init();
+    comb_merge<NB>(acc, ml[p], ov[p]);
+    const int col = 32 * p + c;
+    s_m[sg * C + col] = acc.m;
+    s_l[sg * C + col] = acc.l;
+    s_o[sg * C + col] = acc.o;
+  }
+  __syncthreads();
+  for (int col = tid; col < C; col += 256) {
+    float4 v = comb_final(s_m, s_l, s_o, C, col);
+    if (last == 2) v = make_float4(NAN, NAN, NAN, NAN);
+    store_out(a.out, a.out_f32, nh, kvh, G, col, v);
+  }
 }
 
 // Lane-parallel split kernel, for short key chunks (latency-bound: one to a
@@ -721,10 +887,9 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
       }
     }
     m = mt;
-  } else if (wave > 0) {
-    return;
   }
-  if (l32 >= R) return;
+  // With one active wave only wave 0 writes; rows past R are padding.
+  const bool writer = (nact > 1 || wave == 0) && l32 < R;
   const int r = l32;
   // Writes dims 32dt .. 32dt + 31 of row r (this lane's 16 of them) from od.
   auto write_dims = [&](const f32x16& od, int dt) {
@@ -753,17 +918,24 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
                                                                od[4 * q4 + 3]);
     }
   };
-  if (nact > 1) {
-    write_dims(om, wave);
-  } else {
-    write_dims(o[0], 0);
-    write_dims(o[1], 1);
-    write_dims(o[2], 2);
-    write_dims(o[3], 3);
+  if (writer) {
+    if (nact > 1) {
+      write_dims(om, wave);
+    } else {
+      write_dims(o[0], 0);
+      write_dims(o[1], 1);
+      write_dims(o[2], 2);
+      write_dims(o[3], 3);
+    }
+    if (NS > 1 && hi == 0 && (nact == 1 || wave == 0))
+      *reinterpret_cast<float2*>(a.ws_ml + ((int64_t)(kvh * NS + split) * R + r) * 2) =
+          make_float2(m == -INFINITY ? m : m * qs, lsum);
   }
-  if (NS > 1 && hi == 0 && (nact == 1 || wave == 0))
-    *reinterpret_cast<float2*>(a.ws_ml + ((int64_t)(kvh * NS + split) * R + r) * 2) =
-        make_float2(m == -INFINITY ? m : m * qs, lsum);
+  if constexpr (R <= kFuseMaxRows) {
+    // s_x is free: the merge above read it before its last barrier, and the
+    // combine's first barrier comes before any of its LDS writes.
+    if (NS > 1 && a.tickets) single_launch_combine<R>(a, kvh, NS, nh, G, s_x);
+  }
 }
 
 // Arguments as the entry points pass them: the leading 14 dwords arrive
@@ -792,19 +964,19 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_packed_kernel(uint16_t* kc
                                        (nh + 2 * (nh / G)) * SOLORT_HD, nh, qn_w, kn_w, rope_cs, a);
 }
 
-// The log-sum-exp combine of the n_split partials of each KV head.  Grid
-// (nkv, column blocks): block = (KV head, 32 float4 columns of its [R][128]
-// output); thread = (column, split group sg of 8): it merges splits sg,
-// sg+8, ... on its own (all loads issued together), then the 8 split groups
-// meet once in LDS.  Every argument is preloaded.
+// The combine kernel (two-launch mode): the log-sum-exp combine of the
+// n_split partials of each KV head.  Grid (nkv, column blocks): block = (KV
+// head, 32 float4 columns of its [R][128] output); thread = (column, split
+// group sg of 8): it merges splits sg, sg+8, ... on its own, kCombB at a time
+// (all loads of a batch issued together), then the 8 split groups meet once
+// in LDS.  Every argument is preloaded.
 template <int NQ, int G>
 __global__ __launch_bounds__(256) void combine_kernel(const float* ws_o, const float* ws_ml, void* out, int nh,
                                                       int n_split, int out_f32) {
   constexpr int R = NQ * G;
   constexpr int C = R * 32;  // float4 columns
-  constexpr int B = 8;       // splits per thread per batch
-  __shared__ float s_m[8][32], s_l[8][32];
-  __shared__ float4 s_o[8][32];
+  __shared__ float s_m[8 * 32], s_l[8 * 32];
+  __shared__ float4 s_o[8 * 32];
   const int tid = threadIdx.x, c = tid & 31, sg = tid >> 5;
   const int kvh = blockIdx.x, cb = blockIdx.y;
   const int col = cb * 32 + c;
@@ -813,13 +985,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* ws_o, const f
   const int NS = n_split;
   const float2* wml = reinterpret_cast<const float2*>(ws_ml) + (int64_t)kvh * NS * R;
   const float4* wo = reinterpret_cast<const float4*>(ws_o) + (int64_t)kvh * NS * C;
-  float mloc = -INFINITY, lloc = 0.f;
-  float4 oloc = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (int s0 = sg; s0 < NS; s0 += 8 * B) {
-    float2 ml[B];
-    float4 ov[B];
+  CombAcc acc = comb_init();
+  for (int s0 = sg; s0 < NS; s0 += 8 * kCombB) {
+    float2 ml[kCombB];
+    float4 ov[kCombB];
 #pragma unroll
-    for (int k = 0; k < B; ++k) {
+    for (int k = 0; k < kCombB; ++k) {
       const int s = s0 + 8 * k;
       if (act && s < NS) {
         ml[k] = wml[(int64_t)s * R + r];
@@ -829,44 +1000,13 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* ws_o, const f
         ov[k] = make_float4(0.f, 0.f, 0.f, 0.f);
       }
     }
-    float mb = mloc;
-#pragma unroll
-    for (int k = 0; k < B; ++k) mb = fmaxf(mb, ml[k].x);
-    if (mb != -INFINITY) {
-      const float sc = fast_exp2(mloc - mb);  // mloc = -inf gives 0
-      lloc *= sc;
-      oloc.x *= sc; oloc.y *= sc; oloc.z *= sc; oloc.w *= sc;
-#pragma unroll
-      for (int k = 0; k < B; ++k) {
-        const float w = (ml[k].x == -INFINITY) ? 0.f : fast_exp2(ml[k].x - mb);
-        lloc = fmaf(w, ml[k].y, lloc);
-        oloc = f4fma(w, ov[k], oloc);
-      }
-      mloc = mb;
-    }
+    comb_merge<kCombB>(acc, ml, ov);
   }
-  s_m[sg][c] = mloc;
-  s_l[sg][c] = lloc;
-  s_o[sg][c] = oloc;
+  s_m[sg * 32 + c] = acc.m;
+  s_l[sg * 32 + c] = acc.l;
+  s_o[sg * 32 + c] = acc.o;
   __syncthreads();
-  if (tid < 32 && act) {
-    float Mx = -INFINITY;
-#pragma unroll
-    for (int g = 0; g < 8; ++g) Mx = fmaxf(Mx, s_m[g][c]);
-    float Ls = 0.f;
-    float4 Os = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (Mx != -INFINITY) {
-#pragma unroll
-      for (int g = 0; g < 8; ++g) {
-        const float w = (s_m[g][c] == -INFINITY) ? 0.f : fast_exp2(s_m[g][c] - Mx);
-        Ls = fmaf(w, s_l[g][c], Ls);
-        Os = f4fma(w, s_o[g][c], Os);
-      }
-    }
-    const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
-    Os.x *= inv; Os.y *= inv; Os.z *= inv; Os.w *= inv;
-    store_out(out, out_f32, nh, kvh, G, col, Os);
-  }
+  if (tid < 32 && act) store_out(out, out_f32, nh, kvh, G, col, comb_final(s_m, s_l, s_o, 32, c));
 }
 
 // ---------------------------------------------------------------- host side
@@ -890,6 +1030,13 @@ struct DecodeArgs {
   DecodeTail tail;
 };
 
+// Workspace: the single-launch tickets (128 bytes per KV head, for up to
+// kTicketHeads heads, at a fixed offset so that calls of any shape sharing a
+// workspace agree on them; zero between launches), then the splits' (max,
+// sum) pairs and unnormalised outputs.
+constexpr int kTicketHeads = 128;
+constexpr size_t kTicketBytes = (size_t)kTicketHeads * 128;
+
 struct WsLayout {
   size_t ml_off, o_off, total;
 };
@@ -899,10 +1046,33 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 static WsLayout ws_layout(int nq, int nh, int nkv, int n_split) {
   const size_t R = (size_t)nq * (nh / nkv);
   WsLayout w;
-  w.ml_off = 0;
-  w.o_off = align256((size_t)nkv * n_split * R * 2 * sizeof(float));
+  w.ml_off = kTicketBytes;
+  w.o_off = align256(w.ml_off + (size_t)nkv * n_split * R * 2 * sizeof(float));
   w.total = align256(w.o_off + (size_t)nkv * n_split * R * 128 * sizeof(float));
   return w;
+}
+
+// Single-launch combine, per device: on once solort_init has checked the
+// workgroup placement (probe.hip), unless switched off by solort_combine_mode.
+namespace {
+constexpr int kMaxDev = 64;
+int g_combine_off[kMaxDev];
+}  // namespace
+
+// The single launch saves the combine kernel's launch but adds, to the split
+// kernel, a wait for the partials' stores, a device-scope ticket round trip
+// and the last split's reads of the partials: measured on MI355X (Qwen3
+// shapes), +1.0 us for the ticket and +1.7 us for the merge.  That beats a
+// second launch only after a long split kernel (Qwen3-8B at KV 32768, 32
+// splits of 1024 keys: 31.3 against 32.3 us per call); after the short
+// lane-parallel kernel the second launch is cheaper (KV 1024: 5.93 against
+// 6.21 us), so only MFMA-kernel chunks of at least kFuseMinChunk keys use it.
+static bool single_launch_ok(int nq, int nh, int nkv, int n_split, bool lanes, int chunk) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return false;
+  const int R = nq * (nh / nkv);
+  return !g_combine_off[dev] && xcd_round_robin(dev) && n_split > 1 && n_split <= kFuseMaxSplit &&
+         R <= kFuseMaxRows && nkv % 8 == 0 && nkv <= kTicketHeads && !lanes && chunk >= kFuseMinChunk;
 }
 
 template <int NQ, int G, bool FUSED, bool PAGED>
@@ -1075,6 +1245,7 @@ static int prepare(const char* name, int nq, int nh, int nkv, int hd, void* k_ca
   a.tail.pos0_dev = pos0_dev;
   a.tail.ws_o = (float*)((char*)ws + w.o_off);
   a.tail.ws_ml = (float*)((char*)ws + w.ml_off);
+  a.tail.tickets = single_launch_ok(nq, nh, nkv, n_split, a.lanes, a.chunk) ? (unsigned long long*)ws : nullptr;
   a.tail.out = out;
   a.tail.qscale = scale * 1.4426950408889634f;
   a.tail.pos_limit = (int)max_len;
@@ -1088,7 +1259,7 @@ static int launch_all(const char* name, bool fused, int nq, const DecodeArgs& a,
   if (!dispatch_attn(G, nq, fused, a, s))
     return set_error(SOLORT_EINVAL, "%s: no kernel for nq=%d group=%d", name, nq, G);
   int rc = check_launch(name);
-  if (rc || a.n_split == 1) return rc;
+  if (rc || a.n_split == 1 || a.tail.tickets) return rc;
   if (!dispatch_combine(G, nq, a, s))
     return set_error(SOLORT_EINVAL, "%s: no combine kernel for nq=%d group=%d", name, nq, G);
   return check_launch(name);
@@ -1112,6 +1283,15 @@ static int attn_impl(const char* name, const void* q, int nq, int nh, int nkv, i
 }  // namespace solort
 
 using namespace solort;
+
+extern "C" int solort_combine_mode(int mode) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev)
+    return set_error(SOLORT_EINVAL, "combine_mode: no current device");
+  if (mode != -1 && mode != 0 && mode != 1) return set_error(SOLORT_EINVAL, "combine_mode: mode %d", mode);
+  if (mode >= 0) g_combine_off[dev] = mode == 0;
+  return !g_combine_off[dev] && xcd_round_robin(dev) ? 1 : 0;
+}
 
 extern "C" size_t solort_attn_workspace_bytes(int nq, int nh, int nkv, int hd, int n_split) {
   if (nq < 1 || nh <= 0 || nkv <= 0 || nh % nkv || hd != SOLORT_HD || n_split < 1) return 0;

@@ -20,8 +20,10 @@
 //   online softmax in fp32 with a lazy maximum: a row's reference max moves
 //                 only when a block's max exceeds it by more than 8 (log2
 //                 units), so p = 2^(s*c - m*c) <= 2^8 (c = scale*log2(e))
-//                 and O is rarely rescaled; P is rounded to bf16 and the row
-//                 sum adds the rounded P (v_dot2_f32_bf16)
+//                 and O is rarely rescaled; bf16 output: P is rounded to bf16
+//                 and the row sum adds the rounded P (v_dot2_f32_bf16); fp32
+//                 output: P enters as bf16 high + low parts (two MFMAs) and
+//                 the row sum adds P in fp32
 //   O^T += V^T P^T  A = V^T from the row-major V tile by ds_read_b64_tr_b16,
 //                 B = P^T straight from the S^T registers, 4 dim tiles x 4
 //                 key steps
@@ -286,16 +288,26 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
       const float mn = bump ? mx : m;
       const float mq = mn == -INFINITY ? 0.f : mn * qs;
       const float alpha = (bump && m != -INFINITY) ? fast_exp2(m * qs - mq) : 1.f;
-      // p in bf16 pairs; the row sum adds the rounded p that weigh V.
+      // p in bf16 pairs.  bf16 output: p enters P V rounded to bf16 and the row
+      // sum adds the rounded p.  fp32 output: p enters as a bf16 high part plus
+      // the bf16 remainder (two MFMAs, ~16 bits of p) and the row sum adds p in
+      // fp32, which keeps the output within 1e-4 of exact attention.
       float ps = 0.f;
-      uint32_t pk[2][8];  // bf16 pairs of p: [kt][i / 2]
+      uint32_t pk[2][8];              // bf16 pairs of p (high parts): [kt][i / 2]
+      uint32_t pl[2][F32 ? 8 : 1];    // fp32 output: the remainders p - high
 #pragma unroll
       for (int kt = 0; kt < 2; ++kt)
 #pragma unroll
         for (int i = 0; i < 16; i += 2) {
-          const uint32_t pr = pack2(fast_exp2(fmaf(s[kt][i], qs, -mq)), fast_exp2(fmaf(s[kt][i + 1], qs, -mq)));
+          const float e0 = fast_exp2(fmaf(s[kt][i], qs, -mq)), e1 = fast_exp2(fmaf(s[kt][i + 1], qs, -mq));
+          const uint32_t pr = pack2(e0, e1);
           pk[kt][i >> 1] = pr;
-          ps = dot2bf(pr, 0x3f803f80u, ps);  // + p_lo + p_hi
+          if constexpr (F32) {
+            pl[kt][i >> 1] = pack2(e0 - __uint_as_float(pr << 16), e1 - __uint_as_float(pr & 0xffff0000u));
+            ps += e0 + e1;
+          } else {
+            ps = dot2bf(pr, 0x3f803f80u, ps);  // + p_lo + p_hi
+          }
         }
       lsum = fmaf(lsum, alpha, ps);
       if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {  // some row's reference max moved
@@ -323,6 +335,11 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
                                              pk[kt][4 * h + 3]));
       const bf16x8 va = as_bf16x8(make_uint4(vlo[q].x, vlo[q].y, vup[q].x, vup[q].y));
       o[q & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pb, o[q & 3], 0, 0, 0);
+      if constexpr (F32) {
+        const bf16x8 pbl = as_bf16x8(make_uint4(pl[kt][4 * h], pl[kt][4 * h + 1], pl[kt][4 * h + 2],
+                                                pl[kt][4 * h + 3]));
+        o[q & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(va, pbl, o[q & 3], 0, 0, 0);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   }

@@ -1,0 +1,119 @@
+// Device probes: where workgroups run, and the launch / streaming floor that
+// bounds a latency-bound call on this device.
+//
+// None of these has a counterpart in the reference; bench.py uses them to
+// measure the floor a decode-attention call is compared with, and the
+// library uses the placement probe once per device (solort_init) before it
+// relies on the workgroup -> XCD placement for the single-launch split
+// combine (decode.hip).
+#include <mutex>
+
+#include "common.h"
+#include "capi_internal.h"
+
+namespace solort {
+
+// hwreg(HW_REG_XCC_ID, 0, 16): the index of the accelerator complex die
+// (XCD) the wave runs on; hwreg(HW_REG_HW_ID): CU, SIMD and wave slot.
+__device__ __forceinline__ uint32_t xcc_id() { return __builtin_amdgcn_s_getreg(20 | (0 << 6) | ((16 - 1) << 11)); }
+__device__ __forceinline__ uint32_t hw_id() { return __builtin_amdgcn_s_getreg(4 | (0 << 6) | ((32 - 1) << 11)); }
+
+__global__ __launch_bounds__(64) void placement_kernel(uint32_t* __restrict__ out) {
+  if (threadIdx.x == 0) {
+    out[2 * blockIdx.x] = xcc_id();
+    out[2 * blockIdx.x + 1] = hw_id();
+  }
+}
+
+__global__ __launch_bounds__(64) void empty_kernel() {}
+
+// Streaming read of n16 16-byte chunks, grid-stride, U loads in flight per
+// thread; each workgroup stores one word of the xor of what it read (so the
+// loads cannot be dropped).
+template <int U>
+__global__ __launch_bounds__(256) void read_kernel(const uint4* __restrict__ src, int64_t n16,
+                                                   uint32_t* __restrict__ sink) {
+  __shared__ uint32_t s_x[4];
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  uint32_t x = 0;
+  for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride * U) {
+    uint4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) v[u] = i + u * stride < n16 ? src[i + u * stride] : make_uint4(0u, 0u, 0u, 0u);
+#pragma unroll
+    for (int u = 0; u < U; ++u) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+  }
+  for (int m = 32; m >= 1; m >>= 1) x ^= __shfl_xor(x, m, 64);
+  if ((threadIdx.x & 63) == 0) s_x[threadIdx.x >> 6] = x;
+  __syncthreads();
+  if (threadIdx.x == 0) sink[blockIdx.x] = s_x[0] ^ s_x[1] ^ s_x[2] ^ s_x[3];
+}
+
+namespace {
+constexpr int kMaxDevices = 64;
+constexpr int kProbeBlocks = 2048;
+std::mutex g_mu;
+int g_xcd_state[kMaxDevices];  // 0 unknown, 1 verified round robin over 8, -1 not
+}  // namespace
+
+// Runs the placement probe on the current device and records whether
+// workgroup b always runs on the XCD of workgroup b % 8.  Synchronous: call
+// outside graph capture.
+int verify_xcd_placement(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return set_error(SOLORT_EINVAL, "init: device %d out of range", dev);
+  uint32_t* d = nullptr;
+  const size_t bytes = (size_t)kProbeBlocks * 2 * sizeof(uint32_t);
+  hipError_t e = hipMalloc((void**)&d, bytes);
+  if (e != hipSuccess) return set_error((int)e, "init: hipMalloc: %s", hipGetErrorString(e));
+  uint32_t h[kProbeBlocks * 2];
+  hipLaunchKernelGGL(placement_kernel, dim3(kProbeBlocks), dim3(64), 0, (hipStream_t)0, d);
+  e = hipGetLastError();
+  if (e == hipSuccess) e = hipMemcpy(h, d, bytes, hipMemcpyDeviceToHost);
+  hipFree(d);
+  if (e != hipSuccess) return set_error((int)e, "init: placement probe: %s", hipGetErrorString(e));
+  bool ok = true;
+  for (int b = 8; b < kProbeBlocks && ok; ++b) ok = h[2 * b] == h[2 * (b % 8)];
+  std::lock_guard<std::mutex> lk(g_mu);
+  g_xcd_state[dev] = ok ? 1 : -1;
+  return 0;
+}
+
+bool xcd_round_robin(int dev) {
+  if (dev < 0 || dev >= kMaxDevices) return false;
+  std::lock_guard<std::mutex> lk(g_mu);
+  return g_xcd_state[dev] == 1;
+}
+
+}  // namespace solort
+
+using namespace solort;
+
+extern "C" int solort_probe_placement(uint32_t* out, int n_wg, solort_stream_t stream) {
+  if (!out || ((uintptr_t)out & 3u)) return set_error(SOLORT_EINVAL, "probe_placement: out must be 4-byte aligned");
+  if (n_wg < 1 || n_wg > (1 << 20)) return set_error(SOLORT_EINVAL, "probe_placement: n_wg %d", n_wg);
+  hipLaunchKernelGGL(placement_kernel, dim3(n_wg), dim3(64), 0, (hipStream_t)stream, out);
+  return check_launch("probe_placement");
+}
+
+extern "C" int solort_probe_empty(int n_wg, solort_stream_t stream) {
+  if (n_wg < 1 || n_wg > (1 << 20)) return set_error(SOLORT_EINVAL, "probe_empty: n_wg %d", n_wg);
+  hipLaunchKernelGGL(empty_kernel, dim3(n_wg), dim3(64), 0, (hipStream_t)stream);
+  return check_launch("probe_empty");
+}
+
+extern "C" int solort_probe_read(const void* src, int64_t nbytes, int n_wg, int in_flight, uint32_t* sink,
+                                 solort_stream_t stream) {
+  if (!src || !sink || !aligned16(src) || ((uintptr_t)sink & 3u))
+    return set_error(SOLORT_EINVAL, "probe_read: src must be 16-byte and sink 4-byte aligned");
+  if (nbytes < 16 || nbytes % 16) return set_error(SOLORT_EINVAL, "probe_read: nbytes %lld", (long long)nbytes);
+  if (n_wg < 1 || n_wg > (1 << 20)) return set_error(SOLORT_EINVAL, "probe_read: n_wg %d", n_wg);
+  const int64_t n16 = nbytes / 16;
+  hipStream_t s = (hipStream_t)stream;
+  switch (in_flight) {
+    case 1: hipLaunchKernelGGL(read_kernel<1>, dim3(n_wg), dim3(256), 0, s, (const uint4*)src, n16, sink); break;
+    case 2: hipLaunchKernelGGL(read_kernel<2>, dim3(n_wg), dim3(256), 0, s, (const uint4*)src, n16, sink); break;
+    case 4: hipLaunchKernelGGL(read_kernel<4>, dim3(n_wg), dim3(256), 0, s, (const uint4*)src, n16, sink); break;
+    default: return set_error(SOLORT_EINVAL, "probe_read: in_flight %d not in {1, 2, 4}", in_flight);
+  }
+  return check_launch("probe_read");
+}

@@ -1,15 +1,11 @@
 """GPU parity of the MFMA causal prefill attention (with the prologue writing the cache first).
 
 Bars: bf16 output within max-abs 2e-2 / mean-abs 2e-3 of the reference's bf16
-SDPA (torch on CPU).  fp32 output against the fp64 evaluation of the kernel's
-own blockwise arithmetic (bf16 probabilities, oracle/exact.py
-prefill_blockwise): mean-abs <= 1e-5, at most 1% of the (row, head) outputs
-with an element off by more than 1e-4, max-abs <= 2e-2.  The stragglers are rare one-ulp flips in
-the bf16 rounding of a probability (the hardware exp2 is not correctly
-rounded, so fp64 cannot reproduce every rounding; one flip of p near 1 moves
-an output by up to 2^-8 * |V|); a wrong mask, scale or index shows up in the
-mean as errors of 1e-3 and more.  fp32 output against exact fp64 attention is
-reported.
+SDPA (torch on CPU); fp32 output within max-abs 1e-4 of exact fp64 causal
+attention over the same bf16 q/K/V (oracle/exact.py causal_attn_fp64), the
+fp32 yardstick for this path.  The bf16 output rounds the probabilities to
+bf16 before the second matrix product (and its row sums add the rounded
+values); the fp32 output feeds them as bf16 high + low parts.
 """
 from __future__ import annotations
 
@@ -25,6 +21,7 @@ from solort_amd import workloads as wl
 
 pytestmark = pytest.mark.gpu
 HD = 128
+F32_MAX = 1e-4
 
 
 def _say(msg):
@@ -68,28 +65,22 @@ def test_prefill_qwen3_4b(gpu, T):
     d = (out.float().cpu() - want.float()).abs()
     _say(f"  bf16 vs reference ops: max-abs {d.max().item():.3e} mean-abs {d.mean().item():.3e}")
     assert d.max().item() <= 2e-2 and d.mean().item() <= 2e-3
-    # fp32 output against the kernel's blockwise arithmetic and against exact attention, per head
+    # fp32 output against exact attention, per head
     qg = q.float().cpu().numpy()
     kg = kc.float().cpu().numpy()[:T]
     vg = vc.float().cpu().numpy()[:T]
     o32 = out32.cpu().numpy().reshape(T, sh.nh, HD)
-    worst_blk, sum_blk, worst_exact, n_far = 0.0, 0.0, 0.0, 0
+    worst, total = 0.0, 0.0
     for h in range(sh.nh):
         kvh = h // sh.group
-        blk = exact.prefill_blockwise(qg[:, h], kg[:, kvh], vg[:, kvh], sh.scale)
-        e = np.abs(o32[:, h] - blk)
-        worst_blk = max(worst_blk, float(e.max()))
-        sum_blk += float(e.sum())
-        n_far += int((e.max(axis=1) > 1e-4).sum())
-        if T <= 128:
-            ex = exact.causal_decode_fp64(qg[:, h][:, None, :], kg[:, kvh][:, None, :], vg[:, kvh][:, None, :], 0,
-                                          sh.scale)[:, 0]
-            worst_exact = max(worst_exact, float(np.abs(o32[:, h] - ex).max()))
-    mean_blk = sum_blk / o32.size
-    _say(f"  fp32 vs blockwise fp64: max-abs {worst_blk:.3e} mean-abs {mean_blk:.3e} rows-over-1e-4 {n_far}; "
-         f"vs exact fp64 (T<=128): {worst_exact:.3e}")
-    assert worst_blk <= 2e-2 and mean_blk <= 1e-5 and n_far <= 0.01 * T * sh.nh
-    assert torch.equal(out, out32.to(torch.bfloat16))
+        e = np.abs(o32[:, h] - exact.causal_attn_fp64(qg[:, h], kg[:, kvh], vg[:, kvh], sh.scale))
+        worst = max(worst, float(e.max()))
+        total += float(e.sum())
+    _say(f"  fp32 vs exact fp64: max-abs {worst:.3e} mean-abs {total / o32.size:.3e}")
+    assert worst <= F32_MAX
+    # the bf16 output's extra error is the bf16 rounding of p
+    d = (out.float() - out32).abs()
+    assert d.max().item() <= 2e-2 and d.mean().item() <= 2e-3
 
 
 def test_prefill_row0_and_last_row_pins(gpu):
@@ -106,8 +97,8 @@ def test_prefill_row0_and_last_row_pins(gpu):
     pos = torch.tensor([T - 1], dtype=torch.long, device=gpu)
     ops.decode_attn(q[T - 1:T].contiguous(), kc, vc, pos, 512, sh.scale, ws, 8, dec)
     torch.cuda.synchronize()
-    # decode keeps fp32 probabilities, prefill rounds them to bf16: equal to bf16 precision
-    assert torch.allclose(o[T - 1], dec.reshape(sh.nh, HD), atol=2e-2, rtol=0)
+    # both keep ~16 bits of every probability in their fp32 outputs
+    assert torch.allclose(o[T - 1], dec.reshape(sh.nh, HD), atol=F32_MAX, rtol=0)
 
 
 @pytest.mark.parametrize("shape", [wl.QWEN3_0_6B, wl.AttnShape("g1", 8, 8, 1)], ids=["g2", "g1"])
@@ -121,9 +112,8 @@ def test_prefill_other_groups(gpu, shape):
     o32 = out32.cpu().numpy().reshape(T, shape.nh, HD)
     for h in range(shape.nh):
         kvh = h // shape.group
-        blk = exact.prefill_blockwise(qg[:, h], kg[:, kvh], vg[:, kvh], shape.scale)
-        e = np.abs(o32[:, h] - blk)
-        assert e.max() <= 2e-2 and e.mean() <= 1e-5 and (e.max(axis=1) > 1e-4).sum() <= max(1, 0.01 * T), h
+        e = np.abs(o32[:, h] - exact.causal_attn_fp64(qg[:, h], kg[:, kvh], vg[:, kvh], shape.scale))
+        assert e.max() <= F32_MAX, (h, e.max())
 
 
 @pytest.mark.parametrize("T,shape", [(1, wl.QWEN3_4B), (17, wl.QWEN3_4B), (128, wl.QWEN3_4B), (333, wl.QWEN3_4B),

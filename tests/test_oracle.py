@@ -238,6 +238,22 @@ def test_prefill_ref_rows_pinned():
     assert np.allclose(out.double().numpy(), want, atol=1e-5)
 
 
+def test_causal_attn_fp64_equals_per_row_attention():
+    """The vectorised causal attention (one head, rows 0..T-1) equals the per-row fp64 evaluation
+    (causal_decode_fp64, each row over its own prefix); row 0 is V[0]; a wrong diagonal (row t seeing
+    t+1 keys, or only t) breaks the equality."""
+    g = np.random.default_rng(23)
+    for T in (1, 2, 17, 130):
+        q, k, v = (g.standard_normal((T, HD)) for _ in range(3))
+        got = exact.causal_attn_fp64(q, k, v, SCALE)
+        want = exact.causal_decode_fp64(q[:, None, :], k[:, None, :], v[:, None, :], 0, SCALE)[:, 0]
+        assert np.allclose(got, want, atol=1e-12)
+        assert np.allclose(got[0], v[0], atol=1e-12)
+        if T > 1:
+            shifted = exact.causal_decode_fp64(q[1:, None, :], k[:, None, :], v[:, None, :], 0, SCALE)[:, 0]
+            assert not np.allclose(got[1:], shifted, atol=1e-3)  # row t with only t keys
+
+
 def test_verify_equals_sequential_decode_steps():
     kc, vc = _small_cache(16, 300, 8, max_len=320)
     q = torch.randn(32, 5, HD)
