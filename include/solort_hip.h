@@ -66,7 +66,8 @@ const char* solort_last_error(void);
  * on the XCD (L2 domain) of workgroup b % 8, the round-robin placement of
  * MI355X, which the single-launch split combine relies on (see
  * solort_decode_attn).  Without it, or if the check fails, every split call
- * combines in a second launch.
+ * combines in a second launch.  It also looks up the device address of
+ * solort_decode_layer_noalloc's scratch array.
  */
 int solort_init(void);
 
@@ -210,6 +211,27 @@ int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int nq, int nh,
                         const int64_t* pos0_dev, void* k_cache, void* v_cache, int64_t kv_tok_stride,
                         int64_t kv_head_stride, int64_t max_len, int bound, float scale, void* ws,
                         int n_split, void* out, int out_dtype, solort_stream_t stream);
+
+/*
+ * solort_decode_layer without a workspace argument.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory (code
+ * under graph capture that must not call hipMalloc, tight serving loops,
+ * harnesses that forbid allocation).  The partials live in a fixed
+ * per-device array of SOLORT_NOALLOC_SCRATCH_BYTES (4 MiB) inside the
+ * library, held until the process ends; a call whose
+ * solort_attn_workspace_bytes(nq, nh, nkv, hd, n_split) exceeds it returns
+ * SOLORT_EINVAL.  It allocates nothing: the array's device address is looked
+ * up once per device (by solort_init, else by the first call on the device).
+ * All calls on one GPU share the array, so calls that overlap in time on one
+ * GPU race.  Results equal solort_decode_layer's with any workspace, bit for
+ * bit.  Other arguments as in solort_decode_layer.
+ */
+#define SOLORT_NOALLOC_SCRATCH_BYTES (4u << 20)
+int solort_decode_layer_noalloc(const void* qkv, int64_t qkv_row_stride, int nq, int nh, int nkv, int hd,
+                                const void* qn_w, const void* kn_w, float eps, const void* rope_cs,
+                                const int64_t* pos0_dev, void* k_cache, void* v_cache, int64_t kv_tok_stride,
+                                int64_t kv_head_stride, int64_t max_len, int bound, float scale, int n_split,
+                                void* out, int out_dtype, solort_stream_t stream);
 
 /*
  * solort_decode_layer over a paged KV cache: the layout of the reference's

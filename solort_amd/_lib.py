@@ -61,6 +61,11 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_float,
          c_void_p, c_int, c_void_p],
     ),
+    "solort_decode_layer_noalloc": (
+        c_int,
+        [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int, c_float, c_int, c_void_p, c_int, c_void_p],
+    ),
     "solort_paged_decode_layer": (
         c_int,
         [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p, c_void_p,

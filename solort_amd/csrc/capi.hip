@@ -37,7 +37,8 @@ extern "C" int solort_init(void) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return solort::set_error((int)e, "init: no device: %s", hipGetErrorString(e));
-  return solort::verify_xcd_placement(dev);
+  const int rc = solort::verify_xcd_placement(dev);
+  return rc ? rc : solort::noalloc_scratch_setup(dev);
 }
 
 extern "C" const char* solort_last_error(void) { return g_err; }

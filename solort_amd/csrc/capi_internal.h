@@ -28,6 +28,10 @@ int verify_xcd_placement(int dev);
 // probe.hip: whether that check passed on device `dev`.
 bool xcd_round_robin(int dev);
 
+// noalloc.hip: looks up the device address of the allocation-free entry
+// point's scratch array on device `dev` (current), once.  0 or the error code.
+int noalloc_scratch_setup(int dev);
+
 // prologue.hip: QK-RMSNorm + RoPE of the K rows and the cache write of the K
 // and V rows of T tokens at positions 0..T-1 (no q rows), cos/sin from a
 // solort_rope_rows table; arguments already validated.

@@ -250,6 +250,36 @@ def decode_layer(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps:
     _lib.check(rc, "decode_layer")
 
 
+def decode_layer_noalloc(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps: float,
+                         rope_cs: torch.Tensor, pos0: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
+                         bound: int, scale: float, n_split: int, out: torch.Tensor, nh: int, nkv: int) -> None:
+    """decode_layer with the partials in the library's fixed per-GPU scratch array instead of a
+    workspace (no allocation anywhere; calls that overlap on one GPU race); see
+    solort_decode_layer_noalloc."""
+    _on_gpu("qkv", qkv, torch.bfloat16)
+    _need(qkv.dim() == 2 and qkv.shape[1] == (nh + 2 * nkv) * HD and qkv.stride(1) == 1,
+          f"qkv must be [nq, {(nh + 2 * nkv) * HD}] with unit column stride")
+    nq = qkv.shape[0]
+    for name, w in (("qn_w", qn_w), ("kn_w", kn_w)):
+        _on_gpu(name, w, torch.bfloat16)
+        _need(w.shape == (HD,) and w.is_contiguous(), f"{name} must be [{HD}] contiguous")
+    _rope_rows_ok(rope_cs, nq)
+    ts, hs, max_len = _cache_strides("k_cache", k_cache, nkv)
+    _on_gpu("v_cache", v_cache, torch.bfloat16)
+    _need(v_cache.shape == k_cache.shape and v_cache.stride() == k_cache.stride(),
+          "v_cache must match k_cache in shape and strides")
+    _need(pos0.is_cuda and pos0.dtype == torch.int64 and pos0.numel() >= 1, "pos0 must be int64 on the device")
+    _need(out.is_cuda and out.dtype in (torch.bfloat16, torch.float32), "out must be bf16 or fp32 on the device")
+    _need(out.shape == (nq, nh * HD) and out.is_contiguous() and out.data_ptr() % 16 == 0,
+          f"out must be [{nq}, {nh * HD}] contiguous and 16-byte aligned")
+    dt = DTYPE_F32 if out.dtype == torch.float32 else DTYPE_BF16
+    rc = _lib.load().solort_decode_layer_noalloc(
+        qkv.data_ptr(), qkv.stride(0), nq, nh, nkv, HD, qn_w.data_ptr(), kn_w.data_ptr(), float(eps),
+        rope_cs.data_ptr(), pos0.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), ts, hs, max_len, int(bound),
+        float(scale), int(n_split), out.data_ptr(), dt, _stream(qkv))
+    _lib.check(rc, "decode_layer_noalloc")
+
+
 def paged_decode_layer(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps: float, rope_cs: torch.Tensor,
                        pos0: torch.Tensor, kv_pages: torch.Tensor, page_table: torch.Tensor, bound: int,
                        scale: float, ws: torch.Tensor, n_split: int, out: torch.Tensor, nh: int, nkv: int) -> None:
