@@ -242,3 +242,133 @@ def test_speculative_generation(gpu, draft_seed):
         assert sum(accepted) >= 0.6 * k * len(accepted)
     else:
         assert sum(accepted) <= 0.2 * k * len(accepted)
+
+
+# the Qwen3-0.6B shape as a draft for a target at the Qwen3-4B widths: different hidden size, heads,
+# layer count and query group, the same 151,936-token vocabulary (untied: the lm_head is its own matrix)
+DRAFT_0_6B = ModelShape("qwen3-0.6b-draft", hidden=1024, inter=3072, nh=16, nkv=8, layers=28, vocab=151936,
+                        tie_embeddings=False)
+TARGET_4B_2L = ModelShape("qwen3-4b-widths-2l", hidden=2560, inter=9728, nh=32, nkv=8, layers=2, vocab=151936,
+                          tie_embeddings=False)
+
+
+def test_speculative_cross_shape_draft(gpu):
+    """A 0.6B-shape draft (28 layers, hidden 1024, 16/8 heads) proposing for a target at the Qwen3-4B
+    widths (2 layers, hidden 2560, 32/8 heads), as cuda_graph_executor.py:408-424, :463-482 pair a
+    0.6B draft with a 4B target.  Every round's accepted count and appended token equal the reference
+    rule (:476-481) applied to that round's drafts and the target's verify argmaxes; the emitted tokens
+    equal the target-only greedy run, except that they may part at a position whose fp32 top-2 margin
+    is under 0.05 (there the verify and decode paths' roundings may legitimately pick different
+    tokens), after which the two runs continue different sequences; the draft's
+    cache holds the emitted sequence, as a fresh draft prefilled with it does.  With independent
+    random weights the draft almost never agrees, so rounds reject; the accepting rounds are the next
+    test's."""
+    wt = RandomQwen3(TARGET_4B_2L, gpu, seed=91)
+    wd = RandomQwen3(DRAFT_0_6B, gpu, seed=92)
+    target = GraphQwen3Decode(wt, 256)
+    draft = GraphQwen3Decode(wd, 256)
+    ids = torch.randint(0, 151936, (20,), generator=torch.Generator().manual_seed(93)).tolist()
+    n = 24
+    plen, k = len(ids), target.k1 - 1
+    target.prefill(ids)
+    draft.prefill(ids)
+    out = [int(target.tok.item())]
+    rounds = []
+    while len(out) < n:
+        got = target.speculative_round(draft, out[-1], plen + len(out) - 1)
+        drafts = target.vtok[1:].tolist()
+        tg = target.tok_ver.tolist()
+        a, nxt = target.acc_ver.tolist()
+        assert [a, nxt] == list(ref.accept_prefix(torch.tensor(tg), torch.tensor(drafts)))
+        assert got == drafts[:a] + [nxt]
+        rounds.append(a)
+        out += got
+    out = out[:n]
+    _say(f"  tokens {out}\n  accepted per round {rounds}")
+
+    greedy = GraphQwen3Decode(wt, 256).generate_from_prompt(ids, n)
+    same = next((i for i in range(n) if out[i] != greedy[i]), n)
+    if same < n:  # a divergence is allowed only where the fp32 model's top-2 margin is thin
+        bf = {kk: (v.cpu() if torch.is_tensor(v) else [t.cpu() for t in v]) for kk, v in vars(wt).items()
+              if kk != "shape"}
+        f32 = {kk: (v.float() if torch.is_tensor(v) else [t.float() for t in v]) for kk, v in bf.items()}
+        kc32 = torch.zeros(TARGET_4B_2L.layers, 256, TARGET_4B_2L.nkv, 128)
+        vc32 = torch.zeros_like(kc32)
+        lg = ref.prefill_model(f32, ids, kc32, vc32, TARGET_4B_2L.nh, TARGET_4B_2L.nkv)
+        for i in range(same):
+            lg = ref.decode_model_step(f32, greedy[i], plen + i, kc32, vc32, target.bucket_for(plen + i),
+                                       TARGET_4B_2L.nh, TARGET_4B_2L.nkv)
+        top2 = torch.topk(lg, 2).values
+        margin = (top2[0] - top2[1]).item()
+        _say(f"  first divergence from the target-only greedy run at token {same}, fp32 margin {margin:.3e}")
+        assert margin < 0.05
+    _say(f"  target-only greedy {greedy}; equal for the first {same} tokens")
+
+    fresh = GraphQwen3Decode(wd, 256)
+    fresh.prefill(ids + out[:n - 1])
+    P = plen + n - 1
+    d = (draft.kc[:, :P].float() - fresh.kc[:, :P].float()).abs()
+    _say(f"  draft cache vs a fresh draft prefilled with the emitted tokens: max-abs {d.max().item():.3e} "
+         f"mean-abs {d.mean().item():.3e}")
+    # 28 layers of bf16 rounding in two accumulation orders (decode GEMVs against prefill GEMMs) leave
+    # a few ulps; a row of another token would differ by ~1 on average
+    assert d.mean().item() <= 1e-2 and d.max().item() <= 0.25
+    assert sum(rounds) <= 0.2 * k * len(rounds)
+
+
+def _bigram(w: RandomQwen3, skip_every: int = 0) -> None:
+    """Turns random weights into a bigram model with a known greedy rule: o_proj and down are zero, so
+    the residual stream stays embed[t] and the logits are lm_head @ rmsnorm(embed[t]); lm_head row v
+    is embed row v - 1, so the self term (|embed[t]|^2 / rms, about 0.05 * hidden) leads every other
+    logit by dozens of its spread and the next token is t + 1.  With skip_every = m, row v also gets
+    1.5 x embed row v - 2 when (v - 2) % m == 0: then a token t with t % m == 0 is followed by t + 2."""
+    for t in w.wo + w.wd:
+        t.zero_()
+    e = w.embed.float()
+    lm = e.roll(1, dims=0)
+    if skip_every:
+        v = torch.arange(e.shape[0], device=e.device)
+        lm += 1.5 * ((v - 2) % skip_every == 0).float()[:, None] * e.roll(2, dims=0)
+    w.lm_head = lm.to(torch.bfloat16)
+
+
+def test_speculative_cross_shape_partial_acceptance(gpu):
+    """The same cross-shape pair as bigram models with known greedy rules: the target always emits
+    t + 1, the 0.6B-shape draft emits t + 2 after a multiple of 7 and t + 1 otherwise.  Then every
+    round's drafts, accepted count and appended token follow exactly from the reference's acceptance
+    rule (cuda_graph_executor.py:463-482), rounds accept 0 to all 4 drafts, and the emitted tokens are
+    the target's own greedy sequence."""
+    wt = RandomQwen3(TARGET_4B_2L, gpu, seed=94)
+    wd = RandomQwen3(DRAFT_0_6B, gpu, seed=95)
+    _bigram(wt)
+    _bigram(wd, skip_every=7)
+    target = GraphQwen3Decode(wt, 256)
+    draft = GraphQwen3Decode(wd, 256)
+    ids = [1000 + 7 * i for i in range(20)]
+    n = 40
+    plen, k = len(ids), target.k1 - 1
+    target.prefill(ids)
+    draft.prefill(ids)
+    out = [int(target.tok.item())]
+    assert out[0] == ids[-1] + 1
+    rounds = []
+    f = lambda u: u + 2 if u % 7 == 0 else u + 1  # noqa: E731  (the draft's rule)
+    while len(out) < n:
+        last = out[-1]
+        got = target.speculative_round(draft, last, plen + len(out) - 1)
+        drafts = [f(last)]
+        for _ in range(k - 1):
+            drafts.append(f(drafts[-1]))
+        tg = [last + 1] + [d + 1 for d in drafts]
+        a = next((j for j in range(k) if drafts[j] != tg[j]), k)
+        assert target.vtok[1:].tolist() == drafts
+        assert target.tok_ver.tolist() == tg
+        assert target.acc_ver.tolist() == [a, tg[a]]
+        assert got == drafts[:a] + [tg[a]]
+        rounds.append(a)
+        out += got
+    _say(f"  accepted per round {rounds}")
+    assert out == list(range(ids[-1] + 1, ids[-1] + 1 + len(out)))
+    # the first token after the prompt (1134) is a multiple of 7 (nothing accepted); after that the
+    # rounds alternate between all k drafts and one
+    assert 0 in rounds and k in rounds and any(0 < a < k for a in rounds)

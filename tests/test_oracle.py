@@ -473,3 +473,91 @@ def test_verify_model_equals_sequential_decode_steps():
     for i, t in enumerate(toks):
         assert (lg[i] - ref.decode_model_step(w, t, 20 + i, kc2, vc2, 64, nh, nkv)).abs().max().item() < 1e-5
     assert (kc - kc2).abs().max().item() < 1e-4 and (vc - vc2).abs().max().item() < 1e-4
+
+
+def _model_weights(seed: int, L=2, H=256, I=512, nh=4, nkv=2, V=300):
+    g = torch.Generator().manual_seed(seed)
+    width = (nh + 2 * nkv) * HD
+
+    def f(*s, std=0.02, mean=0.0):
+        return torch.randn(*s, generator=g) * std + mean
+
+    return {"embed": f(V, H, std=0.05), "in_ln": f(L, H, std=0.1, mean=1), "post_ln": f(L, H, std=0.1, mean=1),
+            "qn": f(L, HD, std=0.1, mean=1), "kn": f(L, HD, std=0.1, mean=1), "wqkv": [f(width, H) for _ in range(L)],
+            "wo": [f(H, nh * HD) for _ in range(L)], "wgu": [f(2 * I, H) for _ in range(L)],
+            "wd": [f(H, I) for _ in range(L)], "final_norm": f(H, std=0.1, mean=1), "lm_head": f(V, H)}
+
+
+def _np_rms(x, w, eps=1e-6):
+    x = np.asarray(x, np.float64)
+    return x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * np.asarray(w, np.float64)
+
+
+def _first_position_model_fp64(w: dict, tok: int, nh: int, nkv: int) -> np.ndarray:
+    """The model at position 0, written from the architecture in numpy fp64: there, attention over the
+    single visible key is exactly that key's V row (softmax of one score is 1), for query head h the
+    row of KV head h // (nh / nkv); q, k, their norms and RoPE drop out.  Per layer:
+    x += o_proj(ctx); x += down(silu(gate) * up) of the post-norm; logits = lm_head(final norm)."""
+    d = lambda t: np.asarray(t, np.float64)
+    g = nh // nkv
+    x = d(w["embed"][tok])
+    for li in range(len(w["wqkv"])):
+        qkv = d(w["wqkv"][li]) @ _np_rms(x, w["in_ln"][li])
+        v = qkv[(nh + nkv) * HD:].reshape(nkv, HD)
+        ctx = np.concatenate([v[h // g] for h in range(nh)])
+        x = x + d(w["wo"][li]) @ ctx
+        gu = d(w["wgu"][li]) @ _np_rms(x, w["post_ln"][li])
+        gate, up = np.split(gu, 2)
+        x = x + d(w["wd"][li]) @ (gate / (1.0 + np.exp(-gate)) * up)
+    return d(w["lm_head"]) @ _np_rms(x, w["final_norm"])
+
+
+def test_whole_model_restatements_pinned_at_the_first_position():
+    """decode_model_step at position 0, prefill_model of a one-token prompt and verify_model of one
+    token at position 0 (all fp32 weights) equal an fp64 evaluation written from the architecture
+    (residual order, o_proj, gate/up split, SiLU, down, final norm, lm_head, the query-head to KV-head
+    map), which shares no code with the oracle; a dropped final norm or residual changes the logits
+    by far more than the 1e-4 bar."""
+    nh, nkv = 4, 2
+    w = _model_weights(41, nh=nh, nkv=nkv)
+    L = len(w["wqkv"])
+    for tok in (0, 7, 299):
+        want = _first_position_model_fp64(w, tok, nh, nkv)
+        kc, vc = torch.zeros(L, 16, nkv, HD), torch.zeros(L, 16, nkv, HD)
+        got_d = ref.decode_model_step(w, tok, 0, kc, vc, 16, nh, nkv).double().numpy()
+        kc, vc = torch.zeros(L, 16, nkv, HD), torch.zeros(L, 16, nkv, HD)
+        got_p = ref.prefill_model(w, [tok], kc, vc, nh, nkv).double().numpy()
+        kc, vc = torch.zeros(L, 16, nkv, HD), torch.zeros(L, 16, nkv, HD)
+        got_v = ref.verify_model(w, [tok], 0, kc, vc, nh, nkv)[0].double().numpy()
+        scale = np.abs(want).max()
+        for got in (got_d, got_p, got_v):
+            assert np.abs(got - want).max() <= 1e-4 * scale
+    # the pin has teeth: without the final norm the logits move far outside the bar
+    no_norm = np.asarray(w["lm_head"], np.float64) @ np.asarray(w["embed"][7], np.float64)
+    assert np.abs(no_norm - _first_position_model_fp64(w, 7, nh, nkv)).max() > 1e-2 * scale
+
+
+def test_whole_model_residual_stream_is_the_embedding_when_the_branches_are_zero():
+    """With o_proj and down set to zero every layer adds nothing, so at any position and for any cache
+    the logits of decode_model_step, prefill_model (last row) and verify_model (each row) are
+    lm_head @ rmsnorm(embed[tok], final_norm), evaluated here in fp64."""
+    nh, nkv = 4, 2
+    w = _model_weights(43, nh=nh, nkv=nkv)
+    L = len(w["wqkv"])
+    w["wo"] = [torch.zeros_like(t) for t in w["wo"]]
+    w["wd"] = [torch.zeros_like(t) for t in w["wd"]]
+    lm = np.asarray(w["lm_head"], np.float64)
+
+    def want(tok):
+        return lm @ _np_rms(w["embed"][tok], w["final_norm"])
+
+    g = torch.Generator().manual_seed(44)
+    kc, vc = torch.randn(L, 64, nkv, HD, generator=g), torch.randn(L, 64, nkv, HD, generator=g)
+    got = ref.decode_model_step(w, 11, 37, kc.clone(), vc.clone(), 64, nh, nkv).double().numpy()
+    assert np.abs(got - want(11)).max() <= 1e-5 * np.abs(want(11)).max()
+    ids = [5, 17, 42, 7]
+    got = ref.prefill_model(w, ids, torch.zeros(L, 64, nkv, HD), torch.zeros(L, 64, nkv, HD), nh, nkv)
+    assert np.abs(got.double().numpy() - want(ids[-1])).max() <= 1e-5 * np.abs(want(ids[-1])).max()
+    got = ref.verify_model(w, ids, 30, kc.clone(), vc.clone(), nh, nkv).double().numpy()
+    for i, t in enumerate(ids):
+        assert np.abs(got[i] - want(t)).max() <= 1e-5 * np.abs(want(t)).max()
