@@ -384,17 +384,20 @@ int solort_greedy_advance(const void* ws, int vocab, const void* embed, int64_t 
                           void* x, int64_t* tok, int64_t* tokens, int max_tokens, int64_t* step, int64_t* pos,
                           solort_stream_t stream);
 
-/* Workspace bytes for solort_argmax_rows with `rows` rows. Allocate once,
- * zero-fill once, reuse; overlapping calls must not share it. */
+/* Workspace bytes for solort_argmax_rows with `rows` rows: per row 64 slots
+ * of 16 bytes and a 32-bit epoch (the launch count of the row, which tags the
+ * slots each launch writes).  Allocate once, zero-fill once, reuse (16-byte
+ * aligned); overlapping calls must not share it. */
 size_t solort_argmax_workspace_bytes(int rows);
 
 /*
  * Greedy argmax over each row of logits [rows, vocab] (row stride
  * `row_stride` elements), bf16 (dtype 0) or fp32 (dtype 1), into int64
  * out_idx[rows].  Ties go to the lowest index and NaN counts as the maximum
- * (first NaN wins), as torch.argmax does.
+ * (first NaN wins), as torch.argmax does.  One launch: up to 64 blocks per
+ * row each store their best key, and the row's last block reduces them.
  * Replaces cuda_graph_executor.py:201/:206 (in-graph), :234 (draft) and
- * :475 (verify) `argmax(-1)`.
+ * :475 (verify) `argmax(-1)`.  rows <= 65528.
  */
 int solort_argmax_rows(const void* logits, int dtype, int rows, int64_t vocab, int64_t row_stride,
                        int64_t* out_idx, void* ws, solort_stream_t stream);

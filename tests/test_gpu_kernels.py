@@ -291,6 +291,40 @@ def test_argmax_ties_across_blocks_nan_and_zero(gpu):
     _argmax_check(gpu, x.to(torch.bfloat16))
 
 
+def test_argmax_workspace_across_shapes_and_graph_replays(gpu):
+    """One workspace over calls whose rows are cut into different numbers of chunks (each launch
+    tags its slots with the row's next epoch, so slots left by a longer row earlier are never
+    read), then a graph of two argmax launches replayed with eager calls in between."""
+    g = torch.Generator().manual_seed(11)
+    xs = [torch.randn(5, 151936, generator=g), torch.randn(5, 8, generator=g), torch.randn(3, 20000, generator=g),
+          torch.randn(5, 151936, generator=g).to(torch.bfloat16), torch.randn(1, 3000, generator=g)]
+    ws = ops.argmax_workspace(5, gpu)
+    for rep in range(3):
+        for x in xs:
+            out = torch.empty(x.shape[0], dtype=torch.long, device=gpu)
+            ops.argmax_rows(x.to(gpu), out, ws)
+            torch.cuda.synchronize()
+            assert np.array_equal(out.cpu().numpy(), exact.argmax_first(x.float().numpy())), (rep, tuple(x.shape))
+    a, b = xs[0].to(gpu), xs[3].to(gpu)
+    oa = torch.empty(5, dtype=torch.long, device=gpu)
+    ob = torch.empty(5, dtype=torch.long, device=gpu)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        ops.argmax_rows(a, oa, ws)
+        ops.argmax_rows(b, ob, ws)
+    wa, wb = exact.argmax_first(xs[0].float().numpy()), exact.argmax_first(xs[3].float().numpy())
+    for r in range(4):
+        oa.zero_()
+        ob.zero_()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(oa.cpu().numpy(), wa) and np.array_equal(ob.cpu().numpy(), wb), f"replay {r}"
+        out = torch.empty(3, dtype=torch.long, device=gpu)
+        ops.argmax_rows(xs[2].to(gpu), out, ws)  # eager work between replays
+        torch.cuda.synchronize()
+        assert np.array_equal(out.cpu().numpy(), exact.argmax_first(xs[2].numpy()))
+
+
 def test_argmax_strided_rows(gpu):
     g = torch.Generator().manual_seed(5)
     big = torch.randn(3, 1003, generator=g)
