@@ -184,12 +184,12 @@ def main() -> int:
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4),
                      "traffic": None,
-                     "kernel": (f"solort_decode_layer = {DECODE_KERNEL} (split-KV attention with the "
-                                "single-launch combine)" if single else
+                     "kernel": (f"solort_decode_layer = {DECODE_KERNEL} (split-KV attention, splits "
+                                "merged in the same launch)" if single else
                                 f"solort_decode_layer = {DECODE_KERNEL} + combine_kernel<1, 4>"),
                      "kernel_us": round(kern_us, 3),
                      "algorithmic_bytes": kbytes,
-                     "single_launch_combine": single},
+                     "in_launch_merge": single},
     }
 
     if not args.no_sweep and args.only == "all":
@@ -258,7 +258,7 @@ def extras(torch, ops, wl, runners, dev, sh) -> dict:
 
     lib = _lib.load()
     default_mode = lib.solort_combine_mode(-1)
-    out: dict = {"decode_call_us": {}, "n_split_sweep_kv1024": {}, "single_launch_combine": default_mode == 1}
+    out: dict = {"decode_call_us": {}, "n_split_sweep_kv1024": {}, "in_launch_merge": default_mode == 1}
     for live in (128, 256, 512, 1024):
         ns = decode_splits(live, sh.nkv)
         pos = torch.tensor([live - 1], dtype=torch.long, device=dev)

@@ -64,7 +64,7 @@ const char* solort_last_error(void);
  * outside graph capture (it launches a probe, synchronises and allocates a
  * few KB that it frees).  It checks that workgroup b of a launch always runs
  * on the XCD (L2 domain) of workgroup b % 8, the round-robin placement of
- * MI355X, which the single-launch split combine relies on (see
+ * MI355X, which the in-launch split merge relies on (see
  * solort_decode_attn).  Without it, or if the check fails, every split call
  * combines in a second launch.  It also looks up the device address of
  * solort_decode_layer_noalloc's scratch array.
@@ -143,25 +143,27 @@ int solort_rope_rows(const float* inv_freq, int half_dim, const int64_t* pos0_de
 
 /* Workspace bytes needed by solort_decode_attn / solort_verify_attn /
  * solort_decode_layer for `nq` query tokens and `n_split` key splits: 16 KB
- * of per-KV-head tickets of the single-launch combine, then the splits'
- * partial results (per KV head and split: running max and sum, and the
- * unnormalised [nq * group][128] output, fp32).  The caller allocates it
- * once, zero-fills it once and reuses it (the kernels leave the tickets at
- * zero).  A workspace sized for (nq, n_split) serves any call with the same
- * nh/nkv and no larger nq or n_split.  Calls that overlap in time must not
- * share a workspace. */
+ * of per-KV-head launch counters of the in-launch merge, then the splits'
+ * partial results (per KV head, split and query row: running max and sum,
+ * and the unnormalised 128-dim output, fp32, each value paired with a 32-bit
+ * tag: 1040 bytes).  The caller allocates it once, zero-fills it once and
+ * reuses it (each call advances the counters of its KV heads).  A workspace
+ * sized for (nq, n_split) serves any call with the same nh/nkv and no larger
+ * nq or n_split, and calls of different shapes may share one.  Calls that
+ * overlap in time must not share a workspace. */
 size_t solort_attn_workspace_bytes(int nq, int nh, int nkv, int hd, int n_split);
 
 /*
  * Grouped-query attention of `nq` new tokens over the static KV cache, split
  * across `n_split` workgroups per KV head (flash-decoding), and the
  * log-sum-exp combine of the splits (none when n_split is 1).  The combine
- * runs inside the same launch -- the last split of each KV head to finish
- * merges the head's partials, which meet in the L2 of the XCD all of that
- * head's splits run on -- for long chunks: when solort_init's placement check
- * passed, nkv is a multiple of 8, n_split <= 32, nq * (nh / nkv) <= 8 and
- * each split covers at least 512 keys; otherwise (where a second launch is
- * cheaper) as a second launch on the same stream.
+ * runs inside the same launch -- each split tags its partial with the KV
+ * head's launch counter and the head's last min(n_split, nq * nh / nkv)
+ * splits each merge rows of the output once every split's partial carries
+ * the tag, in the L2 of the XCD all of the head's splits run on -- when
+ * solort_init's placement check passed, nkv is a multiple of 8 up to 128,
+ * n_split <= 64 and nq * nh / nkv <= 8; otherwise as a second launch on the
+ * same stream.
  * Replaces the decode block cuda_graph_executor.py:168, :180-184 (nq = 1:
  * softmax(q K^T * scale, keys > pos masked) V over the bucket) and the verify
  * block :247-250, :261-263 (nq = K+1, query t at position pos0+t sees keys
@@ -217,7 +219,7 @@ int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int nq, int nh,
  * reference: it is for callers that cannot allocate device memory (code
  * under graph capture that must not call hipMalloc, tight serving loops,
  * harnesses that forbid allocation).  The partials live in a fixed
- * per-device array of SOLORT_NOALLOC_SCRATCH_BYTES (4 MiB) inside the
+ * per-device array of SOLORT_NOALLOC_SCRATCH_BYTES (8 MiB) inside the
  * library, held until the process ends; a call whose
  * solort_attn_workspace_bytes(nq, nh, nkv, hd, n_split) exceeds it returns
  * SOLORT_EINVAL.  It allocates nothing: the array's device address is looked
@@ -226,7 +228,7 @@ int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int nq, int nh,
  * GPU race.  Results equal solort_decode_layer's with any workspace, bit for
  * bit.  Other arguments as in solort_decode_layer.
  */
-#define SOLORT_NOALLOC_SCRATCH_BYTES (4u << 20)
+#define SOLORT_NOALLOC_SCRATCH_BYTES (8u << 20)
 int solort_decode_layer_noalloc(const void* qkv, int64_t qkv_row_stride, int nq, int nh, int nkv, int hd,
                                 const void* qn_w, const void* kn_w, float eps, const void* rope_cs,
                                 const int64_t* pos0_dev, void* k_cache, void* v_cache, int64_t kv_tok_stride,

@@ -121,7 +121,7 @@ def _source_id() -> int | None:
 
 def _init_device(lib: ctypes.CDLL) -> None:
     """solort_init once per device, outside graph capture (it synchronises): checks the
-    workgroup placement the single-launch split combine relies on."""
+    workgroup placement the in-launch split merge relies on."""
     if not torch.cuda.is_available():
         return
     dev = torch.cuda.current_device()

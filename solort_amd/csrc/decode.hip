@@ -1,6 +1,7 @@
 // Split-KV (flash-decoding) grouped-query attention for 1..8 new tokens over
 // the static KV cache, optionally fused with the QK-RMSNorm + RoPE prologue
-// and KV write, followed by a small kernel that combines the splits.
+// and KV write; the splits are merged in the same launch or by a small
+// second kernel.
 //
 // Reference semantics (src/solort/model/cuda_graph_executor.py):
 //   decode :168, :173-184  q/k norm + rope, KV write at pos, then
@@ -42,9 +43,11 @@
 //     contiguous cache with packed qkv rows, the same body runs as
 //     decode_mfma_packed_kernel (packed arguments, as above).
 // Output: with one split the block writes the answer; otherwise its partial
-// (running max in log2 units, sum, unnormalised output).  Combine kernel:
-// merges the partials of each KV head (log-sum-exp); the kernel boundary
-// orders its reads after the split kernel's writes.
+// (running max in log2 units, sum, unnormalised output), tagged.  The
+// partials of each KV head are merged (log-sum-exp) by the head's last
+// splits, which poll for the tags of this launch (in-launch merge), or by
+// the combine kernel, whose launch boundary orders its reads after the split
+// kernel's writes.
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -63,8 +66,12 @@ struct DecodeTail {
   const uint16_t* kn_w;
   const uint16_t* rope_cs;  // [2][nq][64] bf16: cos rows, then sin rows, of this step
   const int64_t* pos0_dev;
-  float* ws_o;   // [nkv][n_split][R][128]
-  float* ws_ml;  // [nkv][n_split][R][2]: running max (log2 units), sum
+  // Partials of the splits.  In-launch merge: tagged, ws_o [nkv][n_split][R][64] items (O[2i],
+  // tag, O[2i+1], tag) and ws_ml [nkv][n_split][R] items (running max in log2 units, tag, sum,
+  // tag).  Otherwise untagged, in the same regions: fp32 [nkv][n_split][R][128] and
+  // [nkv][n_split][R][2].
+  uint4* ws_o;
+  uint4* ws_ml;
   void* out;     // [nq][nh][128]
   float qscale;  // softmax scale * log2(e)
   float eps;
@@ -76,9 +83,11 @@ struct DecodeTail {
   int64_t page_stride;
   int page_shift;
   int num_pages;
-  // Single-launch combine (null: the combine kernel runs as a second launch): per KV head a
-  // 64-bit ticket, 128 bytes apart, zero between launches.
-  unsigned long long* tickets;
+  // Per KV head a 32-bit launch counter of the in-launch merge, 128 bytes apart (the
+  // workspace's start).
+  unsigned* epochs;
+  int n_split;  // splits per KV head
+  int merge;    // 1: the in-launch merge; 0: the combine kernel's second launch
 };
 
 // Element offset of the cache row at position t (head 0, dim 0).  Paged: a
@@ -132,9 +141,8 @@ __device__ __forceinline__ void store_out2(void* out, int out_f32, int nh, int k
 // The log-sum-exp combine of the n_split partials of one KV head: thread =
 // (float4 column c of the head's [R][128] output, split group sg of 8) merges
 // splits sg, sg + 8, ... on its own (up to kCombB loads in flight per batch),
-// then the 8 split groups meet once in LDS.  The combine kernel runs 32
-// columns per workgroup; the single-launch combine (the last split of the
-// head to finish) runs all of the head's columns at once.  Both use these
+// then the 8 split groups meet once in LDS.  The combine kernel and the
+// in-launch merge both run one row (32 columns) per workgroup with these
 // functions, so both give the same bits.
 
 constexpr int kCombB = 8;  // splits per thread per batch (combine kernel)
@@ -191,103 +199,123 @@ __device__ __forceinline__ float4 comb_final(const float* s_m, const float* s_l,
   return Os;
 }
 
-// Loads that miss the CU's L1 and hit the XCD's L2 (cache policy sc0): the
-// partials of the other splits of a head were stored by other CUs of the same
-// XCD during this launch.
-__device__ __forceinline__ float4 ld_l2_f4(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 1));
-}
-__device__ __forceinline__ float2 ld_l2_f2(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(float2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, 1));
-}
-
-constexpr int kFuseMaxSplit = 32;   // single-launch combine: splits per head (4 per split group)
-constexpr int kFuseMaxRows = 8;     // ... query rows per KV head
-constexpr int kFuseMinChunk = 512;  // ... and keys per split (the MFMA split kernel's long chunks)
-
-// Bytes of LDS the single-launch combine of R rows needs: [8][32 R] max, sum, output.
-constexpr int fuse_lds_bytes(int R) { return R <= kFuseMaxRows ? 8 * 32 * R * (4 + 4 + 16) : 0; }
-
-// The end of a split block in single-launch mode, after its partial is
-// stored: the block takes the head's ticket; the last split of the head to
-// arrive merges all of its partials and writes the head's output rows.
+// ---------------------------------------------------------------- in-launch merge
+// In-launch mode (DecodeTail::merge), with more than one split: each split
+// stores its partial as tagged 8-byte pairs (value, tag): per row of the
+// head, 64 items of 16 bytes (O[2i], tag, O[2i+1], tag), then one item (max,
+// tag, sum, tag).  A naturally aligned 8-byte store is single-copy atomic, so
+// a reader that sees the tag of this launch in a pair also sees that pair's
+// value.  The tag is this launch's value of the KV head's counter, and the
+// last K = min(n_split, R) splits of the head each merge rows j, j + K, ...
+// (j = split - (n_split - K)) once every split's items for them carry the
+// tag: they poll the items with loads that miss the CU's L1 (cache policy
+// sc1) and read the XCD's L2, where every split of the head stores (blocks
+// (kvh, split) have linear index kvh + nkv * split, nkv is a multiple of 8,
+// and workgroup b runs on the XCD of workgroup b % 8, checked by
+// solort_init).  No store waits for an acknowledgement, no atomic is issued
+// and nothing is cleared: items of earlier launches carry earlier tags.  The
+// merge functions are the combine kernel's, so both modes give the same bits.
+// (Two-launch mode: untagged partials, half the bytes, which the combine
+// kernel reads after the launch boundary.)
 //
-// Every split of a head runs on one XCD: blocks (kvh, split) have linear
-// index kvh + nkv * split, nkv is a multiple of 8, and workgroup b runs on
-// the XCD of workgroup b % 8 (round-robin dispatch, checked by solort_init).
-// So the partials meet in that XCD's L2: each block waits until its stores
-// are acknowledged (by the L2), then adds to the ticket; the last one reads
-// the partials past its L1.  No cache writeback or invalidate is needed.
-// The ticket adds 1 << (8 xcc) per block, so the last block also sees that
-// every split ran on its own XCD; if not (placement other than checked), it
-// writes NaN rather than a result built from partials it cannot see.  It
-// then clears the ticket for the next launch.  lds: fuse_lds_bytes(R) bytes.
+// Tags: the head's counter (32 bits, 128 bytes apart per head at the start of
+// the workspace, zero-filled once) holds c; this launch uses n = c + 1
+// (skipping multiples of 2^25) and tag (n mod 2^25) << 7 | kvh, and the block
+// merging the head's first row stores n once its poll is done (by then every
+// split of the head has read c: its tagged items depend on it).  A tag is
+// never another head's, and it repeats only after 2^25 - 1 launches on the
+// head.
+constexpr int kMergeMaxSplit = 64;   // in-launch merge: splits per head (8 per split group)
+constexpr int kMergeHeads = 128;     // ... KV heads (counters at the start of the workspace)
+constexpr int kMergeSpin = 1 << 18;  // polling rounds before a merging block gives up (writes NaN)
+
+__device__ __forceinline__ unsigned merge_next(unsigned c) {
+  unsigned n = c + 1u;
+  if ((n & 0x1ffffffu) == 0u) ++n;
+  return n;
+}
+__device__ __forceinline__ unsigned merge_tag(unsigned n, int kvh) { return ((n & 0x1ffffffu) << 7) | (unsigned)kvh; }
+
+__device__ __forceinline__ uint4 tagged2(float x, float y, unsigned tag) {
+  return make_uint4(__float_as_uint(x), tag, __float_as_uint(y), tag);
+}
+
+// Device-scope 16-byte load (cache policy sc1): misses the CU's L1, reads the XCD's L2.
+__device__ __forceinline__ uint4 ld_l2(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16));
+}
+
+// Merges the head's rows j, j + K, ... (see above) and writes them.  Called
+// by every thread of a merging block, after its own partial is stored; lds:
+// 6 KiB no other wave still uses.  Thread (column c of the row, split group
+// sg) polls splits sg + 8k.
 template <int R>
-__device__ __forceinline__ void single_launch_combine(const DecodeTail& a, int kvh, int NS, int nh, int G,
-                                                      uint8_t* lds) {
-  static_assert(R <= kFuseMaxRows, "single-launch combine serves at most 8 rows per KV head");
-  constexpr int C = R * 32;  // float4 columns of the head's output
-  constexpr int NB = kFuseMaxSplit / 8;
-  __shared__ int s_last;
-  const int tid = threadIdx.x;
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this wave's partial stores are in the L2
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t xcc = __builtin_amdgcn_s_getreg(20 | (0 << 6) | ((16 - 1) << 11)) & 7u;
-    unsigned long long* t = a.tickets + (size_t)kvh * 16;
-    const unsigned long long mine = 1ull << (8 * xcc);
-    const unsigned long long now =
-        __hip_atomic_fetch_add(t, mine, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + mine;
-    unsigned total = 0;
-#pragma unroll
-    for (int x = 0; x < 8; ++x) total += (unsigned)(now >> (8 * x)) & 0xffu;
-    const bool last = total == (unsigned)NS;
-    const bool same = ((now >> (8 * xcc)) & 0xffu) == (unsigned long long)NS;
-    if (last) __hip_atomic_store(t, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = last ? (same ? 1 : 2) : 0;
-  }
-  __syncthreads();
-  const int last = s_last;
-  if (last == 0) return;
-  const int c = tid & 31, sg = tid >> 5;
+__device__ __forceinline__ void split_merge(const DecodeTail& a, int kvh, int split, int NS, int nh, int G,
+                                            unsigned tag, unsigned next, uint8_t* lds) {
+  const int K = min(NS, R);
+  const int j = split - (NS - K);
+  if (j < 0) return;  // block-uniform
+  __shared__ int s_bad;
+  const int tid = threadIdx.x, c = tid & 31, sg = tid >> 5;
+  const int nk = (NS - sg + 7) >> 3;  // splits sg + 8k (k < nk) exist
   const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
-      a.ws_o + (size_t)kvh * NS * C * 4, (short)0, NS * C * 16, 0x00020000);
+      a.ws_o + (size_t)kvh * NS * R * 64, (short)0, NS * R * 64 * 16, 0x00020000);
   const __amdgpu_buffer_rsrc_t rm = __builtin_amdgcn_make_buffer_rsrc(
-      a.ws_ml + (size_t)kvh * NS * R * 2, (short)0, NS * R * 8, 0x00020000);
+      a.ws_ml + (size_t)kvh * NS * R, (short)0, NS * R * 16, 0x00020000);
   float* s_m = reinterpret_cast<float*>(lds);
-  float* s_l = s_m + 8 * C;
-  float4* s_o = reinterpret_cast<float4*>(s_l + 8 * C);
-  // All loads first, unconditionally (splits past NS lie past the buffer
-  // ranges and read as zeros): column 32 p + c (row p) of splits sg + 8 k.
-  float2 ml[R][NB];
-  float4 ov[R][NB];
+  float* s_l = s_m + 8 * 32;
+  float4* s_o = reinterpret_cast<float4*>(s_l + 8 * 32);
+  for (int r = j; r < R; r += K) {
+    if (tid == 0) s_bad = 0;
+    __syncthreads();  // the LDS region is free; s_bad is set
+    float2 ml[kCombB];
+    float4 ov[kCombB];
 #pragma unroll
-  for (int p = 0; p < R; ++p)
-#pragma unroll
-    for (int k = 0; k < NB; ++k) {
-      const int s = sg + 8 * k;
-      ml[p][k] = ld_l2_f2(rm, (s * R + p) * 8);
-      ov[p][k] = ld_l2_f4(ro, (s * C + 32 * p + c) * 16);
+    for (int k = 0; k < kCombB; ++k) {
+      ml[k] = make_float2(-INFINITY, 0.f);  // an absent split
+      ov[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
+    bool pend = true;
+    for (int it = 0; it < kMergeSpin; ++it) {
+      asm volatile("" ::: "memory");  // a fresh load every round
+      uint4 mv[kCombB], xv[kCombB], yv[kCombB];
 #pragma unroll
-  for (int p = 0; p < R; ++p)
+      for (int k = 0; k < kCombB; ++k) {
+        if (k < nk) {
+          const int pr = (sg + 8 * k) * R + r;
+          mv[k] = ld_l2(rm, pr * 16);
+          xv[k] = ld_l2(ro, (pr * 64 + 2 * c) * 16);
+          yv[k] = ld_l2(ro, (pr * 64 + 2 * c + 1) * 16);
+        }
+      }
+      pend = false;
 #pragma unroll
-    for (int k = 0; k < NB; ++k)
-      if (sg + 8 * k >= NS) ml[p][k].x = -INFINITY;  // an absent split
-#pragma unroll
-  for (int p = 0; p < R; ++p) {
+      for (int k = 0; k < kCombB; ++k) {
+        if (k < nk) {
+          ml[k] = make_float2(__uint_as_float(mv[k].x), __uint_as_float(mv[k].z));
+          ov[k] = make_float4(__uint_as_float(xv[k].x), __uint_as_float(xv[k].z), __uint_as_float(yv[k].x),
+                              __uint_as_float(yv[k].z));
+          pend |= (mv[k].y != tag) | (mv[k].w != tag) | (xv[k].y != tag) | (xv[k].w != tag) | (yv[k].y != tag) |
+                  (yv[k].w != tag);
+        }
+      }
+      if (__builtin_amdgcn_ballot_w64(pend) == 0) break;
+    }
+    if (pend) s_bad = 1;
     CombAcc acc = comb_init();
-    comb_merge<NB>(acc, ml[p], ov[p]);
-    const int col = 32 * p + c;
-    s_m[sg * C + col] = acc.m;
-    s_l[sg * C + col] = acc.l;
-    s_o[sg * C + col] = acc.o;
-  }
-  __syncthreads();
-  for (int col = tid; col < C; col += 256) {
-    float4 v = comb_final(s_m, s_l, s_o, C, col);
-    if (last == 2) v = make_float4(NAN, NAN, NAN, NAN);
-    store_out(a.out, a.out_f32, nh, kvh, G, col, v);
+    comb_merge<kCombB>(acc, ml, ov);
+    s_m[sg * 32 + c] = acc.m;
+    s_l[sg * 32 + c] = acc.l;
+    s_o[sg * 32 + c] = acc.o;
+    __syncthreads();
+    // Every wave has seen every split's items: each split has read the counter.
+    if (r == 0 && tid == 0) a.epochs[kvh * 32] = next;
+    if (tid < 32) {
+      float4 v = comb_final(s_m, s_l, s_o, 32, c);
+      if (s_bad) v = make_float4(NAN, NAN, NAN, NAN);
+      store_out(a.out, a.out_f32, nh, kvh, G, 32 * r + c, v);
+    }
+    __syncthreads();  // LDS and s_bad are reused by the next row
   }
 }
 
@@ -305,11 +333,12 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
   constexpr int RPW = (R + 3) / 4;     // output rows per wavefront
   __shared__ __align__(16) uint4 s_q[R * 16];         // q rows, bf16 bits [row][16 x 16 B]
   __shared__ uint4 s_new[FUSED ? 2 * NQ * 16 : 1];   // fresh K rows then V rows (bf16 bits)
-  __shared__ __align__(16) uint4 s_v[KPI * 16];      // the iteration's V rows [key][16 x 16 B]
+  // the iteration's V rows [key][16 x 16 B]; at least 6 KiB (the in-launch merge's LDS)
+  __shared__ __align__(16) uint4 s_v[KPI * 16 > 384 ? KPI * 16 : 384];
   __shared__ __align__(16) float s_s[R * KPI];       // its masked scores [row][key] (log2 units), then p
 
   const int tid = threadIdx.x, j = tid & 15, slot = tid >> 4, wave = tid >> 6, lane = tid & 63;
-  const int kvh = blockIdx.x, split = blockIdx.y, NS = gridDim.y;
+  const int kvh = blockIdx.x, split = blockIdx.y;
   const int nkv = nh / G;  // = gridDim.x, without the hidden-argument load
   const int kbeg = min(split * chunk, bound);
   const int kstat = min(kbeg + chunk, bound);
@@ -521,22 +550,32 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
     }
   }
 
-  // 5. One split: the answer; otherwise this split's partial (max, sum,
-  //    unnormalised output) for the combine kernel.
+  // 5. One split: the answer; otherwise this split's tagged partial (max,
+  //    sum, unnormalised output), merged in this launch or by the combine
+  //    kernel.
+  const int NS = a.n_split;
+  const bool inl = a.merge;
+  const unsigned next = inl ? merge_next(a.epochs[kvh * 32]) : 0u;
+  const unsigned tag = merge_tag(next, kvh);
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
     const int r = wave + 4 * i;
     if (r >= R) continue;
     const float Ls = wave_sum(Lk[i]);
+    const int64_t pr = (int64_t)(kvh * NS + split) * R + r;
     if (NS == 1) {
       const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
       store_out2(a.out, a.out_f32, nh, kvh, G, r, 2 * lane, O[i][0] * inv, O[i][1] * inv);
+    } else if (inl) {
+      a.ws_o[pr * 64 + lane] = tagged2(O[i][0], O[i][1], tag);
+      if (lane == 0) a.ws_ml[pr] = tagged2(M[i], Ls, tag);
     } else {
-      const int64_t pr = (int64_t)(kvh * NS + split) * R + r;
-      *reinterpret_cast<float2*>(a.ws_o + pr * 128 + 2 * lane) = make_float2(O[i][0], O[i][1]);
-      if (lane == 0) *reinterpret_cast<float2*>(a.ws_ml + pr * 2) = make_float2(M[i], Ls);
+      reinterpret_cast<float2*>(a.ws_o)[pr * 64 + lane] = make_float2(O[i][0], O[i][1]);
+      if (lane == 0) reinterpret_cast<float2*>(a.ws_ml)[pr] = make_float2(M[i], Ls);
     }
   }
+  // s_v (>= 6 KiB) is free: every wave passed the loop's last barrier.
+  if (NS > 1 && inl) split_merge<R>(a, kvh, split, NS, nh, G, tag, next, reinterpret_cast<uint8_t*>(s_v));
 }
 
 // Arguments as the entry points pass them: the leading 14 dwords arrive
@@ -636,7 +675,7 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
 
   const int tid = threadIdx.x, j = tid & 15, slot = tid >> 4, wave = tid >> 6, lane = tid & 63;
   const int l32 = lane & 31, hi = lane >> 5;
-  const int kvh = blockIdx.x, split = blockIdx.y, NS = gridDim.y;
+  const int kvh = blockIdx.x, split = blockIdx.y;
   const int nkv = nh / G;  // = gridDim.x, without the hidden-argument load
   const int kbeg = min(split * chunk, bound);
   const int kstat = min(kbeg + chunk, bound);
@@ -890,6 +929,10 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
   }
   // With one active wave only wave 0 writes; rows past R are padding.
   const bool writer = (nact > 1 || wave == 0) && l32 < R;
+  const int NS = a.n_split;
+  const bool inl = a.merge;
+  const unsigned next = inl ? merge_next(a.epochs[kvh * 32]) : 0u;
+  const unsigned tag = merge_tag(next, kvh);
   const int r = l32;
   // Writes dims 32dt .. 32dt + 31 of row r (this lane's 16 of them) from od.
   auto write_dims = [&](const f32x16& od, int dt) {
@@ -911,11 +954,18 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
         }
       }
     } else {
-      float* dst = a.ws_o + ((int64_t)(kvh * NS + split) * R + r) * 128 + 32 * dt + 4 * hi;
+      // dims 32dt + 8q4 + 4hi .. +3: tagged items 16dt + 4q4 + 2hi, +1, or one float4
+      uint4* dst = a.ws_o + ((int64_t)(kvh * NS + split) * R + r) * 64 + 16 * dt + 2 * hi;
 #pragma unroll
-      for (int q4 = 0; q4 < 4; ++q4)
-        *reinterpret_cast<float4*>(dst + 8 * q4) = make_float4(od[4 * q4], od[4 * q4 + 1], od[4 * q4 + 2],
-                                                               od[4 * q4 + 3]);
+      for (int q4 = 0; q4 < 4; ++q4) {
+        if (inl) {
+          dst[4 * q4] = tagged2(od[4 * q4], od[4 * q4 + 1], tag);
+          dst[4 * q4 + 1] = tagged2(od[4 * q4 + 2], od[4 * q4 + 3], tag);
+        } else {
+          reinterpret_cast<float4*>(a.ws_o)[((int64_t)(kvh * NS + split) * R + r) * 32 + 8 * dt + 2 * q4 + hi] =
+              make_float4(od[4 * q4], od[4 * q4 + 1], od[4 * q4 + 2], od[4 * q4 + 3]);
+        }
+      }
     }
   };
   if (writer) {
@@ -927,15 +977,18 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
       write_dims(o[2], 2);
       write_dims(o[3], 3);
     }
-    if (NS > 1 && hi == 0 && (nact == 1 || wave == 0))
-      *reinterpret_cast<float2*>(a.ws_ml + ((int64_t)(kvh * NS + split) * R + r) * 2) =
-          make_float2(m == -INFINITY ? m : m * qs, lsum);
+    if (NS > 1 && hi == 0 && (nact == 1 || wave == 0)) {
+      const int64_t pr = (int64_t)(kvh * NS + split) * R + r;
+      const float mq = m == -INFINITY ? m : m * qs;
+      if (inl)
+        a.ws_ml[pr] = tagged2(mq, lsum, tag);
+      else
+        reinterpret_cast<float2*>(a.ws_ml)[pr] = make_float2(mq, lsum);
+    }
   }
-  if constexpr (R <= kFuseMaxRows) {
-    // s_x is free: the merge above read it before its last barrier, and the
-    // combine's first barrier comes before any of its LDS writes.
-    if (NS > 1 && a.tickets) single_launch_combine<R>(a, kvh, NS, nh, G, s_x);
-  }
+  // s_x is free: the merge above read it before its last barrier, and the
+  // in-launch merge's first barrier comes before any of its LDS writes.
+  if (NS > 1 && inl) split_merge<R>(a, kvh, split, NS, nh, G, tag, next, s_x);
 }
 
 // Arguments as the entry points pass them: the leading 14 dwords arrive
@@ -965,13 +1018,13 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_packed_kernel(uint16_t* kc
 }
 
 // The combine kernel (two-launch mode): the log-sum-exp combine of the
-// n_split partials of each KV head.  Grid (nkv, column blocks): block = (KV
+// n_split untagged partials of each KV head.  Grid (nkv, column blocks): block = (KV
 // head, 32 float4 columns of its [R][128] output); thread = (column, split
 // group sg of 8): it merges splits sg, sg+8, ... on its own, kCombB at a time
 // (all loads of a batch issued together), then the 8 split groups meet once
 // in LDS.  Every argument is preloaded.
 template <int NQ, int G>
-__global__ __launch_bounds__(256) void combine_kernel(const float* ws_o, const float* ws_ml, void* out, int nh,
+__global__ __launch_bounds__(256) void combine_kernel(const uint4* ws_o, const uint4* ws_ml, void* out, int nh,
                                                       int n_split, int out_f32) {
   constexpr int R = NQ * G;
   constexpr int C = R * 32;  // float4 columns
@@ -1028,14 +1081,15 @@ struct DecodeArgs {
   bool paged;  // K/V rows through the page table in tail
   int U;       // key rows per slot per step of the lane-parallel kernel
   DecodeTail tail;
+
+  dim3 grid() const { return dim3(nkv, n_split); }
 };
 
-// Workspace: the single-launch tickets (128 bytes per KV head, for up to
-// kTicketHeads heads, at a fixed offset so that calls of any shape sharing a
-// workspace agree on them; zero between launches), then the splits' (max,
-// sum) pairs and unnormalised outputs.
-constexpr int kTicketHeads = 128;
-constexpr size_t kTicketBytes = (size_t)kTicketHeads * 128;
+// Workspace: the per-KV-head launch counters of the in-launch merge (128
+// bytes per head, for up to kMergeHeads heads, at a fixed offset so that
+// calls of any shape sharing a workspace agree on them), then the splits'
+// tagged (max, sum) items and output items.
+constexpr size_t kCounterBytes = (size_t)kMergeHeads * 128;
 
 struct WsLayout {
   size_t ml_off, o_off, total;
@@ -1046,39 +1100,44 @@ static size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 static WsLayout ws_layout(int nq, int nh, int nkv, int n_split) {
   const size_t R = (size_t)nq * (nh / nkv);
   WsLayout w;
-  w.ml_off = kTicketBytes;
-  w.o_off = align256(w.ml_off + (size_t)nkv * n_split * R * 2 * sizeof(float));
-  w.total = align256(w.o_off + (size_t)nkv * n_split * R * 128 * sizeof(float));
+  w.ml_off = kCounterBytes;
+  w.o_off = align256(w.ml_off + (size_t)nkv * n_split * R * 16);
+  w.total = align256(w.o_off + (size_t)nkv * n_split * R * 64 * 16);
   return w;
 }
 
-// Single-launch combine, per device: on once solort_init has checked the
-// workgroup placement (probe.hip), unless switched off by solort_combine_mode.
+// In-launch merge, per device: on once solort_init has checked the workgroup
+// placement (probe.hip), unless switched off by solort_combine_mode.
 namespace {
 constexpr int kMaxDev = 64;
 int g_combine_off[kMaxDev];
 }  // namespace
 
-// The single launch saves the combine kernel's launch but adds, to the split
-// kernel, a wait for the partials' stores, a device-scope ticket round trip
-// and the last split's reads of the partials: measured on MI355X (Qwen3
-// shapes), +1.0 us for the ticket and +1.7 us for the merge.  That beats a
-// second launch only after a long split kernel (Qwen3-8B at KV 32768, 32
-// splits of 1024 keys: 31.3 against 32.3 us per call); after the short
-// lane-parallel kernel the second launch is cheaper (KV 1024: 5.93 against
-// 6.21 us), so only MFMA-kernel chunks of at least kFuseMinChunk keys use it.
-static bool single_launch_ok(int nq, int nh, int nkv, int n_split, bool lanes, int chunk) {
+// The in-launch merge needs every split of a head on one XCD (nkv a multiple
+// of 8, round-robin placement) and at most kMergeMaxSplit splits (one batch
+// of loads per polling round).  A merging block waits for blocks dispatched
+// before it and for the head's other merging blocks; at most 256 merging
+// blocks in all (one per CU) keeps the blocks they wait for from being held
+// back by blocks that wait.  It is used for at most kMergeMaxRows query rows
+// per KV head: its partials carry a tag per value (twice the bytes), which
+// the merge saving pays for only while they are few.  Measured on MI355X,
+// one call, graph of 288 calls on distinct caches: Qwen3-4B decode at KV
+// 1024 (4 rows, 32 splits) 5.68 us in-launch against 5.91 us two-launch;
+// Qwen3-8B at KV 32768 (4 rows, 32 splits of 1024 keys) 32.7 against 32.9;
+// a 5-token verify at 4096 (20 rows, 32 splits) 10.90 against 10.55.
+constexpr int kMergeMaxRows = 8;
+
+static bool merge_ok(int rows, int n_split, int nkv) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return false;
-  const int R = nq * (nh / nkv);
-  return !g_combine_off[dev] && xcd_round_robin(dev) && n_split > 1 && n_split <= kFuseMaxSplit &&
-         R <= kFuseMaxRows && nkv % 8 == 0 && nkv <= kTicketHeads && !lanes && chunk >= kFuseMinChunk;
+  return !g_combine_off[dev] && xcd_round_robin(dev) && n_split > 1 && n_split <= kMergeMaxSplit && nkv % 8 == 0 &&
+         nkv <= kMergeHeads && rows <= kMergeMaxRows && nkv * (n_split < rows ? n_split : rows) <= 256;
 }
 
 template <int NQ, int G, bool FUSED, bool PAGED>
 static bool launch_split_p(const DecodeArgs& a, hipStream_t s) {
   if constexpr (NQ * G <= kMaxRows) {
-    const dim3 grid(a.nkv, a.n_split);
+    const dim3 grid = a.grid();
     if constexpr (NQ == 1 && G <= kLanesMaxGroup) {
       if constexpr (FUSED && !PAGED) {
         // The packed-argument kernel when the layout fits its fields.
@@ -1088,8 +1147,11 @@ static bool launch_split_p(const DecodeArgs& a, hipStream_t s) {
           if (a.U == 4)
             hipLaunchKernelGGL((decode_lanes_packed_kernel<G, 4>), grid, dim3(256), 0, s, a.kc, a.vc, strides8, geom,
                                a.qsrc, a.qn_w, a.tail.kn_w, a.tail.rope_cs, a.tail);
-          else
+          else if (a.U == 2)
             hipLaunchKernelGGL((decode_lanes_packed_kernel<G, 2>), grid, dim3(256), 0, s, a.kc, a.vc, strides8, geom,
+                               a.qsrc, a.qn_w, a.tail.kn_w, a.tail.rope_cs, a.tail);
+          else
+            hipLaunchKernelGGL((decode_lanes_packed_kernel<G, 1>), grid, dim3(256), 0, s, a.kc, a.vc, strides8, geom,
                                a.qsrc, a.qn_w, a.tail.kn_w, a.tail.rope_cs, a.tail);
           return true;
         }
@@ -1099,8 +1161,12 @@ static bool launch_split_p(const DecodeArgs& a, hipStream_t s) {
           hipLaunchKernelGGL((decode_lanes_kernel<NQ, G, 4, FUSED, PAGED>), grid, dim3(256), 0, s, a.kc, a.vc,
                              a.tok_stride, a.head_stride, a.chunk, a.bound, a.qsrc, a.qsrc_stride, a.nh, a.qn_w,
                              a.tail);
-        else
+        else if (a.U == 2)
           hipLaunchKernelGGL((decode_lanes_kernel<NQ, G, 2, FUSED, PAGED>), grid, dim3(256), 0, s, a.kc, a.vc,
+                             a.tok_stride, a.head_stride, a.chunk, a.bound, a.qsrc, a.qsrc_stride, a.nh, a.qn_w,
+                             a.tail);
+        else
+          hipLaunchKernelGGL((decode_lanes_kernel<NQ, G, 1, FUSED, PAGED>), grid, dim3(256), 0, s, a.kc, a.vc,
                              a.tok_stride, a.head_stride, a.chunk, a.bound, a.qsrc, a.qsrc_stride, a.nh, a.qn_w,
                              a.tail);
         return true;
@@ -1237,15 +1303,18 @@ static int prepare(const char* name, int nq, int nh, int nkv, int hd, void* k_ca
   a.lanes = nq == 1 && G <= kLanesMaxGroup && raw_chunk <= kLanesMaxChunk;
   const int gran = a.lanes ? 16 : kTile;
   a.chunk = ((raw_chunk + gran - 1) / gran) * gran;  // static key chunk per split
-  a.U = a.chunk >= 64 ? 4 : 2;
+  a.U = a.chunk >= 64 ? 4 : (a.chunk >= 32 ? 2 : 1);
   a.bound = bound;
   a.nh = nh;
   a.nkv = nkv;
-  a.n_split = n_split;
+  // Trailing splits without keys are dropped: they add nothing to the combine.
+  a.n_split = (bound + a.chunk - 1) / a.chunk;
   a.tail.pos0_dev = pos0_dev;
-  a.tail.ws_o = (float*)((char*)ws + w.o_off);
-  a.tail.ws_ml = (float*)((char*)ws + w.ml_off);
-  a.tail.tickets = single_launch_ok(nq, nh, nkv, n_split, a.lanes, a.chunk) ? (unsigned long long*)ws : nullptr;
+  a.tail.ws_o = (uint4*)((char*)ws + w.o_off);
+  a.tail.ws_ml = (uint4*)((char*)ws + w.ml_off);
+  a.tail.epochs = (unsigned*)ws;
+  a.tail.n_split = a.n_split;
+  a.tail.merge = merge_ok(nq * G, a.n_split, nkv) ? 1 : 0;
   a.tail.out = out;
   a.tail.qscale = scale * 1.4426950408889634f;
   a.tail.pos_limit = (int)max_len;
@@ -1259,7 +1328,7 @@ static int launch_all(const char* name, bool fused, int nq, const DecodeArgs& a,
   if (!dispatch_attn(G, nq, fused, a, s))
     return set_error(SOLORT_EINVAL, "%s: no kernel for nq=%d group=%d", name, nq, G);
   int rc = check_launch(name);
-  if (rc || a.n_split == 1 || a.tail.tickets) return rc;
+  if (rc || a.n_split == 1 || a.tail.merge) return rc;
   if (!dispatch_combine(G, nq, a, s))
     return set_error(SOLORT_EINVAL, "%s: no combine kernel for nq=%d group=%d", name, nq, G);
   return check_launch(name);

@@ -1,12 +1,14 @@
 // solort_decode_layer without a caller-supplied workspace, for callers that
-// cannot allocate device memory.  The splits' partials and the single-launch
-// tickets live in `scratch`, one fixed array per GPU (SOLORT_NOALLOC_SCRATCH_BYTES),
-// loaded with the library and held until the process ends.
+// cannot allocate device memory.  The splits' partials and the in-launch
+// merge's per-KV-head counters live in `scratch`, one fixed array per GPU
+// (SOLORT_NOALLOC_SCRATCH_BYTES), loaded with the library and held until the
+// process ends.
 //
-// The array starts zeroed (the tickets must start at zero; the kernels leave
-// them at zero after every call) and keeps the last call's partials, which
-// every call overwrites before reading.  All calls on one GPU share it, so
-// calls that overlap in time on one GPU race.
+// The array starts zeroed (the counters' first value) and keeps the last
+// call's counters and partials: each call advances the counters of its KV
+// heads and tags its partials with them, so no partial of an earlier call is
+// taken for one of this call.  All calls on one GPU share it, so calls that
+// overlap in time on one GPU race.
 //
 // In host code `scratch` names a host-side stand-in, not the device array:
 // its device address comes from hipGetSymbolAddress, once per device with

@@ -1,11 +1,14 @@
-"""Single-launch split combine: the placement it relies on, and equality with the two-launch combine.
+"""In-launch split merge: the placement it relies on, and equality with the two-launch combine.
 
-For long key chunks (the MFMA split kernel), the last split of each KV head to finish merges the
-head's partials inside the split kernel; the partials meet in the L2 of the XCD all of the head's
-splits run on.  These tests check the workgroup -> XCD placement on this device, and that both
-combine modes give the same bits (outputs and cache rows) for query groups 1, 2, 4 and 8, two new
-tokens, 16 KV heads and mostly empty splits, over many consecutive calls (each call's last split
-must leave the tickets at zero for the next) and over graph replays.
+With more than one split, each split stores its partial tagged with this launch's value of the
+KV head's counter; the last min(n_split, rows) splits of each head poll for the tags and merge
+one row each, in the XCD's L2 that all of the head's splits share.  These tests check the
+workgroup -> XCD placement on this device, and that both combine modes give the same bits
+(outputs and cache rows) for both split kernels (short chunks of one token, long chunks and
+several tokens), query groups 1 to 8, fewer splits than rows, split counts that are not
+multiples of 8, empty splits and 16 KV heads; over many consecutive calls (each call must
+advance the counters so that no partial of an earlier call is taken for a fresh one), over
+calls of different shapes sharing one workspace, and over graph replays.
 """
 from __future__ import annotations
 
@@ -44,7 +47,7 @@ def test_workgroups_round_robin_over_xcds(lib, gpu):
     xcc = out.view(n, 2)[:, 0].cpu()
     _say(f"XCD of workgroups 0..15: {xcc[:16].tolist()}; distinct XCDs {sorted(set(xcc.tolist()))}")
     assert torch.equal(xcc, xcc[torch.arange(n) % 8]), "workgroup b does not share the XCD of b % 8"
-    assert lib.solort_combine_mode(-1) == 1, "solort_init did not enable the single-launch combine"
+    assert lib.solort_combine_mode(-1) == 1, "solort_init did not enable the in-launch merge"
 
 
 def test_read_probe_reads_every_byte(lib, gpu):
@@ -61,8 +64,7 @@ def test_read_probe_reads_every_byte(lib, gpu):
         assert got == want, (n_wg, inflight)
 
 
-# (name, nh, nkv, max_len, bound, pos, n_split, nq): long chunks (at least 512 keys per split, the
-# MFMA split kernel), where the combine runs in the split kernel's launch
+# (name, nh, nkv, max_len, bound, pos, n_split, nq)
 CASES = [
     ("8B KV 32768", 32, 8, 32768, 32768, 32767, 32, 1),
     ("4B KV 16384, 16 splits", 32, 8, 16384, 16384, 12000, 16, 1),
@@ -72,6 +74,18 @@ CASES = [
     ("group 8", 64, 8, 8192, 8192, 7777, 16, 1),
     ("2 tokens, group 4", 32, 8, 8192, 8192, 6000, 16, 2),
     ("16 KV heads", 64, 16, 8192, 8192, 6500, 8, 1),
+    # short chunks (the lane-parallel split kernel)
+    ("8B KV 1024, 32 splits", 32, 8, 1024, 1024, 1000, 32, 1),
+    ("8B KV 1024, 64 splits of 16 keys", 32, 8, 1024, 1024, 1023, 64, 1),
+    ("0.6B KV 1024, 513 keys", 16, 8, 1024, 1024, 512, 32, 1),
+    ("group 8, 64 splits", 64, 8, 2048, 2048, 2047, 64, 1),
+    ("group 1, 12 splits", 8, 8, 384, 384, 300, 12, 1),
+    ("2 splits for 4 rows", 32, 8, 64, 64, 40, 2, 1),
+    ("20 splits, 4 empty", 32, 8, 1024, 1000, 999, 20, 1),
+    ("16 KV heads, short chunks", 64, 16, 1024, 1024, 777, 32, 1),
+    # verify: 5 tokens, 20 rows per KV head (both modes combine in a second launch)
+    ("verify, 32 splits", 32, 8, 4096, 4096, 2048, 32, 5),
+    ("verify, 8 splits for 20 rows", 32, 8, 4096, 4096, 3000, 8, 5),
 ]
 
 
@@ -85,7 +99,7 @@ def _inputs(nh, nkv, max_len, nq, seed):
 
 
 @pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
-def test_single_launch_equals_two_launch(lib, gpu, case):
+def test_in_launch_merge_equals_two_launch(lib, gpu, case):
     name, nh, nkv, max_len, bound, pos, ns, nq = case
     _say(f"[{name}] nh={nh} nkv={nkv} bound={bound} pos={pos} n_split={ns} nq={nq}")
     kc0, vc0, qkv, w = _inputs(nh, nkv, max_len, nq, 900 + nh + nkv + nq)
@@ -110,15 +124,17 @@ def test_single_launch_equals_two_launch(lib, gpu, case):
             assert torch.equal(x, y), name
 
 
-def test_single_launch_repeated_calls_and_graph_replays(lib, gpu):
-    """Consecutive calls at moving positions (each call's last split must clear the tickets), then
-    one graph of 12 calls replayed with eager work between the replays: every result equals the
-    two-launch combine's."""
-    nh, nkv, max_len, ns = 32, 8, 8192, 16
+@pytest.mark.parametrize("max_len,ns,first", [(8192, 16, 5000), (1024, 32, 600)], ids=["long chunks", "short chunks"])
+def test_in_launch_merge_repeated_calls_and_graph_replays(lib, gpu, max_len, ns, first):
+    """Consecutive calls at moving positions (each call must advance the counters), then one graph
+    of 12 calls replayed with eager work between the replays: every result equals the two-launch
+    combine's."""
+    nh, nkv = 32, 8
+    _say(f"[repeated calls] max_len={max_len} n_split={ns}")
     kc0, vc0, qkv, w = _inputs(nh, nkv, max_len, 1, 4242)
     qkv, w = qkv.to(gpu), w.to(gpu)
     inv = ops.inv_freq(HD, wl.THETA, gpu)
-    positions = list(range(5000, 8192, 97))
+    positions = list(range(first, max_len, (max_len - first) // 33 + 1))
 
     def run(mode):
         lib.solort_combine_mode(mode)
@@ -143,7 +159,7 @@ def test_single_launch_repeated_calls_and_graph_replays(lib, gpu):
     layers = 12
     kcs = [kc0.to(gpu) for _ in range(layers)]
     vcs = [vc0.to(gpu) for _ in range(layers)]
-    posb = torch.tensor([8000], dtype=torch.long, device=gpu)
+    posb = torch.tensor([max_len - 7], dtype=torch.long, device=gpu)
     cs = ops.rope_rows(inv, posb, 1)
     ws = ops.attn_workspace(1, nh, nkv, ns, gpu)
     outs = torch.zeros(layers, 1, nh * HD, dtype=torch.bfloat16, device=gpu)
@@ -171,3 +187,40 @@ def test_single_launch_repeated_calls_and_graph_replays(lib, gpu):
     step()
     torch.cuda.synchronize()
     assert torch.equal(outs, eager), "two-launch combine differs"
+
+
+def test_shapes_sharing_one_workspace(lib, gpu):
+    """Calls of different shapes (rows per head, split counts, KV heads) in turn on one workspace:
+    a partial left by one shape lies where another shape polls, and must never pass for fresh.
+    Every result equals the two-launch combine's on a workspace of its own."""
+    # (nq, nh, nkv, max_len, pos, n_split)
+    shapes = [(1, 32, 8, 1024, 1000, 32), (5, 32, 8, 4096, 3000, 32), (1, 64, 16, 1024, 900, 16),
+              (1, 16, 8, 2048, 2000, 64), (2, 32, 8, 8192, 6000, 16), (1, 8, 8, 384, 300, 12)]
+    inv = ops.inv_freq(HD, wl.THETA, gpu)
+    data = []
+    for i, (nq, nh, nkv, max_len, pos, ns) in enumerate(shapes):
+        kc, vc, qkv, w = _inputs(nh, nkv, max_len, nq, 77 + i)
+        posb = torch.tensor([pos], dtype=torch.long, device=gpu)
+        data.append((kc, vc, qkv.to(gpu), w.to(gpu), posb, ops.rope_rows(inv, posb, nq)))
+
+    def call(i, ws):
+        nq, nh, nkv, max_len, pos, ns = shapes[i]
+        kc0, vc0, qkv, w, posb, cs = data[i]
+        kc, vc = kc0.to(gpu), vc0.to(gpu)
+        out = torch.empty(nq, nh * HD, dtype=torch.bfloat16, device=gpu)
+        ops.decode_layer(qkv, w[0], w[1], wl.EPS, cs, posb, kc, vc, max_len, HD ** -0.5, ws, ns, out, nh, nkv)
+        return out
+
+    lib.solort_combine_mode(0)
+    want = []
+    for i, (nq, nh, nkv, max_len, pos, ns) in enumerate(shapes):
+        want.append(call(i, ops.attn_workspace(nq, nh, nkv, ns, gpu)).cpu())
+    lib.solort_combine_mode(1)
+    need = max(lib.solort_attn_workspace_bytes(nq, nh, nkv, HD, ns) for nq, nh, nkv, _, _, ns in shapes)
+    ws = torch.zeros(need, dtype=torch.uint8, device=gpu)
+    order = [0, 1, 2, 3, 4, 5, 1, 0, 3, 2, 5, 4, 0, 0, 1, 1, 2, 3, 4, 5, 0]
+    for n, i in enumerate(order):
+        _say(f"[shared workspace] call {n}: shape {shapes[i]}")
+        got = call(i, ws)
+        torch.cuda.synchronize()
+        assert torch.equal(got.cpu(), want[i]), (n, shapes[i])

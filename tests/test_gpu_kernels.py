@@ -339,7 +339,8 @@ def test_argmax_strided_rows(gpu):
 # ------------------------------------------------------------------ fused layer
 
 @pytest.mark.parametrize("index,live,n_split", [(1, 128, 4), (1, 256, 8), (1, 512, 16), (1, 1024, 32),
-                                                (1, 1024, 7), (0, None, 32), (3, None, 256), (4, None, 64)])
+                                                (1, 1024, 64), (1, 1024, 7), (0, None, 32), (3, None, 256),
+                                                (4, None, 64)])
 def test_decode_layer_equals_prologue_then_attention(gpu, index, live, n_split):
     """The fused launch writes the same KV bits and produces the same output bits as the two-launch path."""
     case = wl.decode_case(index, live=live, layers=1)

@@ -2,9 +2,9 @@
 
 It must give solort_decode_layer's bits (output and the new K/V rows) with the partials in the
 library's fixed scratch array: on two calls in a row, the second with a smaller input (the array
-keeps the first call's contents), for the short-chunk kernel with its second combine launch and
-the long-chunk kernel whose combine runs in the same launch (tickets in the array).  A request
-above the array's size is refused before any launch.
+keeps the first call's contents: counters and partials), for both split kernels, with the splits
+merged in the same launch (up to 8 query rows per KV head) or by the combine kernel (the 5-token
+verify).  A request above the array's size is refused before any launch.
 """
 from __future__ import annotations
 
@@ -64,7 +64,7 @@ def _call_both(gpu, lib, nh, nkv, max_len, bound, pos, ns, nq, dtype, seed):
 
 # (name, nh, nkv, max_len, bound, pos, n_split, nq): first call, then a smaller one
 PAIRS = [
-    (("Qwen3-8B KV 32768, single-launch combine", 32, 8, 32768, 32768, 32767, 32, 1),
+    (("Qwen3-8B KV 32768", 32, 8, 32768, 32768, 32767, 32, 1),
      ("KV 8192, 16 splits", 32, 8, 8192, 8192, 5000, 16, 1)),
     (("Qwen3-4B verify, 5 tokens over 4096", 32, 8, 4096, 4096, 2048, 32, 5),
      ("Qwen3-4B decode KV 1024", 32, 8, 1024, 1024, 1023, 32, 1)),
@@ -88,9 +88,9 @@ def test_noalloc_equals_decode_layer_twice(gpu, pair):
 def test_noalloc_refuses_requests_above_the_scratch(gpu):
     lib = _lib.load()
     p = ctypes.c_void_p(16 * 1024)  # never dereferenced: the size check fails first
-    nh, nkv, nq, ns = 64, 8, 4, 1024  # 8 heads x 1024 splits x 32 rows x 520 B, far above 4 MiB
+    nh, nkv, nq, ns = 64, 8, 4, 1024  # 8 heads x 1024 splits x 32 rows x 1040 B, far above 8 MiB
     need = lib.solort_attn_workspace_bytes(nq, nh, nkv, HD, ns)
-    assert need > (4 << 20)
+    assert need > (8 << 20)
     rc = lib.solort_decode_layer_noalloc(p, (nh + 2 * nkv) * HD, nq, nh, nkv, HD, p, p, 1e-6, p, p, p, p, 1024, 128,
                                          65536, 65536, 0.088, ns, p, 0, None)
     assert rc == EINVAL
