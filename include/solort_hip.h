@@ -387,9 +387,10 @@ int solort_greedy_advance(const void* ws, int vocab, const void* embed, int64_t 
                           solort_stream_t stream);
 
 /* Workspace bytes for solort_argmax_rows with `rows` rows: per row 64 slots
- * of 16 bytes and a 32-bit epoch (the launch count of the row, which tags the
- * slots each launch writes).  Allocate once, zero-fill once, reuse (16-byte
- * aligned); overlapping calls must not share it. */
+ * of 16 bytes, then the row's 32-bit epoch (the launch count of the row,
+ * which tags the slots each launch writes) in 16 bytes.  Allocate once,
+ * zero-fill once, reuse (16-byte aligned) for any call with no more rows;
+ * overlapping calls must not share it. */
 size_t solort_argmax_workspace_bytes(int rows);
 
 /*

@@ -14,10 +14,13 @@
 // path, and no slot needs clearing: a slot of an earlier launch carries an
 // earlier epoch.
 //
-// Workspace per row (zero-filled once): kMaxChunks slots of 16 bytes (key
-// low, key high, epoch, 0), then after all rows' slots one 32-bit epoch per
-// row.  A launch reads the row's epoch e and tags its slots e + 1 (never 0,
-// the zero-filled value, before 2^32 launches).
+// Workspace per row (zero-filled once): kMaxChunks slots of 16 bytes, two
+// 8-byte pairs (key low, epoch) and (key high, epoch), then the row's 32-bit
+// epoch in a 16-byte item, so that calls with any number of rows find a
+// row's slots and epoch at the same place.  A naturally aligned 8-byte store
+// is single-copy atomic, so a pair that carries the epoch carries its half of
+// the key.  A launch reads the row's epoch e and tags its slots e + 1 (never
+// 0, the zero-filled value, before 2^32 launches).
 //
 // Placement: block (x, y) = (row slot, chunk) has linear index x + rows8 y
 // with rows8 a multiple of 8, so all chunks of a row run on the XCD of row %
@@ -29,13 +32,13 @@
 namespace solort {
 
 constexpr int kMaxChunks = 64;     // chunks (blocks) per row
+constexpr int kRowItems = kMaxChunks + 1;  // 16-byte items per row: the slots, then the epoch
 constexpr int kArgmaxSpin = 1 << 20;  // polling rounds before the reader gives up (writes index -1)
 
 template <int F32>
 __global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict__ logits, int64_t vocab,
                                                           int64_t row_stride, int64_t per_block, int rows,
                                                           int vec_ok, uint4* __restrict__ slots,
-                                                          unsigned* __restrict__ epochs,
                                                           int64_t* __restrict__ out) {
   constexpr int VEC = F32 ? 4 : 8;  // elements per 16-byte load
   __shared__ uint64_t s_best[4];
@@ -67,15 +70,16 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict
     for (int e = 0; e < VEC; ++e)
       if (e < n) best = umax64(best, argmax_key(x[e], i + e));
   }
-  const unsigned ep = epochs[row] + 1u;  // this launch's tag
+  uint4* rs = slots + (int64_t)row * kRowItems;
+  unsigned* epoch = reinterpret_cast<unsigned*>(rs + kMaxChunks);
+  const unsigned ep = *epoch + 1u;  // this launch's tag
 #pragma unroll
   for (int mask = 32; mask >= 1; mask >>= 1) best = umax64(best, __shfl_xor(best, mask, 64));
   if ((tid & 63) == 0) s_best[tid >> 6] = best;
   __syncthreads();
   best = umax64(umax64(s_best[0], s_best[1]), umax64(s_best[2], s_best[3]));
-  uint4* rs = slots + (int64_t)row * kMaxChunks;
   if (chunk != nchunk - 1) {
-    if (tid == 0) rs[chunk] = make_uint4((uint32_t)best, (uint32_t)(best >> 32), ep, 0u);
+    if (tid == 0) rs[chunk] = make_uint4((uint32_t)best, ep, (uint32_t)(best >> 32), ep);
     return;
   }
   // The row's last block: lane j polls slot j with device-scope loads (they
@@ -88,8 +92,8 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict
   for (int it = 0; __builtin_amdgcn_ballot_w64(pend) != 0 && it < kArgmaxSpin; ++it) {
     asm volatile("" ::: "memory");
     const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, tid * 16, 0, 16));
-    if (pend && v.z == ep) {
-      k = ((uint64_t)v.y << 32) | v.x;
+    if (pend && v.y == ep && v.w == ep) {
+      k = ((uint64_t)v.z << 32) | v.x;
       pend = false;
     }
   }
@@ -98,11 +102,9 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict
   for (int mask = 32; mask >= 1; mask >>= 1) k = umax64(k, __shfl_xor(k, mask, 64));
   if (tid == 0) {
     out[row] = timed_out ? -1 : (int64_t)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
-    epochs[row] = ep;
+    *epoch = ep;
   }
 }
-
-static size_t slot_bytes(int rows) { return ((size_t)rows * kMaxChunks * 16 + 255) & ~(size_t)255; }
 
 }  // namespace solort
 
@@ -110,7 +112,7 @@ using namespace solort;
 
 extern "C" size_t solort_argmax_workspace_bytes(int rows) {
   if (rows < 1) return 0;
-  return slot_bytes(rows) + (((size_t)rows * 4 + 255) & ~(size_t)255);
+  return ((size_t)rows * kRowItems * 16 + 255) & ~(size_t)255;
 }
 
 extern "C" int solort_argmax_rows(const void* logits, int dtype, int rows, int64_t vocab,
@@ -137,14 +139,13 @@ extern "C" int solort_argmax_rows(const void* logits, int dtype, int rows, int64
   per_block = ((per_block + unit - 1) / unit) * unit;
   const int64_t nblk = (vocab + per_block - 1) / per_block;  // <= target
   uint4* slots = (uint4*)ws;
-  unsigned* epochs = (unsigned*)((char*)ws + slot_bytes(rows));
   const int rows8 = (rows + 7) & ~7;
   dim3 grid((unsigned)rows8, (unsigned)nblk);
   if (dtype == SOLORT_DTYPE_F32)
     hipLaunchKernelGGL(argmax_rows_kernel<1>, grid, dim3(256), 0, (hipStream_t)stream, logits, vocab,
-                       row_stride, per_block, rows, vec_ok, slots, epochs, out_idx);
+                       row_stride, per_block, rows, vec_ok, slots, out_idx);
   else
     hipLaunchKernelGGL(argmax_rows_kernel<0>, grid, dim3(256), 0, (hipStream_t)stream, logits, vocab,
-                       row_stride, per_block, rows, vec_ok, slots, epochs, out_idx);
+                       row_stride, per_block, rows, vec_ok, slots, out_idx);
   return check_launch("argmax_rows");
 }
