@@ -525,6 +525,26 @@ def model_extras(torch, dev, live: int = 960, n: int = 48) -> dict:
              "frac_hbm": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
              "first_tokens": m.tokens[:8].tolist()}
         if fused:
+            # the attention's cost inside the step: the same step captured without the attention
+            # call of each layer (its tokens are not the model's), timed the same way
+            m.attention_in_step = False
+            g0 = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g0):
+                m._step(1024)
+            ms0 = []
+            for _ in range(3):
+                m.start(11, live)
+                torch.cuda.synchronize()
+                e0.record(stream)
+                for _ in range(n):
+                    g0.replay()
+                e1.record(stream)
+                torch.cuda.synchronize()
+                ms0.append(e0.elapsed_time(e1) / n)
+            m.attention_in_step = True
+            del g0
+            r["attention_in_step_us_per_layer"] = round((ms - min(ms0)) * 1e3 / s.layers, 3)
+            r["step_without_attention_ms"] = round(min(ms0), 4)
             # time to first token: a prompt's prefill graph plus the last row's lm_head and argmax
             ttft = {}
             for plen in (128, 1024):

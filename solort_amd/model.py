@@ -93,6 +93,10 @@ class GraphQwen3Decode:
         speculative round (the verify graph scores spec_k + 1 tokens)."""
         self.w = weights
         self.fused_tail = bool(fused_tail)
+        # Measurement hook (bench.py): a decode graph captured with this False leaves the attention
+        # call out of every layer, so the difference in step time is the attention's cost inside
+        # the step.  Its tokens are not the model's.
+        self.attention_in_step = True
         s = self.s = weights.shape
         self.dev = weights.embed.device
         self.max_len, self.eps, self.scale = int(max_len), float(eps), HD ** -0.5
@@ -158,8 +162,9 @@ class GraphQwen3Decode:
         x = self.x.view(s.hidden)
         for li in range(s.layers):
             ops.gemv(w.wqkv[li], x, self.qkv.view(-1), w.in_ln[li], self.eps)                          # :170-171
-            ops.decode_layer(self.qkv, w.qn[li], w.kn[li], self.eps, self.cs, self.pos, self.kc[li],
-                             self.vc[li], bound, self.scale, self.ws, ns, self.ctx, s.nh, s.nkv)       # :172-184
+            if self.attention_in_step:
+                ops.decode_layer(self.qkv, w.qn[li], w.kn[li], self.eps, self.cs, self.pos, self.kc[li],
+                                 self.vc[li], bound, self.scale, self.ws, ns, self.ctx, s.nh, s.nkv)   # :172-184
             ops.gemv(w.wo[li], self.ctx.view(-1), x, res=x, mode=ops.GEMV_RESID)                       # :185
             ops.gemv(w.wgu[li], x, self.act, w.post_ln[li], self.eps, mode=ops.GEMV_SWIGLU,
                      inter=s.inter)                                                                    # :186-187
