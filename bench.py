@@ -45,6 +45,12 @@ def prefill_flops(T: int, nh: int = 32, hd: int = 128) -> int:
     return 4 * nh * hd * T * (T + 1) // 2
 
 
+def prefill_bytes(T: int, nh: int = 32, nkv: int = 8, hd: int = 128) -> int:
+    """Algorithmic HBM bytes of one layer's prefill attention block: the qkv rows read, the K/V
+    cache rows and the output rows written (bf16)."""
+    return T * hd * 2 * ((nh + 2 * nkv) + 2 * nkv + nh)
+
+
 def parse() -> argparse.Namespace:
     p = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     p.add_argument("--gpus", type=int, default=1)
@@ -686,24 +692,28 @@ def prefill_extras(torch, ops, runners, dev, sh) -> dict:
                                        sh.nh, sh.nkv)
             qs.append(q)
 
-        def run_all():
-            for i, r in enumerate(runners):
-                for li in range(sh.layers):
-                    ops.prefill_attn(qs[i], r.kc[li], r.vc[li], sh.scale, outs[(i + li) % 2])
-
-        graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
-            run_all()
-        graph.replay()
-        torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         reps = 3
-        e0.record(stream)
-        for _ in range(reps):
+
+        def kernel_us():
+            def run_all():
+                for i, r in enumerate(runners):
+                    for li in range(sh.layers):
+                        ops.prefill_attn(qs[i], r.kc[li], r.vc[li], sh.scale, outs[(i + li) % 2])
+
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                run_all()
             graph.replay()
-        e1.record(stream)
-        torch.cuda.synchronize()
-        kern_us = e0.elapsed_time(e1) * 1e3 / (reps * len(runners) * sh.layers)
+            torch.cuda.synchronize()
+            e0.record(stream)
+            for _ in range(reps):
+                graph.replay()
+            e1.record(stream)
+            torch.cuda.synchronize()
+            return e0.elapsed_time(e1) * 1e3 / (reps * len(runners) * sh.layers)
+
+        kern_us = kernel_us()
         # whole graphed prefill step (prologue + attention per layer)
         e0.record(stream)
         for i in range(reps):
@@ -713,9 +723,14 @@ def prefill_extras(torch, ops, runners, dev, sh) -> dict:
         step_us = e0.elapsed_time(e1) * 1e3 / (reps * sh.layers)
         fl = prefill_flops(T, sh.nh)
         tf = fl / (kern_us * 1e-6) / 1e12
+        # roofline at this T: min(MFMA peak, arithmetic intensity x HBM peak), with the
+        # algorithmic bytes of the attention block (qkv rows in, K/V rows and output out)
+        nbytes = prefill_bytes(T, sh.nh, sh.nkv)
+        roof = min(BF16_PEAK_TFLOPS, fl / nbytes * HBM_PEAK_GBS / 1e3)
         out[str(T)] = {"kernel_us": round(kern_us, 3), "tflops": round(tf, 2),
                        "frac_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4),
-                       "step_us_per_layer": round(step_us, 3), "flop": fl}
+                       "roofline_tflops": round(roof, 1), "frac_roofline": round(tf / roof, 4),
+                       "step_us_per_layer": round(step_us, 3), "flop": fl, "bytes": nbytes}
     return out
 
 

@@ -66,24 +66,37 @@ def source_id() -> int:
 EXTRA_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
-def _compile(src: Path, sid: int) -> Path:
+def _compile(src: Path, sid: int, reuse: bool = False) -> Path:
+    """Compiles one source; with `reuse`, an object whose recorded compile command and
+    inputs (the source, every csrc/ and include/ header) are unchanged is kept."""
+    import hashlib
     obj = OBJ_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), f"-DSOLORT_SOURCE_ID={sid}ULL", "-I",
+    # Only capi.hip reports the source id; other objects do not depend on it.
+    sid_flag = [f"-DSOLORT_SOURCE_ID={sid}ULL"] if src.name == "capi.hip" else []
+    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), *sid_flag, "-I",
            str(PKG.parent / "include"), "-c", str(src), "-o", str(obj)]
+    h = hashlib.sha256("\0".join(cmd).encode())
+    for f in [src, *sorted(CSRC.glob("*.h")), *sorted((PKG.parent / "include").glob("*.h"))]:
+        h.update(f.read_bytes())
+    stamp = obj.with_suffix(".stamp")
+    if reuse and obj.exists() and stamp.exists() and stamp.read_text() == h.hexdigest():
+        return obj
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{res.stderr}")
+    stamp.write_text(h.hexdigest())
     return obj
 
 
-def build(verbose: bool = False) -> Path:
-    """Compiles every csrc/*.hip for gfx950 and links LIB_PATH; returns its path."""
+def build(verbose: bool = False, reuse: bool = False) -> Path:
+    """Compiles every csrc/*.hip for gfx950 and links LIB_PATH; returns its path.  With `reuse`,
+    objects whose inputs and compile command are unchanged are not compiled again."""
     OBJ_DIR.mkdir(exist_ok=True)
     srcs = sources()
     jobs = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
     sid = source_id()
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(lambda f: _compile(f, sid), srcs))
+        objs = list(ex.map(lambda f: _compile(f, sid, reuse), srcs))
     tmp = LIB_PATH.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -96,5 +109,5 @@ def build(verbose: bool = False) -> Path:
 
 
 if __name__ == "__main__":
-    build(verbose=True)
+    build(verbose=True, reuse="--reuse" in sys.argv)
     sys.exit(0)

@@ -173,6 +173,19 @@ __device__ __forceinline__ void lds_barrier() {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Two fp32 values as tagged 8-byte pairs (value, tag, value, tag): a naturally
+// aligned 8-byte store is single-copy atomic, so a reader that finds the tag
+// it expects in a pair also holds that pair's value.  Workgroups of one launch
+// hand partial results to each other this way without fences or atomics.
+__device__ __forceinline__ uint4 tagged2(float x, float y, unsigned tag) {
+  return make_uint4(__float_as_uint(x), tag, __float_as_uint(y), tag);
+}
+
+// Device-scope 16-byte load (cache policy sc1): misses the CU's L1, reads the XCD's L2.
+__device__ __forceinline__ uint4 ld_l2(__amdgpu_buffer_rsrc_t r, int off) {
+  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16));
+}
+
 // Greedy-argmax key of (value, index): high word = an order-preserving image
 // of the fp32 value (-0 and +0 equal, NaN above every number), low word =
 // 0xffffffff - index, so the integer maximum is torch.argmax's answer (the

@@ -236,14 +236,6 @@ __device__ __forceinline__ unsigned merge_next(unsigned c) {
 }
 __device__ __forceinline__ unsigned merge_tag(unsigned n, int kvh) { return ((n & 0x1ffffffu) << 7) | (unsigned)kvh; }
 
-__device__ __forceinline__ uint4 tagged2(float x, float y, unsigned tag) {
-  return make_uint4(__float_as_uint(x), tag, __float_as_uint(y), tag);
-}
-
-// Device-scope 16-byte load (cache policy sc1): misses the CU's L1, reads the XCD's L2.
-__device__ __forceinline__ uint4 ld_l2(__amdgpu_buffer_rsrc_t r, int off) {
-  return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16));
-}
 
 // Merges the head's rows j, j + K, ... (see above) and writes them.  Called
 // by every thread of a merging block, after its own partial is stored; lds:
