@@ -64,14 +64,15 @@ def parse() -> argparse.Namespace:
     p.add_argument("--no-traffic", action="store_true",
                    help="skip the in-run HBM traffic measurement (two short rocprofv3 --pmc passes)")
     p.add_argument("--only", choices=("all", "decode", "prefill", "long", "verify", "gemv", "model", "paged",
-                                      "torchref", "floor", "cpu"),
+                                      "torchref", "floor", "cpu", "stamps"),
                    default="all",
                    help="decode: the decode step and its kernel only; prefill: the prefill kernels only; "
                         "long: the Qwen3-8B KV 32768 decode only; verify: the speculative verify and argmax "
                         "only; gemv: the decode-step GEMVs only; model: whole-model greedy decode only; paged: the "
                         "paged-KV decode only; torchref: the reference's torch decode ops on this GPU only; "
-                        "floor: the launch and streaming floor probes only; cpu: the CPU baselines only (for "
-                        "per-workload profiles)")
+                        "floor: the launch and streaming floor probes only; cpu: the CPU baselines only; stamps: "
+                        "in-kernel phase timelines of the decode (KV 1024, KV 32768) and prefill (T 1024) kernels "
+                        "from the tracing build (python -m solort_amd.build --stamps) (for per-workload profiles)")
     return p.parse_args()
 
 
@@ -87,7 +88,10 @@ def main() -> int:
 
     import torch
 
-    from solort_amd import _lib, ops
+    from solort_amd import _lib
+    if args.only == "stamps":
+        _lib.use_stamp_build()
+    from solort_amd import ops
     from solort_amd import workloads as wl
     from solort_amd.runner import GraphQwen3Attention, decode_splits
 
@@ -137,6 +141,9 @@ def main() -> int:
         return 0
     if args.only == "floor":
         print(json.dumps({"floor": floor_extras(torch, ops, runners, dev, sh)}), flush=True)
+        return 0
+    if args.only == "stamps":
+        print(json.dumps({"stamps": stamp_extras(torch, ops, wl, runners, dev, sh, bound)}), flush=True)
         return 0
     if args.only == "model":
         del runners
@@ -323,6 +330,101 @@ def floor_extras(torch, ops, runners, dev, sh) -> dict:
         torch, dev, [lambda x=x: (read(x.data_ptr(), 4 << 20, 256, 1), read(small.data_ptr(), 512 << 10, 32, 4))
                      for x in slices], reps=4), 3)
     res["slices"] = len(slices)
+    return res
+
+
+STAMP_PHASES_DECODE = {0: "start", 1: "position read", 2: "q ready", 3: "key loop done", 4: "partial stored",
+                       5: "end", 6: "merge poll started", 7: "merge poll done"}
+STAMP_PHASES_PREFILL = {0: "start", 3: "key loop done", 5: "end"}
+
+
+def _stamp_summary(np, st, phases, groups=None) -> dict:
+    """Per phase: min / median / p90 / max in microseconds after the launch's first workgroup start
+    (100 MHz ticks), over the workgroups that reached it; optional per-group medians of one phase."""
+    st = st.astype(np.int64)
+    t0 = st[:, 0].min()
+    out = {}
+    for i, name in phases.items():
+        v = st[:, i]
+        v = (v[(v >= t0) & (v < t0 + 10_000_000)] - t0) / 100.0  # this launch's stamps only
+        if v.size:
+            out[name] = {"min": round(float(v.min()), 2), "median": round(float(np.median(v)), 2),
+                         "p90": round(float(np.percentile(v, 90)), 2), "max": round(float(v.max()), 2),
+                         "workgroups": int(v.size)}
+    if groups is not None:
+        name, idx, col = groups
+        out[name] = [round(float(np.median((st[g, col] - t0) / 100.0)), 2) for g in idx]
+    return out
+
+
+def stamp_extras(torch, ops, wl, runners, dev, sh, bound) -> dict:
+    """In-kernel phase timelines from the tracing build (include/solort_trace.h): the last
+    solort_decode_layer launch of a replayed Qwen3-4B decode step at KV 1024, the last call of a
+    graph of 8 Qwen3-8B calls at KV 32768 (32 splits), and the last prefill_kernel launch of a graph
+    at T = 1024."""
+    import numpy as np
+
+    from solort_amd import _lib
+    from solort_amd.runner import decode_splits
+
+    lib = _lib.load()
+    res = {"clock": "s_memrealtime, 100 MHz; microseconds after the launch's first workgroup started"}
+
+    def read(fn, nb):
+        h = np.zeros(nb * 8, dtype=np.uint64)
+        _lib.check(getattr(lib, fn)(h.ctypes.data, nb), fn)
+        return h.reshape(nb, 8)
+
+    # Qwen3-4B decode at KV 1024: the step graph's last layer call
+    for i in range(4):
+        runners[i % len(runners)]._graphs[bound].replay()
+    torch.cuda.synchronize()
+    ns = decode_splits(bound, sh.nkv)
+    st = read("solort_phase_stamps_decode", sh.nkv * ns)
+    res["decode_qwen3_4b_kv1024"] = _stamp_summary(np, st, STAMP_PHASES_DECODE)
+    # Qwen3-8B at KV 32768, 32 splits: per-KV-head (one XCD each) median key-loop end
+    s8 = wl.QWEN3_8B
+    L, pos, nc = 32768, 32767, 8
+    gen = torch.Generator(device=dev).manual_seed(1003)
+    kcs = [torch.randn(L, s8.nkv, 128, generator=gen, device=dev).to(torch.bfloat16) for _ in range(nc)]
+    vcs = [torch.randn(L, s8.nkv, 128, generator=gen, device=dev).to(torch.bfloat16) for _ in range(nc)]
+    qkv = torch.randn(nc, 1, s8.qkv_width, generator=gen, device=dev).to(torch.bfloat16)
+    w = (1.0 + 0.1 * torch.randn(2, 128, generator=gen, device=dev)).to(torch.bfloat16)
+    posb = torch.tensor([pos], dtype=torch.long, device=dev)
+    cs = ops.rope_rows(ops.inv_freq(128, wl.THETA, dev), posb, 1)
+    out = torch.empty(1, s8.nh * 128, dtype=torch.bfloat16, device=dev)
+    ws = ops.attn_workspace(1, s8.nh, s8.nkv, 32, dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(nc):
+            ops.decode_layer(qkv[i], w[0], w[1], wl.EPS, cs, posb, kcs[i], vcs[i], L, s8.scale, ws, 32, out, s8.nh,
+                             s8.nkv)
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    st = read("solort_phase_stamps_decode", s8.nkv * 32)
+    heads = [[kvh + s8.nkv * sp for sp in range(32)] for kvh in range(s8.nkv)]
+    res["decode_qwen3_8b_kv32768"] = _stamp_summary(np, st, STAMP_PHASES_DECODE,
+                                                    ("key loop done, median per KV head", heads, 3))
+    del kcs, vcs
+    torch.cuda.empty_cache()
+    # prefill attention at T = 1024 over the first runner's cache
+    T = 1024
+    r = runners[0]
+    q = torch.randn(T, sh.nh, 128, generator=gen, device=dev).to(torch.bfloat16)
+    o = torch.empty(T, sh.nh * 128, dtype=torch.bfloat16, device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for li in range(4):
+            ops.prefill_attn(q, r.kc[li], r.vc[li], sh.scale, o)
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    nb = (T // 32) * sh.nkv
+    st = read("solort_phase_stamps_prefill", nb)
+    tiles = [[kvh + sh.nkv * s for kvh in range(sh.nkv)] for s in range(T // 32)]  # heaviest tile first
+    res["prefill_qwen3_4b_t1024"] = _stamp_summary(np, st, STAMP_PHASES_PREFILL,
+                                                   ("end, median per query tile (heaviest first)", tiles, 5))
     return res
 
 

@@ -133,6 +133,24 @@ def _init_device(lib: ctypes.CDLL) -> None:
     _init_devices.add(dev)
 
 
+# Phase-stamp readers of the tracing build (include/solort_trace.h).
+TRACE_SIGNATURES: dict[str, tuple[object, list[object]]] = {
+    "solort_phase_stamps_decode": (c_int, [c_void_p, c_int]),
+    "solort_phase_stamps_prefill": (c_int, [c_void_p, c_int]),
+}
+
+
+def use_stamp_build() -> None:
+    """Makes load() bind the tracing build (libsolort_hip_stamps.so: the same kernels with phase
+    stamps, python -m solort_amd.build --stamps) instead of the normal library.  Call before the
+    first load()."""
+    global LIB_PATH
+    if _lib is not None:
+        raise RuntimeError("use_stamp_build() must come before the library is loaded")
+    LIB_PATH = Path(__file__).resolve().parent / "libsolort_hip_stamps.so"
+    SIGNATURES.update(TRACE_SIGNATURES)
+
+
 def load() -> ctypes.CDLL:
     """Loads (once) and returns the library, initialised for the current device; raises
     RuntimeError if it is missing, of another ABI, or built from other sources."""
@@ -143,7 +161,8 @@ def load() -> ctypes.CDLL:
         return _lib
     if not LIB_PATH.exists():
         raise RuntimeError(
-            f"{LIB_PATH} is not built; run `python -m solort_amd.build` (hipcc, gfx950)"
+            f"{LIB_PATH} is not built; run `python -m solort_amd.build"
+            f"{' --stamps' if 'stamps' in LIB_PATH.name else ''}` (hipcc, gfx950)"
         )
     lib = ctypes.CDLL(str(LIB_PATH))
     for name, (restype, argtypes) in SIGNATURES.items():

@@ -1,7 +1,8 @@
 """Builds libsolort_hip.so (the gfx950 kernels + C ABI) in-tree with hipcc.
 
 Every HIP source under csrc/ is compiled for gfx950 only and linked into one
-shared library next to this file.  Usage: ``python -m solort_amd.build``.
+shared library next to this file.  Usage: ``python -m solort_amd.build
+[--reuse] [--stamps]`` (--stamps: the tracing build, libsolort_hip_stamps.so).
 """
 from __future__ import annotations
 
@@ -17,6 +18,9 @@ CSRC = PKG / "csrc"
 LIB_NAME = "libsolort_hip.so"
 LIB_PATH = PKG / LIB_NAME
 OBJ_DIR = PKG / "_build"
+# The tracing build (phase stamps in the decode and prefill kernels, include/solort_trace.h).
+STAMPS_LIB_PATH = PKG / "libsolort_hip_stamps.so"
+STAMPS_OBJ_DIR = PKG / "_build_stamps"
 
 ARCH = "gfx950"
 HIPCC_FLAGS = [
@@ -66,14 +70,15 @@ def source_id() -> int:
 EXTRA_FLAGS = {"prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"]}
 
 
-def _compile(src: Path, sid: int, reuse: bool = False) -> Path:
+def _compile(src: Path, sid: int, reuse: bool = False, stamps: bool = False) -> Path:
     """Compiles one source; with `reuse`, an object whose recorded compile command and
     inputs (the source, every csrc/ and include/ header) are unchanged is kept."""
     import hashlib
-    obj = OBJ_DIR / (src.stem + ".o")
+    obj = (STAMPS_OBJ_DIR if stamps else OBJ_DIR) / (src.stem + ".o")
     # Only capi.hip reports the source id; other objects do not depend on it.
     sid_flag = [f"-DSOLORT_SOURCE_ID={sid}ULL"] if src.name == "capi.hip" else []
-    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), *sid_flag, "-I",
+    stamp_flag = ["-DSOLORT_PHASE_STAMPS"] if stamps else []
+    cmd = [hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), *sid_flag, *stamp_flag, "-I",
            str(PKG.parent / "include"), "-c", str(src), "-o", str(obj)]
     h = hashlib.sha256("\0".join(cmd).encode())
     for f in [src, *sorted(CSRC.glob("*.h")), *sorted((PKG.parent / "include").glob("*.h"))]:
@@ -88,26 +93,28 @@ def _compile(src: Path, sid: int, reuse: bool = False) -> Path:
     return obj
 
 
-def build(verbose: bool = False, reuse: bool = False) -> Path:
-    """Compiles every csrc/*.hip for gfx950 and links LIB_PATH; returns its path.  With `reuse`,
-    objects whose inputs and compile command are unchanged are not compiled again."""
-    OBJ_DIR.mkdir(exist_ok=True)
+def build(verbose: bool = False, reuse: bool = False, stamps: bool = False) -> Path:
+    """Compiles every csrc/*.hip for gfx950 and links LIB_PATH (with `stamps`, the tracing build
+    STAMPS_LIB_PATH); returns its path.  With `reuse`, objects whose inputs and compile command are
+    unchanged are not compiled again."""
+    lib_path = STAMPS_LIB_PATH if stamps else LIB_PATH
+    (STAMPS_OBJ_DIR if stamps else OBJ_DIR).mkdir(exist_ok=True)
     srcs = sources()
     jobs = min(len(srcs), max(1, min(8, os.cpu_count() or 1)))
     sid = source_id()
     with cf.ThreadPoolExecutor(jobs) as ex:
-        objs = list(ex.map(lambda f: _compile(f, sid, reuse), srcs))
-    tmp = LIB_PATH.with_suffix(".so.tmp")
+        objs = list(ex.map(lambda f: _compile(f, sid, reuse, stamps), srcs))
+    tmp = lib_path.with_suffix(".so.tmp")
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", str(tmp), *map(str, objs)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
+    os.replace(tmp, lib_path)
     if verbose:
-        print(f"built {LIB_PATH} from {len(srcs)} sources")
-    return LIB_PATH
+        print(f"built {lib_path} from {len(srcs)} sources")
+    return lib_path
 
 
 if __name__ == "__main__":
-    build(verbose=True, reuse="--reuse" in sys.argv)
+    build(verbose=True, reuse="--reuse" in sys.argv, stamps="--stamps" in sys.argv)
     sys.exit(0)

@@ -173,6 +173,28 @@ __device__ __forceinline__ void lds_barrier() {
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Phase stamps (tracing build only).  A library built with SOLORT_PHASE_STAMPS
+// (python -m solort_amd.build --stamps, a separate .so) records, per workgroup
+// of the most recent launch of each instrumented kernel, the device clock
+// (s_memrealtime, 100 MHz) at fixed points of its work, in a per-source
+// array read back by solort_phase_stamps_* (declared in
+// include/solort_trace.h).  In the normal build SOLORT_STAMP is empty and the
+// kernels are unchanged.  SOLORT_STAMP_TU() defines the array once per source
+// file; slot i < 8 of linear workgroup b is written by the calling thread.
+constexpr int kStampBlocks = 4096;  // workgroups with stamps (later ones are skipped)
+constexpr int kStampSlots = 8;
+#ifdef SOLORT_PHASE_STAMPS
+#define SOLORT_STAMP_TU() __device__ unsigned long long g_phase_stamps[kStampBlocks * kStampSlots]
+#define SOLORT_STAMP(cond, b, i)                                                        \
+  do {                                                                                 \
+    if ((cond) && (b) < kStampBlocks)                                                  \
+      g_phase_stamps[(b) * kStampSlots + (i)] = __builtin_amdgcn_s_memrealtime();       \
+  } while (0)
+#else
+#define SOLORT_STAMP_TU() static_assert(true, "")
+#define SOLORT_STAMP(cond, b, i) ((void)0)
+#endif
+
 // Two fp32 values as tagged 8-byte pairs (value, tag, value, tag): a naturally
 // aligned 8-byte store is single-copy atomic, so a reader that finds the tag
 // it expects in a pair also holds that pair's value.  Workgroups of one launch

@@ -58,6 +58,8 @@
 
 namespace solort {
 
+SOLORT_STAMP_TU();  // phase stamps of the tracing build (common.h)
+
 // The kernel's leading arguments are the ones its first loads need; the
 // compiler preloads the leading kernel arguments into SGPRs (14 dwords, see
 // -amdgpu-kernarg-preload-count in the build), so those loads issue without
@@ -268,6 +270,7 @@ __device__ __forceinline__ void split_merge(const DecodeTail& a, int kvh, int sp
       ov[k] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
     bool pend = true;
+    SOLORT_STAMP(tid == 0 && r == j, blockIdx.x + gridDim.x * blockIdx.y, 6);
     for (int it = 0; it < kMergeSpin; ++it) {
       asm volatile("" ::: "memory");  // a fresh load every round
       uint4 mv[kCombB], xv[kCombB], yv[kCombB];
@@ -294,6 +297,7 @@ __device__ __forceinline__ void split_merge(const DecodeTail& a, int kvh, int sp
       if (__builtin_amdgcn_ballot_w64(pend) == 0) break;
     }
     if (pend) s_bad = 1;
+    SOLORT_STAMP(tid == 0 && r == j, blockIdx.x + gridDim.x * blockIdx.y, 7);
     CombAcc acc = comb_init();
     comb_merge<kCombB>(acc, ml, ov);
     s_m[sg * 32 + c] = acc.m;
@@ -334,6 +338,7 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
   const int nkv = nh / G;  // = gridDim.x, without the hidden-argument load
   const int kbeg = min(split * chunk, bound);
   const int kstat = min(kbeg + chunk, bound);
+  SOLORT_STAMP(tid == 0, kvh + nkv * split, 0);
 
   // 1. Loads for this slot's first prologue row (fused: with its norm
   //    weights and its token's cos/sin), issued before the K/V loads: vector
@@ -377,6 +382,7 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
   __builtin_amdgcn_sched_barrier(0);  // every K/V load issues before the position is read
 
   const int64_t pos0 = a.pos0_dev[0];
+  SOLORT_STAMP(tid == 0, kvh + nkv * split, 1);
 
   // 3. q rows (and, fused, the new tokens' K/V rows) into LDS.
   for (int row = slot; row < NROWS; row += 16) {
@@ -421,6 +427,7 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
 #pragma unroll
   for (int r = 0; r < R; ++r) qb[r] = s_q[r * 16 + j];
 
+  SOLORT_STAMP(tid == 0, kvh + nkv * split, 2);
   // 4. Per iteration: the 16 slots score U keys each (bf16 pair dot products
   //    over the slot's 16 lanes, reduced with DPP) and stage the scores and V
   //    rows in LDS.  Then each wavefront takes the rows it owns (wave + 4i):
@@ -542,6 +549,7 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
     }
   }
 
+  SOLORT_STAMP(tid == 0, kvh + nkv * split, 3);
   // 5. One split: the answer; otherwise this split's tagged partial (max,
   //    sum, unnormalised output), merged in this launch or by the combine
   //    kernel.
@@ -566,8 +574,10 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
       if (lane == 0) reinterpret_cast<float2*>(a.ws_ml)[pr] = make_float2(M[i], Ls);
     }
   }
+  SOLORT_STAMP(tid == 0, kvh + nkv * split, 4);
   // s_v (>= 6 KiB) is free: every wave passed the loop's last barrier.
   if (NS > 1 && inl) split_merge<R>(a, kvh, split, NS, nh, G, tag, next, reinterpret_cast<uint8_t*>(s_v));
+  SOLORT_STAMP(tid == 0, kvh + nkv * split, 5);
 }
 
 // Arguments as the entry points pass them: the leading 14 dwords arrive
@@ -672,6 +682,7 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
   const int kbeg = min(split * chunk, bound);
   const int kstat = min(kbeg + chunk, bound);
   const int kclamp = kstat > kbeg ? kstat - 1 : (kbeg > 0 ? kbeg - 1 : 0);  // a row this split may read
+  SOLORT_STAMP(tid == 0, kvh + nkv * split, 0);
 
   // 1. Loads for this slot's prologue rows slot, slot + 16, ... (fused: with
   //    the norm weights and each row's token's cos/sin), issued before the K/V
@@ -715,6 +726,7 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
   KVTile kv = fetch_tile<PAGED>(kp, vp, tok_stride, kbeg + kTile * wave, kbeg, kstat, kclamp, lrow, a);
 
   const int64_t pos0 = a.pos0_dev[0];
+  SOLORT_STAMP(tid == 0, kvh + nkv * split, 1);
 
   // 3. q rows (and, fused, the new tokens' K/V rows) into LDS; rows R..31 of
   //    the q tile are zero.  Fused: every pass's row is normalised first,
@@ -770,6 +782,7 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
     qb[kk] = as_bf16x8(*reinterpret_cast<const uint4*>(&s_q[l32 * kQStride + 16 * kk + 8 * hi]));
   lds_barrier();  // the q tile's space becomes the waves' K/V tiles
 
+  SOLORT_STAMP(tid == 0, kvh + nkv * split, 2);
   // 4. Key tiles k0 = kbeg + 32 wave + 128 i.  Per tile: V into this wave's
   //    LDS tile, S^T = K q^T (8 MFMAs), the next tile's loads, softmax with a
   //    lazy maximum, then O^T += V^T P^T with P split into bf16 high and low
@@ -871,6 +884,7 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
     }
   }
 
+  SOLORT_STAMP(tid == 0, kvh + nkv * split, 3);
   // 5. Merge the wavefronts that saw keys (log-sum-exp) and write this
   //    split's partial (max in log2 units, sum, unnormalised output) or, with
   //    one split, the answer.  O^T: lane l, register i of o[dt] holds dim
@@ -978,9 +992,11 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
         reinterpret_cast<float2*>(a.ws_ml)[pr] = make_float2(mq, lsum);
     }
   }
+  SOLORT_STAMP(tid == 0, kvh + nkv * split, 4);
   // s_x is free: the merge above read it before its last barrier, and the
   // in-launch merge's first barrier comes before any of its LDS writes.
   if (NS > 1 && inl) split_merge<R>(a, kvh, split, NS, nh, G, tag, next, s_x);
+  SOLORT_STAMP(tid == 0, kvh + nkv * split, 5);
 }
 
 // Arguments as the entry points pass them: the leading 14 dwords arrive
@@ -1445,3 +1461,14 @@ extern "C" int solort_paged_decode_layer(const void* qkv, int64_t qkv_row_stride
   a.tail.num_pages = num_pages;
   return launch_all(name, true, nq, a, (hipStream_t)stream);
 }
+
+#ifdef SOLORT_PHASE_STAMPS
+// Tracing build: copies the phase stamps of the split kernels' most recent
+// launch (n_blocks workgroups, linear index kvh + nkv * split) to host.
+extern "C" int solort_phase_stamps_decode(void* host, int n_blocks) {
+  if (!host || n_blocks < 1 || n_blocks > kStampBlocks) return set_error(SOLORT_EINVAL, "phase_stamps_decode: bad arguments");
+  const hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(g_phase_stamps), (size_t)n_blocks * kStampSlots * 8, 0,
+                                           hipMemcpyDeviceToHost);
+  return e == hipSuccess ? 0 : set_error((int)e, "phase_stamps_decode: %s", hipGetErrorString(e));
+}
+#endif

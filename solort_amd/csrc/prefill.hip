@@ -46,6 +46,8 @@
 
 namespace solort {
 
+SOLORT_STAMP_TU();  // phase stamps of the tracing build (common.h)
+
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 
@@ -149,6 +151,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
   const int l32 = lane & 31, hi = lane >> 5;
   const int kvh = blockIdx.x % nkv;
   const int tile = n_qtiles - 1 - (int)(blockIdx.x / nkv);  // heaviest first
+  SOLORT_STAMP(tid == 0, (int)blockIdx.x, 0);
   const int p0 = tile * PB;
   const int head = kvh * G + (ww % G);
   const int pw = p0 + 32 * (ww / G);  // this wave's first position
@@ -351,6 +354,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
     if (j + 2 < nit) st = prefill_fetch(krs, vrs, voff, (j + 2) * kStage * ts2);
   }
 
+  SOLORT_STAMP(tid == 0, (int)blockIdx.x, 3);
   // Merge the two key halves of every row: half 1 hands (m, l, O) to half 0
   // through LDS (the staging buffers are free after the last barrier).
   float* xf = reinterpret_cast<float*>(&sK[0][0]) + ww * (66 * 64);  // [66][64] floats per wave pair
@@ -417,6 +421,7 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
       if (pw + r < T) *reinterpret_cast<uint4*>(out + (pw + r) * orow + c) = v;
     }
   }
+  SOLORT_STAMP(tid == 0, (int)blockIdx.x, 5);
 }
 
 }  // namespace solort
@@ -524,3 +529,14 @@ extern "C" int solort_prefill_layer(const void* qkv, int64_t qkv_row_stride, int
   return launch_prefill(name, qkv, qkv_row_stride, true, qn_w, rope_cs, eps, T, nh, nkv, k_cache, v_cache,
                         kv_tok_stride, kv_head_stride, scale, out, out_dtype, s);
 }
+
+#ifdef SOLORT_PHASE_STAMPS
+// Tracing build: copies the phase stamps of prefill_kernel's most recent
+// launch (n_blocks workgroups) to host.
+extern "C" int solort_phase_stamps_prefill(void* host, int n_blocks) {
+  if (!host || n_blocks < 1 || n_blocks > kStampBlocks) return set_error(SOLORT_EINVAL, "phase_stamps_prefill: bad arguments");
+  const hipError_t e = hipMemcpyFromSymbol(host, HIP_SYMBOL(g_phase_stamps), (size_t)n_blocks * kStampSlots * 8, 0,
+                                           hipMemcpyDeviceToHost);
+  return e == hipSuccess ? 0 : set_error((int)e, "phase_stamps_prefill: %s", hipGetErrorString(e));
+}
+#endif
