@@ -360,8 +360,8 @@ def _stamp_summary(np, st, phases, groups=None) -> dict:
 def stamp_extras(torch, ops, wl, runners, dev, sh, bound) -> dict:
     """In-kernel phase timelines from the tracing build (include/solort_trace.h): the last
     solort_decode_layer launch of a replayed Qwen3-4B decode step at KV 1024, the last call of a
-    graph of 8 Qwen3-8B calls at KV 32768 (32 splits), and the last prefill_kernel launch of a graph
-    at T = 1024."""
+    graph of 8 Qwen3-8B calls at KV 32768 (32 splits), the last of 4 verify calls (5 tokens at 2048,
+    the 17 splits that hold keys) and the last prefill_kernel launch of a graph at T = 1024."""
     import numpy as np
 
     from solort_amd import _lib
@@ -408,6 +408,28 @@ def stamp_extras(torch, ops, wl, runners, dev, sh, bound) -> dict:
                                                     ("key loop done, median per KV head", heads, 3))
     del kcs, vcs
     torch.cuda.empty_cache()
+    # speculative verify, 5 tokens at 2048 over a max-4096 cache (32 splits, the combine in a second
+    # launch): the split kernel's phases
+    pos0, K1, vb = 2048, 5, 4096
+    kc = torch.randn(vb, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16)
+    vc = torch.randn(vb, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16)
+    qv = torch.randn(K1, sh.qkv_width, generator=gen, device=dev).to(torch.bfloat16)
+    pv = torch.tensor([pos0], dtype=torch.long, device=dev)
+    csv = ops.rope_rows(runners[0].inv_freq, pv, K1)
+    wsv = ops.attn_workspace(K1, sh.nh, sh.nkv, 32, dev)
+    ov = torch.empty(K1, sh.nh * 128, dtype=torch.bfloat16, device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for li in range(4):
+            ops.decode_layer(qv, runners[0].qn_w[li], runners[0].kn_w[li], runners[0].eps, csv, pv, kc, vc, vb,
+                             sh.scale, wsv, 32, ov, sh.nh, sh.nkv)
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    st = read("solort_phase_stamps_decode", sh.nkv * 32)
+    live = [kvh + sh.nkv * sp for sp in range(17) for kvh in range(sh.nkv)]  # splits holding keys 0..2052
+    res["verify_qwen3_4b_5_tokens"] = _stamp_summary(np, st[live], STAMP_PHASES_DECODE)
+    del kc, vc
     # prefill attention at T = 1024 over the first runner's cache
     T = 1024
     r = runners[0]
