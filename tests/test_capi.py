@@ -175,3 +175,42 @@ def test_torch_front_end_refuses_cpu_tensors():
                         torch.zeros(1 << 20, dtype=torch.uint8), 32, torch.zeros(1, 4096))
     with pytest.raises(RuntimeError, match="ROCm device"):
         ops.argmax_rows(torch.zeros(1, 10), torch.zeros(1, dtype=torch.long), torch.zeros(512, dtype=torch.uint8))
+
+
+TRACE_HEADER = Path(__file__).resolve().parents[1] / "include" / "solort_trace.h"
+
+
+def test_trace_header_binding_and_builds_agree(lib):
+    """The tracing build's readers: declared in solort_trace.h exactly as bound, absent from the
+    normal library (its kernels carry no stamps), present in the tracing build when it is built."""
+    text = re.sub(r"/\*.*?\*/", "", TRACE_HEADER.read_text(), flags=re.S)
+    declared = sorted(set(re.findall(r"\b(solort_[a-z0-9_]+)\s*\(", text)))
+    assert declared == sorted(_lib.TRACE_SIGNATURES)
+    assert not set(declared) & set(_lib.SIGNATURES)
+    for name in declared:
+        assert not hasattr(lib, name), name
+    stamps = _lib.LIB_PATH.parent / "libsolort_hip_stamps.so"
+    if stamps.exists():  # loaded in a process of its own: it registers the same kernels
+        import subprocess
+        import sys
+        code = (f"import ctypes; l = ctypes.CDLL({str(stamps)!r}); "
+                f"print(all(hasattr(l, n) for n in {declared!r}), l.solort_abi_version())")
+        out = subprocess.run([sys.executable, "-c", code], capture_output=True, text=True, timeout=120)
+        assert out.stdout.split() == ["True", str(_lib.ABI_VERSION)], out.stderr
+
+
+def test_stamp_summary_on_synthetic_stamps():
+    """bench.py's phase summary: microseconds after the first start, stale and missing slots
+    (earlier launches, zeros) left out."""
+    import numpy as np
+
+    import bench
+
+    t0 = 10_000_000
+    st = np.zeros((4, 8), dtype=np.uint64)
+    st[:, 0] = [t0, t0 + 10, t0 + 20, t0 + 30]       # starts: 0, 0.1, 0.2, 0.3 us
+    st[:, 5] = [t0 + 500, t0 + 600, t0 + 700, 5]       # ends; the last is a stale stamp
+    s = bench._stamp_summary(np, st, {0: "start", 5: "end", 6: "never"})
+    assert s["start"]["max"] == 0.3 and s["start"]["workgroups"] == 4
+    assert s["end"] == {"min": 5.0, "median": 6.0, "p90": 6.8, "max": 7.0, "workgroups": 3}
+    assert "never" not in s
