@@ -40,6 +40,8 @@
 // XCD (block index mod 8).
 #include <math.h>
 
+#include <type_traits>
+
 #include "common.h"
 #include "capi_internal.h"
 #include "qknorm_rope.h"
@@ -355,72 +357,109 @@ __global__ __launch_bounds__(kThreads) void prefill_kernel(
   }
 
   SOLORT_STAMP(tid == 0, (int)blockIdx.x, 3);
-  // Merge the two key halves of every row: half 1 hands (m, l, O) to half 0
-  // through LDS (the staging buffers are free after the last barrier).
-  float* xf = reinterpret_cast<float*>(&sK[0][0]) + ww * (66 * 64);  // [66][64] floats per wave pair
-  if (kh == 1) {
+  // Merge the two key halves of every row, each half finishing 64 of the 128
+  // dims: half 0 dims 0..63 (o[0], o[1]), half 1 dims 64..127 (o[2], o[3]).
+  // Each wave hands the other half's dims and its (m, l) over through LDS (the
+  // staging buffers are free after the last barrier): region 2 ww + kh of
+  // kXWords floats, [8][64] float4 items (o[2 (1 - kh) + d][4 q .. 4 q + 3] at
+  // item 4 d + q) and [64] float2 (m, l).  Both halves then merge with half
+  // 0's values first (the same expressions in either wave).
+  constexpr int kXWords = 34 * 64;
+  float* const xs = reinterpret_cast<float*>(&sK[0][0]);
+  float* const mine = xs + (2 * ww + kh) * kXWords;        // written here, read by the other half
+  float* const theirs = xs + (2 * ww + 1 - kh) * kXWords;  // read here, then this wave's output staging
+  static_assert(8 * kXWords * 4 <= 2 * kStage * kKStride * 2, "the exchange regions fit the K staging buffers");
+  const auto hand_over = [&](auto khc) {
+    constexpr int OTHER = 2 - 2 * decltype(khc)::value;  // first dt the other half finishes
+    float4* const m4 = reinterpret_cast<float4*>(mine);
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int d = 0; d < 2; ++d)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) xf[(dt * 16 + i) * 64 + lane] = o[dt][i];
-    xf[64 * 64 + lane] = m;
-    xf[65 * 64 + lane] = lsum;
-  }
-  __syncthreads();
-  if (kh == 1) return;
-  {
-    const float m1 = xf[64 * 64 + lane], l1 = xf[65 * 64 + lane];
-    const float mt = fmaxf(m, m1);  // finite: half 0 saw key 0
-    const float a0 = fast_exp2((m - mt) * qs), a1 = fast_exp2((m1 - mt) * qs);  // m1 = -inf gives 0
-    lsum = fmaf(lsum, a0, l1 * a1);
+      for (int q4 = 0; q4 < 4; ++q4)
+        m4[(4 * d + q4) * 64 + lane] = make_float4(o[OTHER + d][4 * q4], o[OTHER + d][4 * q4 + 1],
+                                                   o[OTHER + d][4 * q4 + 2], o[OTHER + d][4 * q4 + 3]);
+    reinterpret_cast<float2*>(mine + 32 * 64)[lane] = make_float2(m, lsum);
+  };
+  const auto finish = [&](auto khc) {
+    constexpr int KH = decltype(khc)::value;
+    constexpr int OWN = 2 * KH;  // first dt finished here
+    const float2 ml = reinterpret_cast<const float2*>(theirs + 32 * 64)[lane];
+    const float m0 = KH == 0 ? m : ml.x, l0 = KH == 0 ? lsum : ml.y;  // half 0's
+    const float m1 = KH == 0 ? ml.x : m, l1 = KH == 0 ? ml.y : lsum;  // half 1's
+    const float mt = fmaxf(m0, m1);  // finite: half 0 saw key 0
+    const float a0 = fast_exp2((m0 - mt) * qs), a1 = fast_exp2((m1 - mt) * qs);  // m1 = -inf gives 0
+    const float lt = xor32_combine(fmaf(l0, a0, l1 * a1), [](float x, float y) { return x + y; });
+    const float inv = lt > 0.f ? 1.f / lt : 0.f;
+    const float4* const t4 = reinterpret_cast<const float4*>(theirs);
+    float r[2][16];  // dims 64 KH + 32 d + 8 g + 4 hi .. +3 of row l32, normalised
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int d = 0; d < 2; ++d)
 #pragma unroll
-      for (int i = 0; i < 16; ++i) o[dt][i] = fmaf(o[dt][i], a0, xf[(dt * 16 + i) * 64 + lane] * a1);
-  }
-
-  const float lt = xor32_combine(lsum, [](float x, float y) { return x + y; });  // both halves of the row
-  const float inv = lt > 0.f ? 1.f / lt : 0.f;
-  // Normalise and store through this wave's LDS area (its merge reads above
-  // come first in program order): lane (l32, hi) holds dims 32dt + 8g + 4hi
-  // .. +3 of row l32, the tile goes to LDS row-major, and each store
-  // instruction then writes whole 256-byte (bf16) or 512-byte (fp32) rows.
-  const int64_t orow = (int64_t)nh * SOLORT_HD;  // elements per output row
-  if constexpr (F32) {
-    constexpr int kOS = SOLORT_HD + 4;  // 528-byte rows: 32 * 132 floats fill the [66][64] area
+      for (int q4 = 0; q4 < 4; ++q4) {
+        const float4 v = t4[(4 * d + q4) * 64 + lane];
+        const float vo[4] = {v.x, v.y, v.z, v.w};
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g)
-        *reinterpret_cast<float4*>(xf + l32 * kOS + 32 * dt + 8 * g + 4 * hi) =
-            make_float4(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv, o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
-    float* out = reinterpret_cast<float*>(out_ptr) + (int64_t)head * SOLORT_HD;
-#pragma unroll
-    for (int it = 0; it < 16; ++it) {
-      const int r = 2 * it + (lane >> 5), c = 4 * (lane & 31);
-      const float4 v = *reinterpret_cast<const float4*>(xf + r * kOS + c);
-      if (pw + r < T) *reinterpret_cast<float4*>(out + (pw + r) * orow + c) = v;
-    }
-  } else {
-    constexpr int kOS = SOLORT_HD + 8;  // 272-byte rows
-    uint16_t* xo = reinterpret_cast<uint16_t*>(xf);
-#pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        uint2 pkd;
-        pkd.x = pack2(o[dt][4 * g] * inv, o[dt][4 * g + 1] * inv);
-        pkd.y = pack2(o[dt][4 * g + 2] * inv, o[dt][4 * g + 3] * inv);
-        *reinterpret_cast<uint2*>(xo + l32 * kOS + 32 * dt + 8 * g + 4 * hi) = pkd;
+        for (int e = 0; e < 4; ++e) {
+          const float own = o[OWN + d][4 * q4 + e];
+          const float h0 = KH == 0 ? own : vo[e], h1 = KH == 0 ? vo[e] : own;
+          r[d][4 * q4 + e] = fmaf(h0, a0, h1 * a1) * inv;
+        }
       }
-    uint16_t* out = reinterpret_cast<uint16_t*>(out_ptr) + (int64_t)head * SOLORT_HD;
+    // Stage this half's 64 dims of the 32 rows row-major in `theirs` (read
+    // above, in program order; the other half never touches it again), then
+    // each store instruction writes whole 128-byte (bf16) or 256-byte (fp32)
+    // half rows.
+    const int64_t orow = (int64_t)nh * SOLORT_HD;  // elements per output row
+    if constexpr (F32) {
+      constexpr int kOS = 64 + 4;  // 272-byte rows: 32 * 68 floats fill the region
+      static_assert(32 * kOS <= kXWords, "fp32 staging fits the region");
 #pragma unroll
-    for (int it = 0; it < 8; ++it) {
-      const int r = 4 * it + (lane >> 4), c = 8 * (lane & 15);
-      const uint4 v = *reinterpret_cast<const uint4*>(xo + r * kOS + c);
-      if (pw + r < T) *reinterpret_cast<uint4*>(out + (pw + r) * orow + c) = v;
+      for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+          *reinterpret_cast<float4*>(theirs + l32 * kOS + 32 * d + 8 * g + 4 * hi) =
+              make_float4(r[d][4 * g], r[d][4 * g + 1], r[d][4 * g + 2], r[d][4 * g + 3]);
+      float* out = reinterpret_cast<float*>(out_ptr) + (int64_t)head * SOLORT_HD + 64 * KH;
+#pragma unroll
+      for (int it = 0; it < 8; ++it) {
+        const int row = 4 * it + (lane >> 4), c = 4 * (lane & 15);
+        const float4 v = *reinterpret_cast<const float4*>(theirs + row * kOS + c);
+        typedef float f32x4n __attribute__((ext_vector_type(4)));
+        if (pw + row < T)
+          __builtin_nontemporal_store(f32x4n{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4n*>(out + (pw + row) * orow + c));
+      }
+    } else {
+      constexpr int kOS = 64 + 8;  // 144-byte rows
+      uint16_t* xo = reinterpret_cast<uint16_t*>(theirs);
+#pragma unroll
+      for (int d = 0; d < 2; ++d)
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          uint2 pkd;
+          pkd.x = pack2(r[d][4 * g], r[d][4 * g + 1]);
+          pkd.y = pack2(r[d][4 * g + 2], r[d][4 * g + 3]);
+          *reinterpret_cast<uint2*>(xo + l32 * kOS + 32 * d + 8 * g + 4 * hi) = pkd;
+        }
+      uint16_t* out = reinterpret_cast<uint16_t*>(out_ptr) + (int64_t)head * SOLORT_HD + 64 * KH;
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int row = 8 * it + (lane >> 3), c = 8 * (lane & 7);
+        const uint4 v = *reinterpret_cast<const uint4*>(xo + row * kOS + c);
+        typedef unsigned u32x4n __attribute__((ext_vector_type(4)));
+        if (pw + row < T)
+          __builtin_nontemporal_store(u32x4n{v.x, v.y, v.z, v.w}, reinterpret_cast<u32x4n*>(out + (pw + row) * orow + c));
+      }
     }
-  }
+  };
+  if (kh == 0)  // wave-uniform
+    hand_over(std::integral_constant<int, 0>{});
+  else
+    hand_over(std::integral_constant<int, 1>{});
+  __syncthreads();
+  if (kh == 0)
+    finish(std::integral_constant<int, 0>{});
+  else
+    finish(std::integral_constant<int, 1>{});
   SOLORT_STAMP(tid == 0, (int)blockIdx.x, 5);
 }
 
