@@ -203,6 +203,15 @@ __device__ __forceinline__ uint4 tagged2(float x, float y, unsigned tag) {
   return make_uint4(__float_as_uint(x), tag, __float_as_uint(y), tag);
 }
 
+// A load of data streamed once (weights, K/V rows) with the non-temporal
+// hint (`nt`): measured on MI355X, it speeds up the decode K/V streams and the
+// large weight streams (the hint keeps them from displacing cached data).
+__device__ __forceinline__ uint4 ld_stream(const void* p) {
+  typedef unsigned u32x4s __attribute__((ext_vector_type(4)));
+  const u32x4s v = __builtin_nontemporal_load(reinterpret_cast<const u32x4s*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Device-scope 16-byte load (cache policy sc1): misses the CU's L1, reads the XCD's L2.
 __device__ __forceinline__ uint4 ld_l2(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16));

@@ -376,8 +376,8 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
   for (int u = 0; u < U; ++u) {
     const int kid = min(kbeg + u * 16 + slot, kclamp);
     const int64_t off = row_off<PAGED>(kid, tok_stride, a);
-    kr[u] = *reinterpret_cast<const uint4*>(kp + off);
-    vr[u] = *reinterpret_cast<const uint4*>(vp + off);
+    kr[u] = ld_stream(kp + off);
+    vr[u] = ld_stream(vp + off);
   }
   __builtin_amdgcn_sched_barrier(0);  // every K/V load issues before the position is read
 
@@ -453,8 +453,8 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
       for (int u = 0; u < U; ++u) {
         const int kid = min(k1 + u * 16 + slot, kend - 1);
         const int64_t off = row_off<PAGED>(kid, tok_stride, a);
-        kn[u] = *reinterpret_cast<const uint4*>(kp + off);
-        vn[u] = *reinterpret_cast<const uint4*>(vp + off);
+        kn[u] = ld_stream(kp + off);
+        vn[u] = ld_stream(vp + off);
       }
     }
     float part[U * R];  // this lane's share of each score, index u * R + r
@@ -633,8 +633,11 @@ struct KVTile {
 };
 
 // Loads of the tile at key k0 (k0 past the split: its first rows again, which
-// are cached).  Rows are clamped to kclamp, a row the split may read.
-template <bool PAGED>
+// are cached).  Rows are clamped to kclamp, a row the split may read.  NT: the
+// non-temporal hint, for one new token (the long decode streams); the several
+// tokens of a verify step keep plain loads (measured: 10.45 against 10.6 us
+// per layer call with the hint).
+template <bool PAGED, bool NT>
 __device__ __forceinline__ KVTile fetch_tile(const uint16_t* kp, const uint16_t* vp, int tok_stride, int k0, int kbeg,
                                              int kstat, int kclamp, int lrow, const DecodeTail& a) {
   const int base = k0 < kstat ? k0 : kbeg;
@@ -647,8 +650,8 @@ __device__ __forceinline__ KVTile fetch_tile(const uint16_t* kp, const uint16_t*
       off = row_off<true>(min(base + lrow + 4 * i, kclamp), tok_stride, a);
     else
       off = whole ? off0 + i * step : (int64_t)min(base + lrow + 4 * i, kclamp) * tok_stride;
-    kd = *reinterpret_cast<const uint4*>(kp + off);
-    vd = *reinterpret_cast<const uint4*>(vp + off);
+    kd = NT ? ld_stream(kp + off) : *reinterpret_cast<const uint4*>(kp + off);
+    vd = NT ? ld_stream(vp + off) : *reinterpret_cast<const uint4*>(vp + off);
   };
   ld(0, t.k0, t.v0); ld(1, t.k1, t.v1); ld(2, t.k2, t.v2); ld(3, t.k3, t.v3);
   ld(4, t.k4, t.v4); ld(5, t.k5, t.v5); ld(6, t.k6, t.v6); ld(7, t.k7, t.v7);
@@ -723,7 +726,7 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
   const uint16_t* kp = kc + (int64_t)kvh * head_stride + 8 * j;
   const uint16_t* vp = vc + (int64_t)kvh * head_stride + 8 * j;
   const int lrow = lane >> 4;  // this lane's first row of the tile; rows lrow + 4i
-  KVTile kv = fetch_tile<PAGED>(kp, vp, tok_stride, kbeg + kTile * wave, kbeg, kstat, kclamp, lrow, a);
+  KVTile kv = fetch_tile<PAGED, NQ == 1>(kp, vp, tok_stride, kbeg + kTile * wave, kbeg, kstat, kclamp, lrow, a);
 
   const int64_t pos0 = a.pos0_dev[0];
   SOLORT_STAMP(tid == 0, kvh + nkv * split, 1);
@@ -820,7 +823,7 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
     stage_row(0, kv.k0, kv.v0); stage_row(1, kv.k1, kv.v1); stage_row(2, kv.k2, kv.v2); stage_row(3, kv.k3, kv.v3);
     stage_row(4, kv.k4, kv.v4); stage_row(5, kv.k5, kv.v5); stage_row(6, kv.k6, kv.v6); stage_row(7, kv.k7, kv.v7);
     // next tile (past the end: a re-read of cached rows)
-    kv = fetch_tile<PAGED>(kp, vp, tok_stride, k0 + 4 * kTile, kbeg, kstat, kclamp, lrow, a);
+    kv = fetch_tile<PAGED, NQ == 1>(kp, vp, tok_stride, k0 + 4 * kTile, kbeg, kstat, kclamp, lrow, a);
     f32x16 s = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
