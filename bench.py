@@ -739,8 +739,9 @@ def long_decode_extras(torch, ops, wl, dev, n_caches: int = 8) -> dict:
     res.update({"n_split": best[0], "us": round(best[1], 3), "gbps": round(best[2], 1),
                 "frac_hbm": round(best[2] / HBM_PEAK_GBS, 4)})
     # Streaming ceiling for the same traffic: a plain 16-byte streaming-read kernel (grid-stride,
-    # 1-4 loads in flight per thread) over the same 16 rotating 67 MB K and V buffers, one launch
-    # per buffer, in one graph; the best shape's GB/s, launches included.
+    # 2 or 4 loads in flight per thread, with and without the non-temporal hint the decode K/V
+    # loads carry) over the same 16 rotating 67 MB K and V buffers, one launch per buffer, in one
+    # graph; the best shape's GB/s, launches included.
     from solort_amd import _lib
     lib = _lib.load()
     sink = torch.zeros(4096, dtype=torch.int32, device=dev)
@@ -749,15 +750,16 @@ def long_decode_extras(torch, ops, wl, dev, n_caches: int = 8) -> dict:
     ceil = {}
     for n_wg in (512, 1024, 2048):
         for inflight in (2, 4):
-            def rd(x, n_wg=n_wg, inflight=inflight):
-                _lib.check(lib.solort_probe_read(x.data_ptr(), nbytes, n_wg, inflight, sink.data_ptr(),
-                                                 torch.cuda.current_stream(dev).cuda_stream), "probe_read")
-            us = _graph_us(torch, dev, [lambda x=x: rd(x) for x in bufs], reps=4)
-            ceil[f"{n_wg}x{inflight}"] = round(nbytes / (us * 1e-6) / 1e9, 1)
+            for nt in (0, 16):
+                def rd(x, n_wg=n_wg, inflight=inflight | nt):
+                    _lib.check(lib.solort_probe_read(x.data_ptr(), nbytes, n_wg, inflight, sink.data_ptr(),
+                                                     torch.cuda.current_stream(dev).cuda_stream), "probe_read")
+                us = _graph_us(torch, dev, [lambda x=x: rd(x) for x in bufs], reps=4)
+                ceil[f"{n_wg}x{inflight}{'nt' if nt else ''}"] = round(nbytes / (us * 1e-6) / 1e9, 1)
     top = max(ceil, key=ceil.get)
     res["stream_ceiling"] = {"gbps": ceil[top], "frac_hbm": round(ceil[top] / HBM_PEAK_GBS, 4), "shape": top,
                              "by_shape_gbps": ceil, "bytes_per_launch": nbytes,
-                             "note": "plain streaming read of the same rotated K/V buffers"}
+                             "note": "streaming read of the same rotated K/V buffers (nt: non-temporal loads)"}
     res["frac_of_stream_ceiling"] = round(best[2] / ceil[top], 4)
     del kcs, vcs
     torch.cuda.empty_cache()

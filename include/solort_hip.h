@@ -413,7 +413,9 @@ int solort_argmax_rows(const void* logits, int dtype, int rows, int64_t vocab, i
  * probe_empty: an empty kernel of n_wg workgroups of 64 threads.
  * probe_read: streams nbytes (a multiple of 16) from src with n_wg
  *   workgroups of 256 threads, in_flight (1, 2 or 4) 16-byte loads in flight
- *   per thread; workgroup b writes one word to sink[b] (sink: n_wg words).
+ *   per thread, plus 16 for loads with the non-temporal hint (the hint the
+ *   decode K/V and weight streams use); workgroup b writes one word to
+ *   sink[b] (sink: n_wg words).
  */
 int solort_probe_placement(uint32_t* out, int n_wg, solort_stream_t stream);
 int solort_probe_empty(int n_wg, solort_stream_t stream);

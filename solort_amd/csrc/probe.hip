@@ -27,10 +27,12 @@ __global__ __launch_bounds__(64) void placement_kernel(uint32_t* __restrict__ ou
 
 __global__ __launch_bounds__(64) void empty_kernel() {}
 
+constexpr int kProbeReadNT = 16;  // solort_probe_read's in_flight flag: non-temporal loads
+
 // Streaming read of n16 16-byte chunks, grid-stride, U loads in flight per
-// thread; each workgroup stores one word of the xor of what it read (so the
-// loads cannot be dropped).
-template <int U>
+// thread (NT: with the non-temporal hint); each workgroup stores one word of
+// the xor of what it read (so the loads cannot be dropped).
+template <int U, bool NT>
 __global__ __launch_bounds__(256) void read_kernel(const uint4* __restrict__ src, int64_t n16,
                                                    uint32_t* __restrict__ sink) {
   __shared__ uint32_t s_x[4];
@@ -39,7 +41,9 @@ __global__ __launch_bounds__(256) void read_kernel(const uint4* __restrict__ src
   for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride * U) {
     uint4 v[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) v[u] = i + u * stride < n16 ? src[i + u * stride] : make_uint4(0u, 0u, 0u, 0u);
+    for (int u = 0; u < U; ++u)
+      v[u] = i + u * stride < n16 ? (NT ? ld_stream(src + i + u * stride) : src[i + u * stride])
+                                  : make_uint4(0u, 0u, 0u, 0u);
 #pragma unroll
     for (int u = 0; u < U; ++u) x ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
   }
@@ -109,11 +113,17 @@ extern "C" int solort_probe_read(const void* src, int64_t nbytes, int n_wg, int 
   if (n_wg < 1 || n_wg > (1 << 20)) return set_error(SOLORT_EINVAL, "probe_read: n_wg %d", n_wg);
   const int64_t n16 = nbytes / 16;
   hipStream_t s = (hipStream_t)stream;
+#define SOLORT_READ(UU, NN) \
+  hipLaunchKernelGGL((read_kernel<UU, NN>), dim3(n_wg), dim3(256), 0, s, (const uint4*)src, n16, sink)
   switch (in_flight) {
-    case 1: hipLaunchKernelGGL(read_kernel<1>, dim3(n_wg), dim3(256), 0, s, (const uint4*)src, n16, sink); break;
-    case 2: hipLaunchKernelGGL(read_kernel<2>, dim3(n_wg), dim3(256), 0, s, (const uint4*)src, n16, sink); break;
-    case 4: hipLaunchKernelGGL(read_kernel<4>, dim3(n_wg), dim3(256), 0, s, (const uint4*)src, n16, sink); break;
-    default: return set_error(SOLORT_EINVAL, "probe_read: in_flight %d not in {1, 2, 4}", in_flight);
+    case 1: SOLORT_READ(1, false); break;
+    case 2: SOLORT_READ(2, false); break;
+    case 4: SOLORT_READ(4, false); break;
+    case 1 | kProbeReadNT: SOLORT_READ(1, true); break;
+    case 2 | kProbeReadNT: SOLORT_READ(2, true); break;
+    case 4 | kProbeReadNT: SOLORT_READ(4, true); break;
+    default: return set_error(SOLORT_EINVAL, "probe_read: in_flight %d not in {1, 2, 4} (+16: non-temporal)", in_flight);
   }
+#undef SOLORT_READ
   return check_launch("probe_read");
 }

@@ -55,7 +55,7 @@ def test_read_probe_reads_every_byte(lib, gpu):
     data = torch.randint(-2**31, 2**31 - 1, (1 << 20,), generator=g, dtype=torch.int64).to(torch.int32)
     want = int(np.bitwise_xor.reduce(data.numpy().view(np.uint32)))  # xor of every 32-bit word
     src = data.to(gpu)
-    for n_wg, inflight in ((256, 1), (512, 2), (37, 4)):
+    for n_wg, inflight in ((256, 1), (512, 2), (37, 4), (300, 2 | 16), (64, 4 | 16)):  # +16: non-temporal loads
         sink = torch.zeros(n_wg, dtype=torch.int32, device=gpu)
         _lib.check(lib.solort_probe_read(src.data_ptr(), src.numel() * 4, n_wg, inflight, sink.data_ptr(),
                                          torch.cuda.current_stream().cuda_stream), "probe_read")
