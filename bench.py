@@ -297,7 +297,8 @@ def floor_extras(torch, ops, runners, dev, sh) -> dict:
       empty_node_us      an empty kernel (1 workgroup) per graph node
       read_4mib_us       one launch streaming 4 MiB (the call's K and V bytes) with the call's 256
                          workgroups, one 16-byte load in flight per thread; and with 512 workgroups
-                         x 2 loads in flight (the best shape found)
+                         x 2 loads in flight (the best shape found); *_nt_us: both with
+                         the non-temporal hint
       read_4mib_then_32wg_us  the same read followed by a dependent 32-workgroup launch reading
                          512 KiB (the two-launch combine's shape)
     Sources rotate over 144 distinct 4 MiB slices of the rotated KV caches (576 MiB, beyond the 256
@@ -326,6 +327,11 @@ def floor_extras(torch, ops, runners, dev, sh) -> dict:
         torch, dev, [lambda x=x: read(x.data_ptr(), 4 << 20, 256, 1) for x in slices], reps=4), 3)
     res["read_4mib_512wg_x2_us"] = round(_graph_us(
         torch, dev, [lambda x=x: read(x.data_ptr(), 4 << 20, 512, 2) for x in slices], reps=4), 3)
+    # the same two shapes with the non-temporal hint the decode K/V loads carry
+    res["read_4mib_nt_us"] = round(_graph_us(
+        torch, dev, [lambda x=x: read(x.data_ptr(), 4 << 20, 256, 1 | 16) for x in slices], reps=4), 3)
+    res["read_4mib_512wg_x2_nt_us"] = round(_graph_us(
+        torch, dev, [lambda x=x: read(x.data_ptr(), 4 << 20, 512, 2 | 16) for x in slices], reps=4), 3)
     res["read_4mib_then_32wg_us"] = round(_graph_us(
         torch, dev, [lambda x=x: (read(x.data_ptr(), 4 << 20, 256, 1), read(small.data_ptr(), 512 << 10, 32, 4))
                      for x in slices], reps=4), 3)

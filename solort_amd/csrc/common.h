@@ -212,6 +212,18 @@ __device__ __forceinline__ uint4 ld_stream(const void* p) {
   return make_uint4(v.x, v.y, v.z, v.w);
 }
 
+// Stores with the non-temporal hint: the split partials of the two-launch
+// combine, read once by the next launch (5-token verify 10.44 -> 10.36 us per
+// call in one same-box A/B).
+__device__ __forceinline__ void st_stream(float4* p, float4 v) {
+  typedef float f32x4s __attribute__((ext_vector_type(4)));
+  __builtin_nontemporal_store(f32x4s{v.x, v.y, v.z, v.w}, reinterpret_cast<f32x4s*>(p));
+}
+__device__ __forceinline__ void st_stream(float2* p, float2 v) {
+  typedef float f32x2s __attribute__((ext_vector_type(2)));
+  __builtin_nontemporal_store(f32x2s{v.x, v.y}, reinterpret_cast<f32x2s*>(p));
+}
+
 // Device-scope 16-byte load (cache policy sc1): misses the CU's L1, reads the XCD's L2.
 __device__ __forceinline__ uint4 ld_l2(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16));

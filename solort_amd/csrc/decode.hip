@@ -570,8 +570,8 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
       a.ws_o[pr * 64 + lane] = tagged2(O[i][0], O[i][1], tag);
       if (lane == 0) a.ws_ml[pr] = tagged2(M[i], Ls, tag);
     } else {
-      reinterpret_cast<float2*>(a.ws_o)[pr * 64 + lane] = make_float2(O[i][0], O[i][1]);
-      if (lane == 0) reinterpret_cast<float2*>(a.ws_ml)[pr] = make_float2(M[i], Ls);
+      st_stream(reinterpret_cast<float2*>(a.ws_o) + pr * 64 + lane, make_float2(O[i][0], O[i][1]));
+      if (lane == 0) st_stream(reinterpret_cast<float2*>(a.ws_ml) + pr, make_float2(M[i], Ls));
     }
   }
   SOLORT_STAMP(tid == 0, kvh + nkv * split, 4);
@@ -971,8 +971,8 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
           dst[4 * q4] = tagged2(od[4 * q4], od[4 * q4 + 1], tag);
           dst[4 * q4 + 1] = tagged2(od[4 * q4 + 2], od[4 * q4 + 3], tag);
         } else {
-          reinterpret_cast<float4*>(a.ws_o)[((int64_t)(kvh * NS + split) * R + r) * 32 + 8 * dt + 2 * q4 + hi] =
-              make_float4(od[4 * q4], od[4 * q4 + 1], od[4 * q4 + 2], od[4 * q4 + 3]);
+          st_stream(reinterpret_cast<float4*>(a.ws_o) + ((int64_t)(kvh * NS + split) * R + r) * 32 + 8 * dt + 2 * q4 + hi,
+                    make_float4(od[4 * q4], od[4 * q4 + 1], od[4 * q4 + 2], od[4 * q4 + 3]));
         }
       }
     }
@@ -992,7 +992,7 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
       if (inl)
         a.ws_ml[pr] = tagged2(mq, lsum, tag);
       else
-        reinterpret_cast<float2*>(a.ws_ml)[pr] = make_float2(mq, lsum);
+        st_stream(reinterpret_cast<float2*>(a.ws_ml) + pr, make_float2(mq, lsum));
     }
   }
   SOLORT_STAMP(tid == 0, kvh + nkv * split, 4);
