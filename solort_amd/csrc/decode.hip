@@ -272,26 +272,32 @@ __device__ __forceinline__ void split_merge(const DecodeTail& a, int kvh, int sp
     bool pend = true;
     SOLORT_STAMP(tid == 0 && r == j, blockIdx.x + gridDim.x * blockIdx.y, 6);
     for (int it = 0; it < kMergeSpin; ++it) {
-      asm volatile("" ::: "memory");  // a fresh load every round
-      uint4 mv[kCombB], xv[kCombB], yv[kCombB];
-#pragma unroll
-      for (int k = 0; k < kCombB; ++k) {
-        if (k < nk) {
-          const int pr = (sg + 8 * k) * R + r;
-          mv[k] = ld_l2(rm, pr * 16);
-          xv[k] = ld_l2(ro, (pr * 64 + 2 * c) * 16);
-          yv[k] = ld_l2(ro, (pr * 64 + 2 * c + 1) * 16);
-        }
-      }
       pend = false;
+      // Splits in batches of four per thread (the second only past 32 splits): fewer registers.
 #pragma unroll
-      for (int k = 0; k < kCombB; ++k) {
-        if (k < nk) {
-          ml[k] = make_float2(__uint_as_float(mv[k].x), __uint_as_float(mv[k].z));
-          ov[k] = make_float4(__uint_as_float(xv[k].x), __uint_as_float(xv[k].z), __uint_as_float(yv[k].x),
-                              __uint_as_float(yv[k].z));
-          pend |= (mv[k].y != tag) | (mv[k].w != tag) | (xv[k].y != tag) | (xv[k].w != tag) | (yv[k].y != tag) |
-                  (yv[k].w != tag);
+      for (int k0 = 0; k0 < kCombB; k0 += 4) {
+        if (k0 < nk) {
+          asm volatile("" ::: "memory");  // a fresh load every round
+          uint4 mv[4], xv[4], yv[4];
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            if (k0 + k < nk) {
+              const int pr = (sg + 8 * (k0 + k)) * R + r;
+              mv[k] = ld_l2(rm, pr * 16);
+              xv[k] = ld_l2(ro, (pr * 64 + 2 * c) * 16);
+              yv[k] = ld_l2(ro, (pr * 64 + 2 * c + 1) * 16);
+            }
+          }
+#pragma unroll
+          for (int k = 0; k < 4; ++k) {
+            if (k0 + k < nk) {
+              ml[k0 + k] = make_float2(__uint_as_float(mv[k].x), __uint_as_float(mv[k].z));
+              ov[k0 + k] = make_float4(__uint_as_float(xv[k].x), __uint_as_float(xv[k].z),
+                                       __uint_as_float(yv[k].x), __uint_as_float(yv[k].z));
+              pend |= (mv[k].y != tag) | (mv[k].w != tag) | (xv[k].y != tag) | (xv[k].w != tag) |
+                      (yv[k].y != tag) | (yv[k].w != tag);
+            }
+          }
         }
       }
       if (__builtin_amdgcn_ballot_w64(pend) == 0) break;
