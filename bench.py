@@ -79,8 +79,8 @@ def parse() -> argparse.Namespace:
 def main() -> int:
     args = parse()
     if args.gpus != 1:
-        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): this build has no multi-GPU path; "
-              "each GPU would run its own KV heads or key splits (see DESIGN.md).", file=sys.stderr)
+        print(f"bench.py runs on one GPU only (got --gpus {args.gpus}): there is no multi-GPU path; "
+              "each GPU would run its own KV heads or key splits.", file=sys.stderr)
         return 2
     if args.only == "cpu":
         print(json.dumps({"cpu_baseline": cpu_baseline(args.cpu_seconds, args.live)}), flush=True)
@@ -1035,7 +1035,7 @@ def _median_us(fn, budget_s: float, warm: int = 5, min_runs: int = 20, max_runs:
 def cpu_baseline(budget_s: float, live: int) -> dict:
     """The oracle's fp32 torch restatement of the reference path (cuda_graph_executor.py; the
     reference's own method is synchronize + perf_counter over N replays, scripts/microbench_decode.py:
-    30-35) on the host cores, per BASELINE config, on the same seeded inputs as the GPU workloads:
+    30-35) on the host cores, per benchmark config, on the same seeded inputs as the GPU workloads:
       config 1  Qwen3-0.6B decode, all 28 layers, 513 keys (bucket 1024), in full
       config 2  Qwen3-4B decode, 36 layers, KV 128 / 256 / 512 / 1024 (`value`: KV `live`)
       config 3  Qwen3-4B prefill T = 512: prologue + KV write + causal attention, 6 of the 36 layers
