@@ -1,8 +1,8 @@
 """CPU oracle for the attention hot path -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
-this package, and only as the checker (or, for the CPU baseline, as the thing
-timed on the host).  The product path (solort_amd) never imports it and has
+this package, and only to check the HIP results against (or, for the CPU
+baseline, as the thing timed on the host).  The product path (solort_amd) never imports it and has
 no CPU fallback.
 
 Contents (every function cites the reference file:line it restates; paths are
