@@ -380,30 +380,48 @@ int solort_gemv_argmax(const void* w, int64_t w_row_stride, int n_out, int k, co
  * tokens[*step] when *step < max_tokens (the chunk's token list, :372-374),
  * *step and *pos advance by one (pos_buf, :242), and x [hidden] bf16 receives
  * embed row t (x = self.embed[self.tok_buf], :165).  embed [vocab,
- * embed_row_stride] bf16 16-byte aligned, hidden a multiple of 8.
+ * embed_row_stride] bf16 16-byte aligned, hidden a multiple of 8.  Keys that
+ * name no row of the vocabulary (ws not filled by solort_gemv_argmax) are
+ * recorded as token -1 in tokens, an error for the caller to report, and row
+ * 0 is embedded: no row outside embed is read.
  */
 int solort_greedy_advance(const void* ws, int vocab, const void* embed, int64_t embed_row_stride, int hidden,
                           void* x, int64_t* tok, int64_t* tokens, int max_tokens, int64_t* step, int64_t* pos,
                           solort_stream_t stream);
 
 /* Workspace bytes for solort_argmax_rows with `rows` rows: per row 64 slots
- * of 16 bytes, then the row's 32-bit epoch (the launch count of the row,
- * which tags the slots each launch writes) in 16 bytes.  Allocate once,
- * zero-fill once, reuse (16-byte aligned) for any call with no more rows;
- * overlapping calls must not share it. */
+ * of 16 bytes, then a 16-byte item whose first 32-bit word is the row's
+ * epoch (the launch count of the row, which tags the slots each launch
+ * writes) and whose second word counts the calls whose reduction failed
+ * (see solort_argmax_rows).  Allocate once, zero-fill once, reuse (16-byte
+ * aligned) for any call with no more rows; overlapping calls must not share
+ * it. */
 size_t solort_argmax_workspace_bytes(int rows);
 
 /*
  * Greedy argmax over each row of logits [rows, vocab] (row stride
  * `row_stride` elements), bf16 (dtype 0) or fp32 (dtype 1), into int64
  * out_idx[rows].  Ties go to the lowest index and NaN counts as the maximum
- * (first NaN wins), as torch.argmax does.  One launch: up to 64 blocks per
- * row each store their best key, and the row's last block reduces them.
- * Replaces cuda_graph_executor.py:201/:206 (in-graph), :234 (draft) and
- * :475 (verify) `argmax(-1)`.  rows <= 65528.
+ * (first NaN wins), as torch.argmax does.  Up to 64 blocks per row each
+ * store their best key; the row's last block reduces them in the same
+ * launch where solort_init's placement check passed (and solort_argmax_mode
+ * allows it), else a one-wavefront-per-row launch does after it.  Every
+ * index written lies in [0, vocab): a reduction that fails (a block's key
+ * never seen within the polling limit) writes the best key it found and
+ * adds 1 to the row's failure count in ws, which callers read at their next
+ * synchronisation.  Replaces cuda_graph_executor.py:201/:206 (in-graph),
+ * :234 (draft) and :475 (verify) `argmax(-1)`.  rows <= 65528.
  */
 int solort_argmax_rows(const void* logits, int dtype, int rows, int64_t vocab, int64_t row_stride,
                        int64_t* out_idx, void* ws, solort_stream_t stream);
+
+/*
+ * Reduction mode of solort_argmax_rows on the current device (no
+ * counterpart in the reference): 1 = one launch where the placement check
+ * passed, 0 = always the second launch, -1 = query only.  Returns the mode
+ * in effect.  Both give the same indices.
+ */
+int solort_argmax_mode(int mode);
 
 /*
  * Device probes (no counterpart in the reference): the launch and streaming

@@ -15,7 +15,7 @@ from pathlib import Path
 import torch  # noqa: F401  (loads torch's HIP runtime before ours)
 
 LIB_PATH = Path(__file__).resolve().parent / "libsolort_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 # name -> (restype, argtypes); mirrors include/solort_hip.h
 SIGNATURES: dict[str, tuple[object, list[object]]] = {
@@ -24,6 +24,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "solort_last_error": (ctypes.c_char_p, []),
     "solort_init": (c_int, []),
     "solort_combine_mode": (c_int, [c_int]),
+    "solort_argmax_mode": (c_int, [c_int]),
     "solort_probe_placement": (c_int, [c_void_p, c_int, c_void_p]),
     "solort_probe_empty": (c_int, [c_int, c_void_p]),
     "solort_probe_read": (c_int, [c_void_p, c_int64, c_int, c_int, c_void_p, c_void_p]),

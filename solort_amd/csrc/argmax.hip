@@ -8,24 +8,35 @@
 // 0xffffffff - index.  The row's answer is the maximum key.  Each row is cut
 // into chunks, one block each; a block reduces its chunk's keys (wave
 // shuffles, then LDS) and stores its best key in its slot of the row, tagged
-// with this launch's epoch; the row's last block polls the slots until every
-// one carries the epoch, reduces them, writes the index and advances the
-// row's epoch.  No atomic and no store acknowledgement lies on the row's
-// path, and no slot needs clearing: a slot of an earlier launch carries an
-// earlier epoch.
+// with this launch's epoch.  Two ways to reduce the slots:
+//   - one launch (where the placement below has been checked): the row's
+//     last block polls the slots until every one carries the epoch, reduces
+//     them, writes the index and advances the row's epoch.  No atomic and no
+//     store acknowledgement lies on the row's path, and no slot needs
+//     clearing: a slot of an earlier launch carries an earlier epoch.
+//   - two launches (placement unverified, or solort_argmax_mode(0)): every
+//     block stores its slot and a one-wavefront launch per row reduces the
+//     slots after the launch boundary and advances the epoch.
+// Both give the same index.
 //
 // Workspace per row (zero-filled once): kMaxChunks slots of 16 bytes, two
-// 8-byte pairs (key low, epoch) and (key high, epoch), then the row's 32-bit
-// epoch in a 16-byte item, so that calls with any number of rows find a
-// row's slots and epoch at the same place.  A naturally aligned 8-byte store
-// is single-copy atomic, so a pair that carries the epoch carries its half of
-// the key.  A launch reads the row's epoch e and tags its slots e + 1 (never
-// 0, the zero-filled value, before 2^32 launches).
+// 8-byte pairs (key low, epoch) and (key high, epoch), then a 16-byte item
+// holding the row's 32-bit epoch and, in the next word, the number of calls
+// whose reduction failed (a slot never carried its tag), so that calls with
+// any number of rows find a row's slots and epoch at the same place.  A
+// naturally aligned 8-byte store is single-copy atomic, so a pair that
+// carries the epoch carries its half of the key.  A launch reads the row's
+// epoch e and tags its slots e + 1 (never 0, the zero-filled value, before
+// 2^32 launches).  A failed reduction still writes an index inside the row
+// (the best key among the slots it found, its own chunk's included) and
+// counts the failure, which the host reads at its next synchronisation: no
+// index outside [0, vocab) is ever written.
 //
-// Placement: block (x, y) = (row slot, chunk) has linear index x + rows8 y
-// with rows8 a multiple of 8, so all chunks of a row run on the XCD of row %
-// 8 (workgroup b runs on the XCD of b % 8), where their slots meet in the L2;
-// the reading block is the row's last chunk, dispatched after the others.
+// Placement (one launch): block (x, y) = (row slot, chunk) has linear index
+// x + rows8 y with rows8 a multiple of 8, so all chunks of a row run on the
+// XCD of row % 8 (workgroup b runs on the XCD of b % 8, checked by
+// solort_init), where their slots meet in the L2; the reading block is the
+// row's last chunk, dispatched after the others.
 #include "common.h"
 #include "capi_internal.h"
 
@@ -33,9 +44,15 @@ namespace solort {
 
 constexpr int kMaxChunks = 64;     // chunks (blocks) per row
 constexpr int kRowItems = kMaxChunks + 1;  // 16-byte items per row: the slots, then the epoch
-constexpr int kArgmaxSpin = 1 << 20;  // polling rounds before the reader gives up (writes index -1)
+constexpr int kArgmaxSpin = 1 << 20;  // polling rounds before the reader gives up (counts a failure)
 
-template <int F32>
+__device__ __forceinline__ int64_t key_to_index(uint64_t k) {
+  return (int64_t)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
+}
+
+// ONE: the one-launch reduction (the row's last block polls); otherwise every
+// block stores its slot and argmax_finish_kernel reduces them.
+template <int F32, bool ONE>
 __global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict__ logits, int64_t vocab,
                                                           int64_t row_stride, int64_t per_block, int rows,
                                                           int vec_ok, uint4* __restrict__ slots,
@@ -78,7 +95,7 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict
   if ((tid & 63) == 0) s_best[tid >> 6] = best;
   __syncthreads();
   best = umax64(umax64(s_best[0], s_best[1]), umax64(s_best[2], s_best[3]));
-  if (chunk != nchunk - 1) {
+  if (!ONE || chunk != nchunk - 1) {
     if (tid == 0) rs[chunk] = make_uint4((uint32_t)best, ep, (uint32_t)(best >> 32), ep);
     return;
   }
@@ -101,14 +118,68 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict
 #pragma unroll
   for (int mask = 32; mask >= 1; mask >>= 1) k = umax64(k, __shfl_xor(k, mask, 64));
   if (tid == 0) {
-    out[row] = timed_out ? -1 : (int64_t)(0xffffffffu - (uint32_t)(k & 0xffffffffu));
+    // k holds at least this block's own key (its chunk is not empty), so the index is in the row.
+    out[row] = key_to_index(k);
+    if (timed_out) epoch[1] += 1u;
     *epoch = ep;
   }
+}
+
+// Two-launch reduction: one wavefront per row; lane j reads slot j (the
+// launch boundary orders these reads after the slot stores), checks its tag,
+// reduces, writes the index and advances the row's epoch.  A slot without
+// the tag (never expected) is left out and counted as a failure; with no
+// valid slot at all the index written is 0.
+__global__ __launch_bounds__(64) void argmax_finish_kernel(int nchunk, uint4* __restrict__ slots,
+                                                           int64_t* __restrict__ out) {
+  const int row = blockIdx.x, lane = threadIdx.x;
+  uint4* rs = slots + (int64_t)row * kRowItems;
+  unsigned* epoch = reinterpret_cast<unsigned*>(rs + kMaxChunks);
+  const unsigned ep = *epoch + 1u;
+  uint64_t k = 0;
+  bool bad = false;
+  if (lane < nchunk) {
+    const uint4 v = rs[lane];
+    if (v.y == ep && v.w == ep)
+      k = ((uint64_t)v.z << 32) | v.x;
+    else
+      bad = true;
+  }
+  const bool failed = __builtin_amdgcn_ballot_w64(bad) != 0;
+#pragma unroll
+  for (int mask = 32; mask >= 1; mask >>= 1) k = umax64(k, __shfl_xor(k, mask, 64));
+  if (lane == 0) {
+    out[row] = k ? key_to_index(k) : 0;
+    if (failed) epoch[1] += 1u;
+    *epoch = ep;
+  }
+}
+
+namespace {
+constexpr int kMaxDev = 64;
+int g_argmax_two[kMaxDev];  // per device: 1 forces the two-launch reduction (solort_argmax_mode(0))
+}  // namespace
+
+// The one-launch reduction needs the round-robin placement (checked by
+// solort_init) and must not be switched off.
+static bool argmax_one_launch() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return false;
+  return !g_argmax_two[dev] && xcd_round_robin(dev);
 }
 
 }  // namespace solort
 
 using namespace solort;
+
+extern "C" int solort_argmax_mode(int mode) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev)
+    return set_error(SOLORT_EINVAL, "argmax_mode: no current device");
+  if (mode != -1 && mode != 0 && mode != 1) return set_error(SOLORT_EINVAL, "argmax_mode: mode %d", mode);
+  if (mode >= 0) g_argmax_two[dev] = mode == 0;
+  return argmax_one_launch() ? 1 : 0;
+}
 
 extern "C" size_t solort_argmax_workspace_bytes(int rows) {
   if (rows < 1) return 0;
@@ -139,13 +210,27 @@ extern "C" int solort_argmax_rows(const void* logits, int dtype, int rows, int64
   per_block = ((per_block + unit - 1) / unit) * unit;
   const int64_t nblk = (vocab + per_block - 1) / per_block;  // <= target
   uint4* slots = (uint4*)ws;
-  const int rows8 = (rows + 7) & ~7;
-  dim3 grid((unsigned)rows8, (unsigned)nblk);
+  hipStream_t s = (hipStream_t)stream;
+  if (argmax_one_launch()) {
+    const int rows8 = (rows + 7) & ~7;
+    const dim3 grid((unsigned)rows8, (unsigned)nblk);
+    if (dtype == SOLORT_DTYPE_F32)
+      hipLaunchKernelGGL((argmax_rows_kernel<1, true>), grid, dim3(256), 0, s, logits, vocab, row_stride, per_block,
+                         rows, vec_ok, slots, out_idx);
+    else
+      hipLaunchKernelGGL((argmax_rows_kernel<0, true>), grid, dim3(256), 0, s, logits, vocab, row_stride, per_block,
+                         rows, vec_ok, slots, out_idx);
+    return check_launch("argmax_rows");
+  }
+  const dim3 grid((unsigned)rows, (unsigned)nblk);
   if (dtype == SOLORT_DTYPE_F32)
-    hipLaunchKernelGGL(argmax_rows_kernel<1>, grid, dim3(256), 0, (hipStream_t)stream, logits, vocab,
-                       row_stride, per_block, rows, vec_ok, slots, out_idx);
+    hipLaunchKernelGGL((argmax_rows_kernel<1, false>), grid, dim3(256), 0, s, logits, vocab, row_stride, per_block,
+                       rows, vec_ok, slots, out_idx);
   else
-    hipLaunchKernelGGL(argmax_rows_kernel<0>, grid, dim3(256), 0, (hipStream_t)stream, logits, vocab,
-                       row_stride, per_block, rows, vec_ok, slots, out_idx);
+    hipLaunchKernelGGL((argmax_rows_kernel<0, false>), grid, dim3(256), 0, s, logits, vocab, row_stride, per_block,
+                       rows, vec_ok, slots, out_idx);
+  const int rc = check_launch("argmax_rows");
+  if (rc) return rc;
+  hipLaunchKernelGGL(argmax_finish_kernel, dim3((unsigned)rows), dim3(64), 0, s, (int)nblk, slots, out_idx);
   return check_launch("argmax_rows");
 }

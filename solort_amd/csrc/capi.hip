@@ -26,7 +26,7 @@ int check_launch(const char* what) {
 
 }  // namespace solort
 
-extern "C" int solort_abi_version(void) { return 9; }
+extern "C" int solort_abi_version(void) { return 10; }
 
 #ifndef SOLORT_SOURCE_ID
 #define SOLORT_SOURCE_ID 0ULL

@@ -258,20 +258,25 @@ __global__ __launch_bounds__(1024) void argmax_keys_finish_kernel(const uint64_t
 
 // The greedy step's tail: the token the keys name becomes the next input
 // (tok), is recorded at tokens[step], step and pos advance by one, and its
-// embedding row is copied into x for the next step.
-__global__ __launch_bounds__(1024) void greedy_advance_kernel(const uint64_t* __restrict__ keys, int n,
+// embedding row is copied into x for the next step.  Keys that name no row
+// of the vocabulary (a workspace no solort_gemv_argmax call filled) are
+// recorded as token -1, which the host reads as an error, while row 0 is
+// embedded: no row outside the table is ever read.
+__global__ __launch_bounds__(1024) void greedy_advance_kernel(const uint64_t* __restrict__ keys, int n, int vocab,
                                                               const uint16_t* __restrict__ embed,
                                                               int64_t row_stride, int hidden,
                                                               uint16_t* __restrict__ x, int64_t* __restrict__ tok,
                                                               int64_t* __restrict__ tokens, int max_tokens,
                                                               int64_t* __restrict__ step, int64_t* __restrict__ pos) {
   const int64_t t = key_index(reduce_keys_1024(keys, n));
-  const uint4* src = reinterpret_cast<const uint4*>(embed + t * row_stride);
+  const bool ok = t >= 0 && t < vocab;
+  const int64_t te = ok ? t : 0;
+  const uint4* src = reinterpret_cast<const uint4*>(embed + te * row_stride);
   for (int i = threadIdx.x; i < hidden / 8; i += 1024) reinterpret_cast<uint4*>(x)[i] = src[i];
   if (threadIdx.x == 0) {
     const int64_t s = *step;
-    *tok = t;
-    if (s >= 0 && s < max_tokens) tokens[s] = t;
+    *tok = te;
+    if (s >= 0 && s < max_tokens) tokens[s] = ok ? t : -1;
     *step = s + 1;
     *pos += 1;
   }
@@ -406,7 +411,7 @@ extern "C" int solort_greedy_advance(const void* ws, int vocab, const void* embe
   int R = 0;
   const int nkeys = (int)gemv_blocks(vocab, kGemvArgmax, &R);
   hipLaunchKernelGGL(greedy_advance_kernel, dim3(1), dim3(1024), 0, (hipStream_t)stream, (const uint64_t*)ws, nkeys,
-                     (const uint16_t*)embed, embed_row_stride, hidden, (uint16_t*)x, tok, tokens, max_tokens, step,
+                     vocab, (const uint16_t*)embed, embed_row_stride, hidden, (uint16_t*)x, tok, tokens, max_tokens, step,
                      pos);
   return check_launch(name);
 }

@@ -265,7 +265,7 @@ class GraphQwen3Decode:
         self.prefill(ids)
         for i in range(n - 1):
             self.graph(self.bucket_for(plen + i)).replay()
-        return self.tokens[:n].tolist()
+        return self._read_tokens(n)
 
     def _verify_forward(self, bound: int) -> torch.Tensor:
         """cuda_graph_executor.py:245-268 for the k1 tokens in vtok at vpos0..vpos0+k1-1: library GEMMs
@@ -322,6 +322,9 @@ class GraphQwen3Decode:
         self.verify(pos)
         got = torch.cat([self.acc_ver, self.vtok[1:]]).tolist()  # the one synchronisation
         a, nxt, drafts = got[0], got[1], got[2:]
+        ops.check_tokens([nxt] + drafts, self.s.vocab, "speculative round")
+        if ops.argmax_failures(self.ws_argv, self.k1):
+            raise RuntimeError("speculative round: an argmax reduction failed (see solort_argmax_rows)")
         if a == k:
             draft.start(drafts[k - 1], pos + k)
             draft.graph(draft.bucket_for(pos + k)).replay()
@@ -336,7 +339,7 @@ class GraphQwen3Decode:
             raise RuntimeError(f"{plen} + {n} tokens and a round of {self.k1} exceed max_len")
         self.prefill(ids)
         draft.prefill(ids)
-        out = [int(self.tok.item())]
+        out = ops.check_tokens([int(self.tok.item())], self.s.vocab, "prefill")
         accepted = []
         while len(out) < n:
             toks = self.speculative_round(draft, out[-1], plen + len(out) - 1)
@@ -352,4 +355,12 @@ class GraphQwen3Decode:
         self.start(first_token, pos)
         for i in range(n):
             self.graph(self.bucket_for(pos + i)).replay()
-        return self.tokens[:n].tolist()
+        return self._read_tokens(n)
+
+    def _read_tokens(self, n: int) -> list[int]:
+        """The first n recorded tokens (one synchronisation), checked: every token in the vocabulary
+        and, with the separate-ops tail, no argmax reduction failed."""
+        toks = ops.check_tokens(self.tokens[:n].tolist(), self.s.vocab, "greedy decode")
+        if not self.fused_tail and ops.argmax_failures(self.ws_arg, 1):
+            raise RuntimeError("greedy decode: an argmax reduction failed (see solort_argmax_rows)")
+        return toks

@@ -440,6 +440,35 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor, ws: torch.Tensor) -> No
     _lib.check(rc, "argmax_rows")
 
 
+def argmax_mode(mode: int = -1) -> int:
+    """Reduction mode of argmax_rows on the current device: 1 = one launch (where the placement
+    check passed), 0 = always a second launch, -1 = query; returns the mode in effect."""
+    rc = _lib.load().solort_argmax_mode(int(mode))
+    if rc < 0:
+        _lib.check(rc, f"argmax_mode({mode})")
+    return rc
+
+
+# 16-byte items per argmax row: 64 chunk slots, then (epoch, failure count, -, -).
+_ARGMAX_ROW_ITEMS = 65
+
+
+def argmax_failures(ws: torch.Tensor, rows: int) -> int:
+    """Total failure count of the first `rows` rows of an argmax_rows workspace: calls whose
+    reduction did not see every block's key (their index is the best key found).  Reads the
+    device (one synchronisation)."""
+    w = ws[: rows * _ARGMAX_ROW_ITEMS * 16].view(torch.int32).view(rows, _ARGMAX_ROW_ITEMS * 4)
+    return int(w[:, 64 * 4 + 1].sum().item())
+
+
+def check_tokens(tokens: list[int], vocab: int, what: str) -> list[int]:
+    """Raises RuntimeError unless every token lies in [0, vocab)."""
+    bad = [t for t in tokens if not 0 <= t < vocab]
+    if bad:
+        raise RuntimeError(f"{what}: token(s) {bad[:4]} outside the vocabulary [0, {vocab})")
+    return tokens
+
+
 def accept_prefix(target: torch.Tensor, draft: torch.Tensor, out: torch.Tensor) -> None:
     """out[0] = length of the prefix of draft [k] that target [k+1] agrees with, out[1] = target[out[0]]
     (int64, on the device); see solort_accept_prefix."""

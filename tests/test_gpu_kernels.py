@@ -252,8 +252,8 @@ def test_prologue_skips_out_of_range_positions(gpu):
 
 # ------------------------------------------------------------------ argmax
 
-def _argmax_check(dev, x: torch.Tensor):
-    ws = ops.argmax_workspace(x.shape[0], dev)
+def _argmax_check(dev, x: torch.Tensor, ws: torch.Tensor | None = None):
+    ws = ops.argmax_workspace(x.shape[0], dev) if ws is None else ws
     out = torch.empty(x.shape[0], dtype=torch.long, device=dev)
     xd = x.to(dev)
     for _ in range(2):  # the workspace must be ready again after each call
@@ -261,6 +261,19 @@ def _argmax_check(dev, x: torch.Tensor):
         torch.cuda.synchronize()
         want = exact.argmax_first(x.float().numpy())
         assert np.array_equal(out.cpu().numpy(), want)
+    assert ops.argmax_failures(ws, x.shape[0]) == 0
+
+
+def _argmax_hard_rows() -> torch.Tensor:
+    x = torch.full((4, 151936), -5.0)
+    x[0, [151935, 70000, 2048, 2047]] = 3.0        # ties straddling block boundaries
+    x[1, 123456] = float("nan")
+    x[1, 99999] = float("inf")
+    x[1, 140000] = float("nan")                     # first NaN wins
+    x[2] = -0.0
+    x[2, 5] = 0.0                                   # -0 == +0: index 0 wins
+    x[3] = float("-inf")                            # all -inf: index 0
+    return x
 
 
 def test_argmax_planted_ties(gpu):
@@ -279,16 +292,44 @@ def test_argmax_shapes(gpu, rows, vocab):
 
 
 def test_argmax_ties_across_blocks_nan_and_zero(gpu):
-    x = torch.full((4, 151936), -5.0)
-    x[0, [151935, 70000, 2048, 2047]] = 3.0        # ties straddling block boundaries
-    x[1, 123456] = float("nan")
-    x[1, 99999] = float("inf")
-    x[1, 140000] = float("nan")                     # first NaN wins
-    x[2] = -0.0
-    x[2, 5] = 0.0                                   # -0 == +0: index 0 wins
-    x[3] = float("-inf")                            # all -inf: index 0
+    x = _argmax_hard_rows()
     _argmax_check(gpu, x)
     _argmax_check(gpu, x.to(torch.bfloat16))
+
+
+def test_argmax_two_launch_fallback(gpu):
+    """The second-launch reduction (used where the workgroup placement is unverified), forced by
+    the host switch, gives the one-launch indices on the planted-tie and NaN cases; one workspace
+    alternates between the two modes (each mode advances the same per-row epochs) and serves graph
+    replays in the fallback mode."""
+    assert ops.argmax_mode(-1) == 1, "solort_init did not enable the one-launch argmax"
+    case = wl.decode_case(4, layers=1)
+    hard = _argmax_hard_rows()
+    ws = ops.argmax_workspace(5, gpu)
+    try:
+        for mode in (0, 1, 0):
+            assert ops.argmax_mode(mode) == mode
+            _say(f"[argmax mode {mode}: planted ties, NaN, -0, -inf]")
+            _argmax_check(gpu, case.logits, ws)
+            _argmax_check(gpu, case.logits.float(), ws)
+            _argmax_check(gpu, hard, ws)
+            _argmax_check(gpu, hard.to(torch.bfloat16), ws)
+        ops.argmax_mode(0)
+        a = case.logits.to(gpu)
+        oa = torch.empty(a.shape[0], dtype=torch.long, device=gpu)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            ops.argmax_rows(a, oa, ws)
+        want = exact.argmax_first(case.logits.float().numpy())
+        for r in range(3):
+            oa.fill_(-7)
+            graph.replay()
+            torch.cuda.synchronize()
+            assert np.array_equal(oa.cpu().numpy(), want), f"replay {r}"
+            _argmax_check(gpu, hard, ws)  # eager work between replays
+    finally:
+        ops.argmax_mode(1)
+    assert ops.argmax_failures(ws, 5) == 0
 
 
 def test_argmax_workspace_across_shapes_and_graph_replays(gpu):
