@@ -205,6 +205,13 @@ def main() -> int:
                      "in_launch_merge": single},
     }
 
+    if args.only == "decode":
+        # A graph of 288 empty kernels, timed like the decode calls: under a kernel tracer its
+        # dispatches give the tracer's per-dispatch duration beside the decode kernel's.
+        def empty():
+            _lib.check(lib.solort_probe_empty(1, torch.cuda.current_stream(dev).cuda_stream), "probe_empty")
+        result["empty_node_us"] = round(_graph_us(torch, dev, [empty] * 288, reps=4), 3)
+
     if not args.no_sweep and args.only == "all":
         result["extras"] = extras(torch, ops, wl, runners, dev, sh)
         result["extras"]["floor"] = floor_extras(torch, ops, runners, dev, sh)
@@ -363,6 +370,31 @@ def _stamp_summary(np, st, phases, groups=None) -> dict:
     return out
 
 
+def _wave_stamps(np, st, heads) -> dict:
+    """Per-wavefront phases of the MFMA split kernel (slots 8 + w: key loop done by wavefront w,
+    12 + w: the loads of its last key tile issued), microseconds after the launch's first start:
+    percentiles over every wavefront, the spread of loop ends inside each workgroup, and per KV head
+    the last wavefront's loop end and the last workgroup's end."""
+    st = st.astype(np.int64)
+    t0 = st[:, 0].min()
+    us = (st - t0) / 100.0
+    ok = (st >= t0) & (st < t0 + 10_000_000)
+
+    def pct(v):
+        v = v[np.isfinite(v)]
+        return {"min": round(float(v.min()), 2), "median": round(float(np.median(v)), 2),
+                "p90": round(float(np.percentile(v, 90)), 2), "max": round(float(v.max()), 2)} if v.size else {}
+
+    done = np.where(ok[:, 8:12], us[:, 8:12], np.nan)
+    issued = np.where(ok[:, 12:16], us[:, 12:16], np.nan)
+    end = np.where(ok[:, 5], us[:, 5], np.nan)
+    return {"wave key loop done": pct(done.ravel()),
+            "wave last tile issued": pct(issued.ravel()),
+            "wave loop-end spread in a workgroup": pct(np.nanmax(done, 1) - np.nanmin(done, 1)),
+            "last wave loop done per KV head": [round(float(np.nanmax(done[h])), 2) for h in heads],
+            "last end per KV head": [round(float(np.nanmax(end[h])), 2) for h in heads]}
+
+
 def stamp_extras(torch, ops, wl, runners, dev, sh, bound) -> dict:
     """In-kernel phase timelines from the tracing build (include/solort_trace.h): the last
     solort_decode_layer launch of a replayed Qwen3-4B decode step at KV 1024, the last call of a
@@ -377,9 +409,9 @@ def stamp_extras(torch, ops, wl, runners, dev, sh, bound) -> dict:
     res = {"clock": "s_memrealtime, 100 MHz; microseconds after the launch's first workgroup started"}
 
     def read(fn, nb):
-        h = np.zeros(nb * 8, dtype=np.uint64)
+        h = np.zeros(nb * 16, dtype=np.uint64)
         _lib.check(getattr(lib, fn)(h.ctypes.data, nb), fn)
-        return h.reshape(nb, 8)
+        return h.reshape(nb, 16)
 
     # Qwen3-4B decode at KV 1024: the step graph's last layer call
     for i in range(4):
@@ -412,6 +444,7 @@ def stamp_extras(torch, ops, wl, runners, dev, sh, bound) -> dict:
     heads = [[kvh + s8.nkv * sp for sp in range(32)] for kvh in range(s8.nkv)]
     res["decode_qwen3_8b_kv32768"] = _stamp_summary(np, st, STAMP_PHASES_DECODE,
                                                     ("key loop done, median per KV head", heads, 3))
+    res["decode_qwen3_8b_kv32768"].update(_wave_stamps(np, st, heads))
     del kcs, vcs
     torch.cuda.empty_cache()
     # speculative verify, 5 tokens at 2048 over a max-4096 cache (32 splits, the combine in a second

@@ -10,13 +10,15 @@
  * (synchronous; call after the launch completed, outside graph capture).  The
  * normal library has neither the stamps nor these functions.
  *
- * Layout: 8 uint64 slots per workgroup, workgroup b at [8 b, 8 b + 8); slots
- * not reached by a workgroup keep their previous contents (clear them by
- * comparing against a launch's first stamp).
+ * Layout: 16 uint64 slots per workgroup, workgroup b at [16 b, 16 b + 16);
+ * slots not reached by a workgroup keep their previous contents (clear them
+ * by comparing against a launch's first stamp).
  *   decode split kernels (linear workgroup kvh + nkv * split):
  *     0 start, 1 position read, 2 q rows normalised and in LDS, 3 key loop
  *     done (wave 0), 4 partial stored, 5 end, 6 merge poll started and
- *     7 merge poll done (merging workgroups of the in-launch merge only)
+ *     7 merge poll done (merging workgroups of the in-launch merge only);
+ *     MFMA split kernel only: 8 + w key loop done by wavefront w, 12 + w
+ *     wavefront w issued the loads of its last key tile
  *   prefill_kernel (workgroup blockIdx.x):
  *     0 start, 3 key loop done (wave 0), 5 end (outputs stored)
  */

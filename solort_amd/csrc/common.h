@@ -180,9 +180,9 @@ __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_ex
 // array read back by solort_phase_stamps_* (declared in
 // include/solort_trace.h).  In the normal build SOLORT_STAMP is empty and the
 // kernels are unchanged.  SOLORT_STAMP_TU() defines the array once per source
-// file; slot i < 8 of linear workgroup b is written by the calling thread.
+// file; slot i < 16 of linear workgroup b is written by the calling thread.
 constexpr int kStampBlocks = 4096;  // workgroups with stamps (later ones are skipped)
-constexpr int kStampSlots = 8;
+constexpr int kStampSlots = 16;
 #ifdef SOLORT_PHASE_STAMPS
 #define SOLORT_STAMP_TU() __device__ unsigned long long g_phase_stamps[kStampBlocks * kStampSlots]
 #define SOLORT_STAMP(cond, b, i)                                                        \

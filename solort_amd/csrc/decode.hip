@@ -388,6 +388,11 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
   __builtin_amdgcn_sched_barrier(0);  // every K/V load issues before the position is read
 
   const int64_t pos0 = a.pos0_dev[0];
+  // The KV head's merge counter, read by every wave ahead of the staging barrier below: each wave
+  // of the block has read it before any partial of the block is stored, hence before the head's
+  // row-0 merger (which waits for every split's partial) can advance it; and its round trip
+  // overlaps the prologue instead of preceding the partial stores.
+  const unsigned next = a.merge ? merge_next(a.epochs[kvh * 32]) : 0u;
   SOLORT_STAMP(tid == 0, kvh + nkv * split, 1);
 
   // 3. q rows (and, fused, the new tokens' K/V rows) into LDS.
@@ -561,7 +566,6 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
   //    kernel.
   const int NS = a.n_split;
   const bool inl = a.merge;
-  const unsigned next = inl ? merge_next(a.epochs[kvh * 32]) : 0u;
   const unsigned tag = merge_tag(next, kvh);
 #pragma unroll
   for (int i = 0; i < RPW; ++i) {
@@ -735,6 +739,9 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
   KVTile kv = fetch_tile<PAGED, NQ == 1>(kp, vp, tok_stride, kbeg + kTile * wave, kbeg, kstat, kclamp, lrow, a);
 
   const int64_t pos0 = a.pos0_dev[0];
+  // The KV head's merge counter, read ahead of the staging barrier (as in the lane kernel: before
+  // any partial of the block is stored, and off the path to the partial stores).
+  const unsigned next = a.merge ? merge_next(a.epochs[kvh * 32]) : 0u;
   SOLORT_STAMP(tid == 0, kvh + nkv * split, 1);
 
   // 3. q rows (and, fused, the new tokens' K/V rows) into LDS; rows R..31 of
@@ -830,6 +837,7 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
     stage_row(4, kv.k4, kv.v4); stage_row(5, kv.k5, kv.v5); stage_row(6, kv.k6, kv.v6); stage_row(7, kv.k7, kv.v7);
     // next tile (past the end: a re-read of cached rows)
     kv = fetch_tile<PAGED, NQ == 1>(kp, vp, tok_stride, k0 + 4 * kTile, kbeg, kstat, kclamp, lrow, a);
+    SOLORT_STAMP(lane == 0 && k0 + 4 * kTile < kend && k0 + 8 * kTile >= kend, kvh + nkv * split, 12 + wave);
     f32x16 s = f32x16{};
 #pragma unroll
     for (int kk = 0; kk < 8; ++kk) {
@@ -894,6 +902,7 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
   }
 
   SOLORT_STAMP(tid == 0, kvh + nkv * split, 3);
+  SOLORT_STAMP(lane == 0, kvh + nkv * split, 8 + wave);
   // 5. Merge the wavefronts that saw keys (log-sum-exp) and write this
   //    split's partial (max in log2 units, sum, unnormalised output) or, with
   //    one split, the answer.  O^T: lane l, register i of o[dt] holds dim
@@ -946,7 +955,6 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
   const bool writer = (nact > 1 || wave == 0) && l32 < R;
   const int NS = a.n_split;
   const bool inl = a.merge;
-  const unsigned next = inl ? merge_next(a.epochs[kvh * 32]) : 0u;
   const unsigned tag = merge_tag(next, kvh);
   const int r = l32;
   // Writes dims 32dt .. 32dt + 31 of row r (this lane's 16 of them) from od.

@@ -4,7 +4,9 @@ from solort_amd.runner import DECODE_BUCKETS, PREFILL_BUCKETS, decode_splits
 
 def test_decode_splits_heuristic():
     assert decode_splits(1024, 8) == 32
-    assert decode_splits(128, 8) == 4
+    assert decode_splits(128, 8) == 8
+    assert decode_splits(256, 8) == 16
+    assert decode_splits(512, 8) == 16
     assert decode_splits(32768, 8) == 32
     assert decode_splits(16, 8) == 1
 

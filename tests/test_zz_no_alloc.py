@@ -85,13 +85,25 @@ def test_noalloc_equals_decode_layer_twice(gpu, pair):
             assert torch.equal(k1, k2) and torch.equal(v1, v2), name
 
 
+def _scratch_bytes() -> int:
+    """SOLORT_NOALLOC_SCRATCH_BYTES as include/solort_hip.h defines it."""
+    import re
+    from pathlib import Path
+    text = (Path(__file__).resolve().parents[1] / "include" / "solort_hip.h").read_text()
+    m = re.search(r"#define SOLORT_NOALLOC_SCRATCH_BYTES\s+\(?\s*(\d+)u?\s*(?:<<\s*(\d+))?", text)
+    assert m, "SOLORT_NOALLOC_SCRATCH_BYTES not found in include/solort_hip.h"
+    return int(m.group(1)) << int(m.group(2) or 0)
+
+
 def test_noalloc_refuses_requests_above_the_scratch(gpu):
     lib = _lib.load()
-    p = ctypes.c_void_p(16 * 1024)  # never dereferenced: the size check fails first
-    nh, nkv, nq, ns = 64, 8, 4, 1024  # 8 heads x 1024 splits x 32 rows x 1040 B, far above 8 MiB
+    p = ctypes.c_void_p(16 * 1024)  # never dereferenced
+    nh, nkv, nq, ns = 64, 8, 4, 1024  # 8 heads x 1024 splits x 32 rows x 1040 B
     need = lib.solort_attn_workspace_bytes(nq, nh, nkv, HD, ns)
-    assert need > (8 << 20)
-    rc = lib.solort_decode_layer_noalloc(p, (nh + 2 * nkv) * HD, nq, nh, nkv, HD, p, p, 1e-6, p, p, p, p, 1024, 128,
-                                         65536, 65536, 0.088, ns, p, 0, None)
+    assert need > _scratch_bytes()
+    # The caches, the position and the output are NULL: were the size check ever to pass, the
+    # argument checks would still refuse the call before any launch.
+    rc = lib.solort_decode_layer_noalloc(p, (nh + 2 * nkv) * HD, nq, nh, nkv, HD, p, p, 1e-6, p, None, None, None,
+                                         1024, 128, 65536, 65536, 0.088, ns, None, 0, None)
     assert rc == EINVAL
     assert "scratch" in lib.solort_last_error().decode()
