@@ -835,8 +835,10 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
     };
     stage_row(0, kv.k0, kv.v0); stage_row(1, kv.k1, kv.v1); stage_row(2, kv.k2, kv.v2); stage_row(3, kv.k3, kv.v3);
     stage_row(4, kv.k4, kv.v4); stage_row(5, kv.k5, kv.v5); stage_row(6, kv.k6, kv.v6); stage_row(7, kv.k7, kv.v7);
-    // next tile (past the end: a re-read of cached rows)
-    kv = fetch_tile<PAGED, NQ == 1>(kp, vp, tok_stride, k0 + 4 * kTile, kbeg, kstat, kclamp, lrow, a);
+    // The next tile, only if the loop takes it (wave-uniform): a load left in flight past the
+    // last tile would hold the wave merge below, whose registers it writes.
+    if (k0 + 4 * kTile < kend)
+      kv = fetch_tile<PAGED, NQ == 1>(kp, vp, tok_stride, k0 + 4 * kTile, kbeg, kstat, kclamp, lrow, a);
     SOLORT_STAMP(lane == 0 && k0 + 4 * kTile < kend && k0 + 8 * kTile >= kend, kvh + nkv * split, 12 + wave);
     f32x16 s = f32x16{};
 #pragma unroll
