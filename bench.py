@@ -308,6 +308,9 @@ def floor_extras(torch, ops, runners, dev, sh) -> dict:
                          the non-temporal hint
       read_4mib_then_32wg_us  the same read followed by a dependent 32-workgroup launch reading
                          512 KiB (the two-launch combine's shape)
+      read_4mib_by_workgroups  the 4 MiB read by 8..256 workgroups: the streaming rate per
+                         workgroup (one workgroup per KV head would be 8)
+      empty_after_predecessor_us  an empty kernel's cost after a ~3 us and after a ~12 us read
     Sources rotate over 144 distinct 4 MiB slices of the rotated KV caches (576 MiB, beyond the 256
     MB Infinity Cache), as the decode calls do."""
     from solort_amd import _lib
@@ -343,6 +346,29 @@ def floor_extras(torch, ops, runners, dev, sh) -> dict:
         torch, dev, [lambda x=x: (read(x.data_ptr(), 4 << 20, 256, 1), read(small.data_ptr(), 512 << 10, 32, 4))
                      for x in slices], reps=4), 3)
     res["slices"] = len(slices)
+    # Streaming rate of few workgroups: 4 MiB read by n_wg workgroups (4 non-temporal loads in
+    # flight per thread), GB/s in all and per workgroup; one workgroup per KV head would be 8.
+    per_wg = {}
+    for n_wg in (8, 32, 64, 128, 256):
+        us = _graph_us(torch, dev, [lambda x=x, n=n_wg: read(x.data_ptr(), 4 << 20, n, 4 | 16) for x in slices[:72]],
+                       reps=2)
+        per_wg[str(n_wg)] = {"us": round(us, 3), "gbps": round((4 << 20) / (us * 1e-6) / 1e9, 1),
+                             "gbps_per_wg": round((4 << 20) / (us * 1e-6) / 1e9 / n_wg, 2)}
+    res["read_4mib_by_workgroups"] = per_wg
+    # The cost of a one-workgroup empty kernel after a short (4 MiB read, ~3 us) and after a long
+    # (64 MiB read, ~12 us) predecessor: each pair's time minus the predecessor's time alone.
+    big = [r.kc.view(-1)[:32 << 20] for r in runners]
+    t_short = _graph_us(torch, dev, [lambda x=x: read(x.data_ptr(), 4 << 20, 512, 4 | 16) for x in slices[:64]],
+                        reps=4)
+    t_short_e = _graph_us(torch, dev, [lambda x=x: (read(x.data_ptr(), 4 << 20, 512, 4 | 16), empty())
+                                       for x in slices[:64]], reps=4)
+    t_long = _graph_us(torch, dev, [lambda x=x: read(x.data_ptr(), 64 << 20, 512, 4 | 16) for x in big * 4], reps=4)
+    t_long_e = _graph_us(torch, dev, [lambda x=x: (read(x.data_ptr(), 64 << 20, 512, 4 | 16), empty())
+                                      for x in big * 4], reps=4)
+    res["empty_after_predecessor_us"] = {
+        "short_read_us": round(t_short, 3), "after_short": round(t_short_e - t_short, 3),
+        "long_read_us": round(t_long, 3), "after_long": round(t_long_e - t_long, 3),
+        "penalty": round((t_long_e - t_long) - (t_short_e - t_short), 3)}
     return res
 
 

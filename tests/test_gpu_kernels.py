@@ -155,8 +155,11 @@ def test_decode_qwen3_8b_32k(gpu):
         torch.cuda.synchronize()
         e32 = np.abs(out32.cpu().numpy().astype(np.float64) - want64)
         e16 = np.abs(out.float().cpu().numpy() - want64)
+        # Distance from the reference's own bf16 ops, on record: with the x8 keys those ops are
+        # themselves up to ~7.5e-2 from exact attention, so this is not the bar asserted below.
+        dref = np.abs(out.float().cpu().numpy() - ctx_ref.float().numpy())
         _say(f"  n_split={ns}: fp32 vs fp64 max {e32.max():.3e}; bf16 vs fp64 max {e16.max():.3e} "
-             f"mean {e16.mean():.3e}")
+             f"mean {e16.mean():.3e}; bf16 vs the reference's bf16 ops max {dref.max():.3e} mean {dref.mean():.3e}")
         assert e32.max() <= F32_MAX
         # the kernel's bf16 output is at least as close to exact attention as the reference's bf16 ops
         assert e16.max() <= max(BF16_MAX, ref_err.max()) and e16.mean() <= max(BF16_MEAN, ref_err.mean())
