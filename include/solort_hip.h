@@ -418,8 +418,11 @@ int solort_argmax_rows(const void* logits, int dtype, int rows, int64_t vocab, i
 /*
  * Reduction mode of solort_argmax_rows on the current device (no
  * counterpart in the reference): 1 = one launch where the placement check
- * passed, 0 = always the second launch, -1 = query only.  Returns the mode
- * in effect.  Both give the same indices.
+ * passed (the default), 0 = always the second launch, 2 = one launch whose
+ * reducing block gives up at once (a test of the failure path: every index
+ * stays in the row, built from the keys it saw, and each row counts a
+ * failure), -1 = query only.  Returns the mode in effect (0 when the
+ * placement is unverified).  Modes 0 and 1 give the same indices.
  */
 int solort_argmax_mode(int mode);
 

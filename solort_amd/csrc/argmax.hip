@@ -52,11 +52,12 @@ __device__ __forceinline__ int64_t key_to_index(uint64_t k) {
 
 // ONE: the one-launch reduction (the row's last block polls); otherwise every
 // block stores its slot and argmax_finish_kernel reduces them.
+// spin: the reader's polling limit (kArgmaxSpin; 0 in the test mode of solort_argmax_mode(2)).
 template <int F32, bool ONE>
 __global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict__ logits, int64_t vocab,
                                                           int64_t row_stride, int64_t per_block, int rows,
                                                           int vec_ok, uint4* __restrict__ slots,
-                                                          int64_t* __restrict__ out) {
+                                                          int64_t* __restrict__ out, int spin) {
   constexpr int VEC = F32 ? 4 : 8;  // elements per 16-byte load
   __shared__ uint64_t s_best[4];
   const int tid = threadIdx.x;
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(256) void argmax_rows_kernel(const void* __restrict
   const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(rs, (short)0, kMaxChunks * 16, 0x00020000);
   uint64_t k = tid == chunk ? best : 0;
   bool pend = tid < nchunk && tid != chunk;
-  for (int it = 0; __builtin_amdgcn_ballot_w64(pend) != 0 && it < kArgmaxSpin; ++it) {
+  for (int it = 0; __builtin_amdgcn_ballot_w64(pend) != 0 && it < spin; ++it) {
     asm volatile("" ::: "memory");
     const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, tid * 16, 0, 16));
     if (pend && v.y == ep && v.w == ep) {
@@ -157,15 +158,19 @@ __global__ __launch_bounds__(64) void argmax_finish_kernel(int nchunk, uint4* __
 
 namespace {
 constexpr int kMaxDev = 64;
-int g_argmax_two[kMaxDev];  // per device: 1 forces the two-launch reduction (solort_argmax_mode(0))
+// Per device, the mode solort_argmax_mode set, stored as mode + 1 so that the zero-filled start
+// means mode 1: 1 the one-launch reduction where the placement check passed, 0 always two
+// launches, 2 the one-launch reduction whose reducing block gives up at once (test mode).
+int g_argmax_mode[kMaxDev];
 }  // namespace
 
-// The one-launch reduction needs the round-robin placement (checked by
-// solort_init) and must not be switched off.
-static bool argmax_one_launch() {
+// The mode in effect on the current device: the one-launch forms need the
+// round-robin placement checked by solort_init.
+static int argmax_mode_now() {
   int dev = -1;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return false;
-  return !g_argmax_two[dev] && xcd_round_robin(dev);
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev) return 0;
+  const int m = g_argmax_mode[dev] == 0 ? 1 : g_argmax_mode[dev] - 1;  // stored as mode + 1
+  return m != 0 && xcd_round_robin(dev) ? m : 0;
 }
 
 }  // namespace solort
@@ -176,9 +181,9 @@ extern "C" int solort_argmax_mode(int mode) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDev)
     return set_error(SOLORT_EINVAL, "argmax_mode: no current device");
-  if (mode != -1 && mode != 0 && mode != 1) return set_error(SOLORT_EINVAL, "argmax_mode: mode %d", mode);
-  if (mode >= 0) g_argmax_two[dev] = mode == 0;
-  return argmax_one_launch() ? 1 : 0;
+  if (mode < -1 || mode > 2) return set_error(SOLORT_EINVAL, "argmax_mode: mode %d", mode);
+  if (mode >= 0) g_argmax_mode[dev] = mode + 1;
+  return argmax_mode_now();
 }
 
 extern "C" size_t solort_argmax_workspace_bytes(int rows) {
@@ -211,24 +216,26 @@ extern "C" int solort_argmax_rows(const void* logits, int dtype, int rows, int64
   const int64_t nblk = (vocab + per_block - 1) / per_block;  // <= target
   uint4* slots = (uint4*)ws;
   hipStream_t s = (hipStream_t)stream;
-  if (argmax_one_launch()) {
+  const int mode = argmax_mode_now();
+  if (mode != 0) {
     const int rows8 = (rows + 7) & ~7;
     const dim3 grid((unsigned)rows8, (unsigned)nblk);
+    const int spin = mode == 2 ? 0 : kArgmaxSpin;
     if (dtype == SOLORT_DTYPE_F32)
       hipLaunchKernelGGL((argmax_rows_kernel<1, true>), grid, dim3(256), 0, s, logits, vocab, row_stride, per_block,
-                         rows, vec_ok, slots, out_idx);
+                         rows, vec_ok, slots, out_idx, spin);
     else
       hipLaunchKernelGGL((argmax_rows_kernel<0, true>), grid, dim3(256), 0, s, logits, vocab, row_stride, per_block,
-                         rows, vec_ok, slots, out_idx);
+                         rows, vec_ok, slots, out_idx, spin);
     return check_launch("argmax_rows");
   }
   const dim3 grid((unsigned)rows, (unsigned)nblk);
   if (dtype == SOLORT_DTYPE_F32)
     hipLaunchKernelGGL((argmax_rows_kernel<1, false>), grid, dim3(256), 0, s, logits, vocab, row_stride, per_block,
-                       rows, vec_ok, slots, out_idx);
+                       rows, vec_ok, slots, out_idx, 0);
   else
     hipLaunchKernelGGL((argmax_rows_kernel<0, false>), grid, dim3(256), 0, s, logits, vocab, row_stride, per_block,
-                       rows, vec_ok, slots, out_idx);
+                       rows, vec_ok, slots, out_idx, 0);
   const int rc = check_launch("argmax_rows");
   if (rc) return rc;
   hipLaunchKernelGGL(argmax_finish_kernel, dim3((unsigned)rows), dim3(64), 0, s, (int)nblk, slots, out_idx);

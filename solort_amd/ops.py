@@ -442,7 +442,8 @@ def argmax_rows(logits: torch.Tensor, out: torch.Tensor, ws: torch.Tensor) -> No
 
 def argmax_mode(mode: int = -1) -> int:
     """Reduction mode of argmax_rows on the current device: 1 = one launch (where the placement
-    check passed), 0 = always a second launch, -1 = query; returns the mode in effect."""
+    check passed), 0 = always a second launch, 2 = one launch whose reducing block gives up at once
+    (test mode of the failure path), -1 = query; returns the mode in effect."""
     rc = _lib.load().solort_argmax_mode(int(mode))
     if rc < 0:
         _lib.check(rc, f"argmax_mode({mode})")

@@ -177,3 +177,23 @@ def test_greedy_advance_after_gemv_argmax(gpu):
         first = t if first is None else first
         assert tokens.tolist() == [-1, -1, -1, first]  # the second call's step 4 is past the list
         x = (x.float() * -1.5).to(torch.bfloat16)  # another argmax for the second call
+
+
+def test_greedy_advance_never_embeds_a_row_outside_the_table(gpu):
+    """Keys that name no vocabulary row (a workspace no solort_gemv_argmax call filled: all zero
+    here, which decodes to index 2^32 - 1) are recorded as token -1, the error the host checks, while
+    row 0 is embedded and step and pos still advance: no row outside the table is read."""
+    n, hidden = 4099, 64
+    embed = torch.randn(n, hidden, device=gpu).to(torch.bfloat16)
+    gws = ops.gemv_argmax_workspace(n, gpu).zero_()
+    xo = torch.zeros(hidden, dtype=torch.bfloat16, device=gpu)
+    tok = torch.full((1,), 5, dtype=torch.long, device=gpu)
+    tokens = torch.full((2,), 7, dtype=torch.long, device=gpu)
+    step = torch.tensor([1], dtype=torch.long, device=gpu)
+    pos = torch.tensor([30], dtype=torch.long, device=gpu)
+    ops.greedy_advance(gws, n, embed, xo, tok, tokens, step, pos)
+    torch.cuda.synchronize()
+    assert tokens.tolist() == [7, -1] and tok.item() == 0 and torch.equal(xo, embed[0])
+    assert step.item() == 2 and pos.item() == 31
+    with pytest.raises(RuntimeError, match="outside the vocabulary"):
+        ops.check_tokens(tokens.tolist(), n, "greedy decode")

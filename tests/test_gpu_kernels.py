@@ -369,6 +369,35 @@ def test_argmax_workspace_across_shapes_and_graph_replays(gpu):
         assert np.array_equal(out.cpu().numpy(), exact.argmax_first(xs[2].numpy()))
 
 
+def test_argmax_failure_path_stays_in_the_row(gpu):
+    """The host-forced failure mode (solort_argmax_mode(2): a row's reducing block stops polling at
+    once) writes, for every row, the index of the best key that block saw: its own chunk's, the
+    row's last, so x[r, idx] is the maximum of x[r, idx:]; each call counts one failure per row.
+    Back in the default mode the same workspace gives the exact indices and counts nothing more."""
+    g = torch.Generator().manual_seed(17)
+    x = torch.randn(5, 151936, generator=g)
+    ws = ops.argmax_workspace(5, gpu)
+    out = torch.empty(5, dtype=torch.long, device=gpu)
+    xd = x.to(gpu)
+    try:
+        assert ops.argmax_mode(2) == 2
+        for call in (1, 2):
+            ops.argmax_rows(xd, out, ws)
+            torch.cuda.synchronize()
+            idx = out.cpu().numpy()
+            _say(f"[argmax failure mode, call {call}] indices {idx.tolist()}")
+            assert ((idx >= 0) & (idx < x.shape[1])).all()
+            assert ops.argmax_failures(ws, 5) == 5 * call
+            for r in range(5):
+                assert x[r, idx[r]] == x[r, idx[r]:].max()
+    finally:
+        ops.argmax_mode(1)
+    ops.argmax_rows(xd, out, ws)
+    torch.cuda.synchronize()
+    assert np.array_equal(out.cpu().numpy(), exact.argmax_first(x.numpy()))
+    assert ops.argmax_failures(ws, 5) == 10
+
+
 def test_argmax_strided_rows(gpu):
     g = torch.Generator().manual_seed(5)
     big = torch.randn(3, 1003, generator=g)

@@ -171,6 +171,30 @@ def test_generate_from_prompt_is_prefill_then_decode_replays(gpu):
     assert a == b == c and len(set(a)) > 1
 
 
+def test_argmax_failure_raises_at_the_sync(gpu):
+    """A failed argmax reduction never passes silently: with the separate-ops tail and the argmax in
+    its host-forced failure mode (solort_argmax_mode(2)) the greedy decode raises at its one
+    synchronisation, and every token it recorded lies in the vocabulary; the fused tail, which does
+    not use that reduction, decodes as before."""
+    from solort_amd import ops
+    p0, n = 60, 4
+    w, fused = _model(gpu, p0, TINY_UNTIED)
+    sep = GraphQwen3Decode(w, 256, fused_tail=False)
+    sep.kc.copy_(fused.kc)
+    sep.vc.copy_(fused.vc)
+    want = fused.generate(7, p0, n)
+    try:
+        assert ops.argmax_mode(2) == 2
+        with pytest.raises(RuntimeError, match="argmax reduction failed"):
+            sep.generate(7, p0, n)
+        assert all(0 <= t < TINY_UNTIED.vocab for t in sep.tokens[:n].tolist())
+        fused.kc.copy_(sep.kc)
+        fused.vc.copy_(sep.vc)
+        assert fused.generate(7, p0, n) == want
+    finally:
+        ops.argmax_mode(1)
+
+
 def test_verify_graph_matches_reference_ops(gpu):
     """The whole-model verify graph (cuda_graph_executor.py:245-268 with the argmax and acceptance of
     :475-481): its logits against the CPU evaluations in bf16 and fp32 (the decode steps' bar), its
