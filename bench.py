@@ -507,9 +507,14 @@ def stamp_extras(torch, ops, wl, runners, dev, sh, bound) -> dict:
     for _ in range(3):
         graph.replay()
     torch.cuda.synchronize()
-    nb = (T // 32) * sh.nkv
+    n_tiles = T // 16  # 16 positions x 4 query heads per block
+    nb = n_tiles * sh.nkv
     st = read("solort_phase_stamps_prefill", nb)
-    tiles = [[kvh + sh.nkv * s for kvh in range(sh.nkv)] for s in range(T // 32)]  # heaviest tile first
+    # block index of a tile by rank (0 = heaviest): the first round of blocks (one per CU) takes
+    # ranks in order, the second round from the lightest up
+    rnd = max(1, torch.cuda.get_device_properties(dev).multi_processor_count // sh.nkv)
+    ib = [rk if rk < rnd else rnd + (n_tiles - 1 - rk) for rk in range(n_tiles)]
+    tiles = [[kvh + sh.nkv * ib[rk] for kvh in range(sh.nkv)] for rk in range(n_tiles)]  # heaviest tile first
     res["prefill_qwen3_4b_t1024"] = _stamp_summary(np, st, STAMP_PHASES_PREFILL,
                                                    ("end, median per query tile (heaviest first)", tiles, 5))
     return res

@@ -27,6 +27,9 @@ int check_prologue(const char* name, const void* qkv, int64_t qkv_row_stride, in
 int verify_xcd_placement(int dev);
 // probe.hip: whether that check passed on device `dev`.
 bool xcd_round_robin(int dev);
+// probe.hip: compute units of the current device (queried once per device; 0
+// if the query fails).
+int cu_count();
 
 // noalloc.hip: looks up the device address of the allocation-free entry
 // point's scratch array on device `dev` (current), once.  0 or the error code.

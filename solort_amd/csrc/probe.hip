@@ -58,7 +58,20 @@ constexpr int kMaxDevices = 64;
 constexpr int kProbeBlocks = 2048;
 std::mutex g_mu;
 int g_xcd_state[kMaxDevices];  // 0 unknown, 1 verified round robin over 8, -1 not
+int g_cus[kMaxDevices];        // compute units, 0 until first asked
 }  // namespace
+
+int cu_count() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return 0;
+  std::lock_guard<std::mutex> lk(g_mu);
+  if (g_cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    g_cus[dev] = n;
+  }
+  return g_cus[dev];
+}
 
 // Runs the placement probe on the current device and records whether
 // workgroup b always runs on the XCD of workgroup b % 8.  Synchronous: call
