@@ -831,6 +831,25 @@ def long_decode_extras(torch, ops, wl, dev, n_caches: int = 8) -> dict:
                              "by_shape_gbps": ceil, "bytes_per_launch": nbytes,
                              "note": "streaming read of the same rotated K/V buffers (nt: non-temporal loads)"}
     res["frac_of_stream_ceiling"] = round(best[2] / ceil[top], 4)
+    # The decode's own K/V reads without arithmetic (solort_probe_read_heads: the same grid of 8 x 32
+    # workgroups, 32-row tiles per wavefront, one tile in flight as the decode keeps, or two;
+    # non-temporal loads) over the same caches, one launch per cache in one graph: what the call's
+    # streaming alone costs.
+    heads = torch.zeros(sh.nkv * 32, dtype=torch.int32, device=dev)
+    pat = {}
+    for d in (1, 2):
+        def rh(i, d=d):
+            _lib.check(lib.solort_probe_read_heads(kcs[i].data_ptr(), vcs[i].data_ptr(), L, sh.nkv, 32, d,
+                                                   heads.data_ptr(), torch.cuda.current_stream(dev).cuda_stream),
+                       "probe_read_heads")
+        pat[d] = _graph_us(torch, dev, [lambda i=i: rh(i) for i in range(n_caches)], reps=4)
+    pgbs = 2 * nbytes / (pat[1] * 1e-6) / 1e9
+    res["pattern_ceiling"] = {"us": round(pat[1], 3), "gbps": round(pgbs, 1), "frac_hbm": round(pgbs / HBM_PEAK_GBS, 4),
+                              "n_split": 32, "bytes_per_launch": 2 * nbytes,
+                              "us_two_tiles_in_flight": round(pat[2], 3),
+                              "note": "the decode kernel's K/V loads alone (same grid and tiles, one tile in flight "
+                                      "per wavefront; us_two_tiles_in_flight: two)"}
+    res["frac_of_pattern_ceiling"] = round(pat[1] / best[1], 4)
     del kcs, vcs
     torch.cuda.empty_cache()
     return res

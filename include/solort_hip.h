@@ -437,11 +437,20 @@ int solort_argmax_mode(int mode);
  *   per thread, plus 16 for loads with the non-temporal hint (the hint the
  *   decode K/V and weight streams use); workgroup b writes one word to
  *   sink[b] (sink: n_wg words).
+ * probe_read_heads: the split decode kernel's K/V reads without arithmetic,
+ *   over caches k, v of rows x nkv x 128 bf16 (token-major, heads interleaved):
+ *   workgroup h + nkv * s reads head h's rows of keys [s * c, (s + 1) * c),
+ *   c = rows / n_split (a multiple of 128), in the decode's 32-row tiles per
+ *   wavefront with the non-temporal hint, tiles_in_flight (1, as the decode
+ *   keeps, or 2) tiles in flight per wavefront; workgroup b writes one word
+ *   to sink[b] (sink: nkv * n_split words).
  */
 int solort_probe_placement(uint32_t* out, int n_wg, solort_stream_t stream);
 int solort_probe_empty(int n_wg, solort_stream_t stream);
 int solort_probe_read(const void* src, int64_t nbytes, int n_wg, int in_flight, uint32_t* sink,
                       solort_stream_t stream);
+int solort_probe_read_heads(const void* k, const void* v, int64_t rows, int nkv, int n_split, int tiles_in_flight,
+                            uint32_t* sink, solort_stream_t stream);
 
 #ifdef __cplusplus
 }

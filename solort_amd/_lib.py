@@ -28,6 +28,7 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
     "solort_probe_placement": (c_int, [c_void_p, c_int, c_void_p]),
     "solort_probe_empty": (c_int, [c_int, c_void_p]),
     "solort_probe_read": (c_int, [c_void_p, c_int64, c_int, c_int, c_void_p, c_void_p]),
+    "solort_probe_read_heads": (c_int, [c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_void_p, c_void_p]),
     "solort_qknorm_rope_kvwrite": (
         c_int,
         [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p,

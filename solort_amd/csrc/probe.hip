@@ -53,6 +53,70 @@ __global__ __launch_bounds__(256) void read_kernel(const uint4* __restrict__ src
   if (threadIdx.x == 0) sink[blockIdx.x] = s_x[0] ^ s_x[1] ^ s_x[2] ^ s_x[3];
 }
 
+// The long-context decode's K/V reads with no arithmetic: block (h, s) of an
+// (nkv, n_split) grid (linear index h + nkv * s, as the decode's) reads KV head
+// h's 256-byte rows of keys [s * chunk, (s + 1) * chunk) of k and of v, from
+// caches laid out [rows][nkv][128] bf16.  Wavefront w takes the 32-row tiles at
+// s * chunk + 32 w + 128 i, lane l the 16-byte column l % 16 of rows l / 16 + 4 q
+// (q < 8), with the non-temporal hint.  D = 1: a tile's loads issue once the
+// previous tile has arrived (one tile in flight per wavefront, as the decode
+// keeps); D = 2: the next tile's loads issue before the current tile is used
+// (two in flight).  Each workgroup stores one word of the xor of what it read.
+template <int D>
+__global__ __launch_bounds__(256) void read_heads_kernel(const uint16_t* __restrict__ k,
+                                                         const uint16_t* __restrict__ v, int nkv, int chunk,
+                                                         uint32_t* __restrict__ sink) {
+  __shared__ uint32_t s_x[4];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, j = lane & 15, lrow = lane >> 4;
+  const int h = blockIdx.x % nkv, s = blockIdx.x / nkv;
+  const int64_t tok = (int64_t)nkv * 128;
+  const uint16_t* kp = k + h * 128 + 8 * j;
+  const uint16_t* vp = v + h * 128 + 8 * j;
+  uint32_t x = 0;
+  uint4 kt[D][8], vt[D][8];
+  auto fetch = [&](int b, int k0) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q) {
+      const int64_t off = (int64_t)(k0 + lrow + 4 * q) * tok;
+      kt[b][q] = ld_stream(kp + off);
+      vt[b][q] = ld_stream(vp + off);
+    }
+  };
+  auto use = [&](int b) {
+#pragma unroll
+    for (int q = 0; q < 8; ++q)
+      x ^= kt[b][q].x ^ kt[b][q].y ^ kt[b][q].z ^ kt[b][q].w ^ vt[b][q].x ^ vt[b][q].y ^ vt[b][q].z ^ vt[b][q].w;
+  };
+  const int kend = (s + 1) * chunk;
+  int k0 = s * chunk + 32 * wave;  // the tile in buffer 0
+  fetch(0, k0);
+  if constexpr (D == 1) {
+    for (;;) {
+      use(0);
+      k0 += 128;
+      if (k0 >= kend) break;
+      fetch(0, k0);
+    }
+  } else {
+    // Buffers alternate; the tile at k0 sits in buffer 0 at the top of each round.
+    for (;;) {
+      const bool more = k0 + 128 < kend;
+      if (more) fetch(1, k0 + 128);
+      use(0);
+      if (!more) break;
+      const bool more2 = k0 + 256 < kend;
+      if (more2) fetch(0, k0 + 256);
+      use(1);
+      if (!more2) break;
+      k0 += 256;
+    }
+  }
+  for (int m = 32; m >= 1; m >>= 1) x ^= __shfl_xor(x, m, 64);
+  if (lane == 0) s_x[wave] = x;
+  __syncthreads();
+  if (tid == 0) sink[blockIdx.x] = s_x[0] ^ s_x[1] ^ s_x[2] ^ s_x[3];
+}
+
 namespace {
 constexpr int kMaxDevices = 64;
 constexpr int kProbeBlocks = 2048;
@@ -139,4 +203,23 @@ extern "C" int solort_probe_read(const void* src, int64_t nbytes, int n_wg, int 
   }
 #undef SOLORT_READ
   return check_launch("probe_read");
+}
+
+extern "C" int solort_probe_read_heads(const void* k, const void* v, int64_t rows, int nkv, int n_split,
+                                       int tiles_in_flight, uint32_t* sink, solort_stream_t stream) {
+  if (!k || !v || !sink || !aligned16(k) || !aligned16(v) || ((uintptr_t)sink & 3u))
+    return set_error(SOLORT_EINVAL, "probe_read_heads: k and v must be 16-byte and sink 4-byte aligned");
+  if (nkv < 1 || nkv > 1024 || n_split < 1 || n_split > 65536 || rows < 128 || rows > (1LL << 30) ||
+      rows % n_split != 0 || (rows / n_split) % 128 != 0 || (int64_t)nkv * n_split > (1 << 20))
+    return set_error(SOLORT_EINVAL, "probe_read_heads: rows %lld must split into n_split %d chunks of a multiple "
+                     "of 128 rows (nkv %d)", (long long)rows, n_split, nkv);
+  if (tiles_in_flight != 1 && tiles_in_flight != 2)
+    return set_error(SOLORT_EINVAL, "probe_read_heads: tiles_in_flight %d not 1 or 2", tiles_in_flight);
+  if (tiles_in_flight == 1)
+    hipLaunchKernelGGL(read_heads_kernel<1>, dim3((unsigned)(nkv * n_split)), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)k, (const uint16_t*)v, nkv, (int)(rows / n_split), sink);
+  else
+    hipLaunchKernelGGL(read_heads_kernel<2>, dim3((unsigned)(nkv * n_split)), dim3(256), 0, (hipStream_t)stream,
+                       (const uint16_t*)k, (const uint16_t*)v, nkv, (int)(rows / n_split), sink);
+  return check_launch("probe_read_heads");
 }

@@ -167,6 +167,18 @@ def test_paged_kv_copies_reject_bad_arguments(lib):
     assert rc == EINVAL and "aligned" in _err(lib)
 
 
+def test_read_heads_probe_rejects_bad_arguments(lib):
+    p = ctypes.c_void_p(4096)
+    rd = lambda k=p, rows=4096, nkv=8, ns=32, d=1: lib.solort_probe_read_heads(k, p, rows, nkv, ns, d, p,  # noqa: E731
+                                                                             None)
+    assert rd(k=None) == EINVAL and "aligned" in _err(lib)
+    assert rd(k=ctypes.c_void_p(4100)) == EINVAL
+    assert rd(rows=4000) == EINVAL and "multiple of 128" in _err(lib)
+    assert rd(ns=3) == EINVAL
+    assert rd(nkv=0) == EINVAL
+    assert rd(d=3) == EINVAL and "tiles_in_flight" in _err(lib)
+
+
 def test_torch_front_end_refuses_cpu_tensors():
     q = torch.zeros(1, 32, 128, dtype=torch.bfloat16)
     kc = torch.zeros(1024, 8, 128, dtype=torch.bfloat16)

@@ -64,6 +64,21 @@ def test_read_probe_reads_every_byte(lib, gpu):
         assert got == want, (n_wg, inflight)
 
 
+def test_read_heads_probe_reads_every_byte_once(lib, gpu):
+    g = torch.Generator().manual_seed(6)
+    for rows, nkv, n_split, d in ((1024, 8, 8, 1), (4096, 8, 32, 2), (512, 2, 1, 1), (384, 4, 3, 2), (1024, 8, 2, 2),
+                                  (768, 2, 2, 2)):
+        kv = torch.randint(-2**31, 2**31 - 1, (2, rows * nkv * 64), generator=g, dtype=torch.int64).to(torch.int32)
+        want = int(np.bitwise_xor.reduce(kv.numpy().view(np.uint32).ravel()))  # xor of every word of k and v
+        k, v = kv[0].to(gpu), kv[1].to(gpu)
+        sink = torch.zeros(nkv * n_split, dtype=torch.int32, device=gpu)
+        _lib.check(lib.solort_probe_read_heads(k.data_ptr(), v.data_ptr(), rows, nkv, n_split, d, sink.data_ptr(),
+                                               torch.cuda.current_stream().cuda_stream), "probe_read_heads")
+        torch.cuda.synchronize()
+        got = int(np.bitwise_xor.reduce(sink.cpu().numpy().view(np.uint32)))
+        assert got == want, (rows, nkv, n_split, d)
+
+
 # (name, nh, nkv, max_len, bound, pos, n_split, nq)
 CASES = [
     ("8B KV 32768", 32, 8, 32768, 32768, 32767, 32, 1),
