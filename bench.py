@@ -124,7 +124,8 @@ def main() -> int:
         print(json.dumps({"prefill": prefill_extras(torch, ops, runners, dev, sh)}), flush=True)
         return 0
     if args.only == "long":
-        print(json.dumps({"decode_8b_kv32768": long_decode_extras(torch, ops, wl, dev)}), flush=True)
+        print(json.dumps({"decode_8b_kv32768": long_decode_extras(torch, ops, wl, dev),
+                          "decode_mid_kv": mid_decode_extras(torch, ops, wl, dev)}), flush=True)
         return 0
     if args.only == "verify":
         print(json.dumps(verify_extras(torch, ops, wl, runners, dev, sh)), flush=True)
@@ -217,6 +218,7 @@ def main() -> int:
         result["extras"]["floor"] = floor_extras(torch, ops, runners, dev, sh)
         result["extras"].update(verify_extras(torch, ops, wl, runners, dev, sh))
         result["extras"]["decode_8b_kv32768"] = long_decode_extras(torch, ops, wl, dev)
+        result["extras"]["decode_mid_kv"] = mid_decode_extras(torch, ops, wl, dev)
         result["extras"]["decode_gemv"] = gemv_extras(torch, ops, dev)
         result["extras"]["paged_decode_kv1024"] = paged_extras(torch, ops, runners, dev, sh)
         result["extras"]["torch_reference_decode"] = torch_reference_extras(torch, runners, dev, sh, bound)
@@ -852,6 +854,44 @@ def long_decode_extras(torch, ops, wl, dev, n_caches: int = 8) -> dict:
     res["frac_of_pattern_ceiling"] = round(pat[1] / best[1], 4)
     del kcs, vcs
     torch.cuda.empty_cache()
+    return res
+
+
+def mid_decode_extras(torch, ops, wl, dev, n_caches: int = 8) -> dict:
+    """Qwen3-4B decode call at KV 2048 / 4096 / 8192 / 16384 (bucket = live length), one
+    solort_decode_layer call per distinct layer cache, n_caches caches rotated in one graph, for the
+    split count the runner routes (decode_splits) and its neighbours (chunks of 32 to 1024 keys)."""
+    from solort_amd.runner import decode_splits
+
+    sh = wl.QWEN3_4B
+    res = {"workload": "Qwen3-4B decode attention, batch 1, 32q/8kv heads, KV live = bucket, "
+                       f"{n_caches} rotated layer caches; us per call by n_split x chunk", "by_kv": {}}
+    for L in (2048, 4096, 8192, 16384):
+        gen = torch.Generator(device=dev).manual_seed(1004)
+        kcs = [torch.randn(L, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16) for _ in range(n_caches)]
+        vcs = [torch.randn(L, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16) for _ in range(n_caches)]
+        qkv = torch.randn(n_caches, 1, sh.qkv_width, generator=gen, device=dev).to(torch.bfloat16)
+        w = (1.0 + 0.1 * torch.randn(2, 128, generator=gen, device=dev)).to(torch.bfloat16)
+        posb = torch.tensor([L - 1], dtype=torch.long, device=dev)
+        cs = ops.rope_rows(ops.inv_freq(128, wl.THETA, dev), posb, 1)
+        out = torch.empty(1, sh.nh * 128, dtype=torch.bfloat16, device=dev)
+        routed = decode_splits(L, sh.nkv)
+        # neighbours of the routed count, and the count of the earlier rule (32-key chunks up to 4096
+        # keys, 1024-key chunks beyond)
+        r = {"routed_n_split": routed, "by_split": {}}
+        for ns in sorted({routed, routed // 2, routed * 2, min(256, L // 32) if L <= 4096 else L // 1024} - {0}):
+            ws = ops.attn_workspace(1, sh.nh, sh.nkv, ns, dev)
+            calls = [(lambda i=i, ws=ws, ns=ns: ops.decode_layer(qkv[i], w[0], w[1], wl.EPS, cs, posb, kcs[i], vcs[i],
+                                                                 L, sh.scale, ws, ns, out, sh.nh, sh.nkv))
+                     for i in range(n_caches)]
+            us = _graph_us(torch, dev, calls, reps=4)
+            r["by_split"][f"{ns}x{L // ns}"] = round(us, 3)
+        us = r["by_split"][f"{routed}x{L // routed}"]
+        gbs = decode_bytes(L) / (us * 1e-6) / 1e9
+        r.update({"us": us, "gbps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)})
+        res["by_kv"][str(L)] = r
+        del kcs, vcs
+        torch.cuda.empty_cache()
     return res
 
 

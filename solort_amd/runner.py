@@ -41,18 +41,22 @@ FUSED_PREFILL_MIN = 512
 
 
 def decode_splits(bound: int, nkv: int) -> int:
-    """Key splits per KV head for a decode bucket.  Buckets up to 256 keys: 16 keys per split;
-    up to 4096: 32 keys per split (short chunks, latency-bound: enough workgroups to cover the 256
-    CUs).  Longer buckets: 1024-key chunks, so each workgroup streams eight key tiles per
-    wavefront.  Measured on MI355X, Qwen3-4B decode call (graph of 288 calls, 32 q / 8 kv heads):
-    KV 128 4.33 us at 8 splits against 4.67 at 4 and 6.30 at 1; KV 256 4.54 at 16 against 4.67 at
-    8; KV 512 4.90 at 16 against 4.94 at 32 and 5.49 at 8; KV 1024 5.35 at 32 against 5.73 at
-    16 and 6.60 at 64."""
+    """Key splits per KV head for a decode bucket.  Up to 256 keys: 16 keys per split; 512 keys: 32
+    (short chunks, latency-bound).  From 1024 keys on: 256 // nkv splits, i.e. one workgroup per CU
+    of the 256-CU MI355X with 8 KV heads, the chunk growing with the bucket (32 keys at 1024, 64 at
+    2048, ..., 1024 at 32768), and at least bound // 1024 splits (the MFMA kernel's chunks stay at
+    most 1024 keys).  Measured on MI355X, Qwen3-4B decode call (32 q / 8 kv heads, graphs of 8 or
+    288 calls): KV 128 4.33 us at 8 splits against 4.67 at 4 and 6.30 at 1; KV 256 4.54 at 16
+    against 4.67 at 8; KV 512 4.90 at 16 against 4.94 at 32 and 5.49 at 8; KV 1024 5.35 at 32
+    against 5.73 at 16 and 6.60 at 64; KV 2048 7.19 at 32 against 8.05 at 64 and 8.74 at 16; KV
+    4096 9.72 at 32 against 9.78 at 64 and 11.1 at 128; KV 8192 12.98 at 32 against 13.39 at 64
+    and 21.87 at 8; KV 16384 19.1 at 32 against 20.3 at 64 and 23.7 at 16; KV 32768 28.7 at 32
+    against 29.7 at 64."""
     if bound <= 256:
         return max(1, bound // 16)
-    if bound <= 4096:
-        return max(1, min(256, bound // 32))
-    return max(1, min(1024, bound // 1024))
+    if bound <= 512:
+        return max(1, bound // 32)
+    return max(1, min(256 // max(1, nkv), bound // 16), bound // 1024)
 
 
 def verify_splits(bound: int) -> int:

@@ -9,6 +9,10 @@ def test_decode_splits_heuristic():
     assert decode_splits(512, 8) == 16
     assert decode_splits(32768, 8) == 32
     assert decode_splits(16, 8) == 1
+    for bound in (2048, 4096, 8192, 16384):  # one workgroup per CU: 32 splits x 8 KV heads
+        assert decode_splits(bound, 8) == 32
+    assert decode_splits(65536, 8) == 64  # chunks of at most 1024 keys
+    assert decode_splits(1024, 32) == 8 and decode_splits(1024, 1) == 64
 
 
 def test_bucket_tables_follow_reference():
