@@ -892,6 +892,33 @@ def mid_decode_extras(torch, ops, wl, dev, n_caches: int = 8) -> dict:
         res["by_kv"][str(L)] = r
         del kcs, vcs
         torch.cuda.empty_cache()
+    # speculative verify (5 tokens at the bucket's end) over the same lengths from 8192 on: the routed
+    # split count against the earlier rule (64 splits of 128-key multiples)
+    from solort_amd.runner import verify_splits
+    K1 = 5
+    res["verify_by_kv"] = {}
+    for L in (8192, 16384, 32768):
+        gen = torch.Generator(device=dev).manual_seed(1005)
+        nc = 4
+        kcs = [torch.randn(L, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16) for _ in range(nc)]
+        vcs = [torch.randn(L, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16) for _ in range(nc)]
+        qkv = torch.randn(nc, K1, sh.qkv_width, generator=gen, device=dev).to(torch.bfloat16)
+        w = (1.0 + 0.1 * torch.randn(2, 128, generator=gen, device=dev)).to(torch.bfloat16)
+        posb = torch.tensor([L - K1], dtype=torch.long, device=dev)
+        cs = ops.rope_rows(ops.inv_freq(128, wl.THETA, dev), posb, K1)
+        out = torch.empty(K1, sh.nh * 128, dtype=torch.bfloat16, device=dev)
+        routed = verify_splits(L, sh.nkv)
+        r = {"routed_n_split": routed, "by_split": {}}
+        for ns in sorted({routed, 64}):
+            ws = ops.attn_workspace(K1, sh.nh, sh.nkv, ns, dev)
+            calls = [(lambda i=i, ws=ws, ns=ns: ops.decode_layer(qkv[i], w[0], w[1], wl.EPS, cs, posb, kcs[i], vcs[i],
+                                                                 L, sh.scale, ws, ns, out, sh.nh, sh.nkv))
+                     for i in range(nc)]
+            r["by_split"][f"{ns}x{L // ns}"] = round(_graph_us(torch, dev, calls, reps=4), 3)
+        r["us"] = r["by_split"][f"{routed}x{L // routed}"]
+        res["verify_by_kv"][str(L)] = r
+        del kcs, vcs
+        torch.cuda.empty_cache()
     return res
 
 
@@ -912,7 +939,7 @@ def verify_extras(torch, ops, wl, runners, dev, sh) -> dict:
     posb = torch.tensor([pos0], dtype=torch.long, device=dev)
     r0 = runners[0]
     cs = ops.rope_rows(r0.inv_freq, posb, K1)
-    ns = verify_splits(bound)
+    ns = verify_splits(bound, sh.nkv)
     out = torch.empty(K1, sh.nh * 128, dtype=torch.bfloat16, device=dev)
     vbytes = 2 * sh.nkv * (pos0 + K1) * 128 * 2 + K1 * 2 * sh.nh * 128 * 2
 

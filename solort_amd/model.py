@@ -139,7 +139,7 @@ class GraphQwen3Decode:
         self.ctx_ver = torch.zeros(self.k1, s.nh * HD, **bf)
         self.tok_ver = torch.zeros(self.k1, dtype=torch.long, device=self.dev)
         self.acc_ver = torch.zeros(2, dtype=torch.long, device=self.dev)
-        self.ws_ver = ops.attn_workspace(self.k1, s.nh, s.nkv, max(verify_splits(b) for b in self.buckets), self.dev)
+        self.ws_ver = ops.attn_workspace(self.k1, s.nh, s.nkv, max(verify_splits(b, s.nkv) for b in self.buckets), self.dev)
         self.ws_argv = ops.argmax_workspace(self.k1, self.dev)
         self._ver_graphs: dict[int, torch.cuda.CUDAGraph] = {}
         self._ver_logits: dict[int, torch.Tensor] = {}
@@ -278,7 +278,7 @@ class GraphQwen3Decode:
         for li in range(s.layers):
             qkv = F.linear(_rmsnorm_rows(x, w.in_ln[li], self.eps), w.wqkv[li])  # :252-253
             ops.decode_layer(qkv, w.qn[li], w.kn[li], self.eps, self.cs_ver, self.vpos0, self.kc[li], self.vc[li],
-                             bound, self.scale, self.ws_ver, verify_splits(bound), self.ctx_ver, s.nh, s.nkv)
+                             bound, self.scale, self.ws_ver, verify_splits(bound, s.nkv), self.ctx_ver, s.nh, s.nkv)
             x = x + F.linear(self.ctx_ver, w.wo[li])                            # :264
             gate, up = F.linear(_rmsnorm_rows(x, w.post_ln[li], self.eps), w.wgu[li]).split(s.inter, dim=-1)
             x = x + F.linear(F.silu(gate) * up, w.wd[li])                       # :265-267

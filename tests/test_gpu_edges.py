@@ -76,7 +76,7 @@ def test_decode_positions(gpu, pos0):
 @pytest.mark.parametrize("pos0,bound,max_len", [(0, 128, 128), (3, 128, 128), (123, 128, 128), (4091, 4096, 4096)],
                          ids=["start", "start+3", "bucket-end", "cache-end"])
 def test_verify_positions(gpu, pos0, bound, max_len):
-    _check(gpu, pos0, 5, bound, max_len, verify_splits(bound), 800 + pos0)
+    _check(gpu, pos0, 5, bound, max_len, verify_splits(bound, 8), 800 + pos0)
 
 
 def test_decode_single_split_long_chunk(gpu):

@@ -94,7 +94,7 @@ def test_verify_graph_replays_match_eager(gpu):
     q = torch.empty(5, sh.nh, HD, dtype=torch.bfloat16, device=gpu)
     for rep, pos0 in enumerate((2048, 17, 4091, 2048, 100)):
         bound = r._bucket_for(pos0 + 4)
-        ns = verify_splits(bound)
+        ns = verify_splits(bound, sh.nkv)
         ws = ops.attn_workspace(5, sh.nh, sh.nkv, ns, gpu)
         _say(f"[verify replay pos0={pos0} bound={bound}]")
         qkv = torch.randn(r.L, 5, r.width, generator=g).to(torch.bfloat16)

@@ -1,5 +1,5 @@
 """Host-side logic of the runner that needs no GPU."""
-from solort_amd.runner import DECODE_BUCKETS, PREFILL_BUCKETS, decode_splits
+from solort_amd.runner import DECODE_BUCKETS, PREFILL_BUCKETS, decode_splits, verify_splits
 
 
 def test_decode_splits_heuristic():
@@ -13,6 +13,13 @@ def test_decode_splits_heuristic():
         assert decode_splits(bound, 8) == 32
     assert decode_splits(65536, 8) == 64  # chunks of at most 1024 keys
     assert decode_splits(1024, 32) == 8 and decode_splits(1024, 1) == 64
+
+
+def test_verify_splits_heuristic():
+    assert verify_splits(4096, 8) == 32 and verify_splits(2048, 8) == 16 and verify_splits(128, 8) == 1
+    for bound in (8192, 16384, 32768):  # one workgroup per CU: 32 splits x 8 KV heads
+        assert verify_splits(bound, 8) == 32
+    assert verify_splits(65536, 8) == 64  # chunks of at most 1024 keys
 
 
 def test_bucket_tables_follow_reference():
