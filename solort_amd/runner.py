@@ -33,11 +33,12 @@ PREFILL_BUCKETS = (16, 32, 64, 128, 256, 512, 1024)
 
 
 # Prefill buckets from this length on use solort_prefill_layer (q normalised inside the attention
-# kernel); shorter ones the two-launch prologue + attention.  Measured on MI355X, Qwen3-4B shape:
-# the fused layer saves the q round trip through HBM (5.2 us of prologue per layer at 1024 rows,
-# 2.2 us at 512) and adds 1.2-1.7 us of normalisation work ahead of each attention workgroup's
-# first MFMA, so it loses at 128 rows (prologue 4.3 -> 4.0 us, attention 7.3 -> 9.0 us).
-FUSED_PREFILL_MIN = 512
+# kernel); shorter ones the two-launch prologue + attention.  The fused layer saves the q round
+# trip through HBM and adds the normalisation work ahead of each attention workgroup's first MFMA.
+# Measured on MI355X, Qwen3-4B shape, graphed 36-layer step per layer (two-launch against fused):
+# 128 rows 9.28 against 9.40 us, 256 rows 11.64 against 11.43, 512 rows 17.83 against 16.28, 1024
+# rows 30.1 against 26.6.
+FUSED_PREFILL_MIN = 256
 
 
 def decode_splits(bound: int, nkv: int) -> int:
