@@ -1034,6 +1034,33 @@ def prefill_extras(torch, ops, runners, dev, sh) -> dict:
                        "frac_mfma_peak": round(tf / BF16_PEAK_TFLOPS, 4),
                        "roofline_tflops": round(roof, 1), "frac_roofline": round(tf / roof, 4),
                        "step_us_per_layer": round(step_us, 3), "flop": fl, "bytes": nbytes}
+    # The two prefill forms per prompt length (runner.FUSED_PREFILL_MIN picks between them): the
+    # whole K/V + q prologue then attention on the materialised q, against the K/V prologue and
+    # attention normalising q itself; graphed 36-layer steps over the first runner's cache, per layer.
+    r = runners[0]
+    zp = torch.zeros(1, dtype=torch.long, device=dev)
+    forms = {}
+    for T in (128, 256, 512):
+        qkv = torch.randn(sh.layers, T, sh.qkv_width, generator=gen, device=dev).to(torch.bfloat16)
+        cs = torch.empty(2, T, 64, dtype=torch.bfloat16, device=dev)
+        q = torch.empty(T, sh.nh, 128, dtype=torch.bfloat16, device=dev)
+        ctx = torch.empty(sh.layers, T, sh.nh * 128, dtype=torch.bfloat16, device=dev)
+
+        def two_launch(T=T, qkv=qkv, cs=cs, q=q, ctx=ctx):
+            ops.rope_rows(r.inv_freq, zp, T, cs)
+            for li in range(sh.layers):
+                ops.qknorm_rope_kvwrite_cs(qkv[li], r.qn_w[li], r.kn_w[li], r.eps, cs, None, q, r.kc[li], r.vc[li],
+                                           sh.nh, sh.nkv)
+                ops.prefill_attn(q, r.kc[li], r.vc[li], sh.scale, ctx[li])
+
+        def fused(T=T, qkv=qkv, cs=cs, ctx=ctx):
+            ops.rope_rows(r.inv_freq, zp, T, cs)
+            for li in range(sh.layers):
+                ops.prefill_layer(qkv[li], r.qn_w[li], r.kn_w[li], r.eps, cs, r.kc[li], r.vc[li], sh.scale, ctx[li],
+                                  sh.nh, sh.nkv)
+        forms[str(T)] = {"two_launch_us_per_layer": round(_graph_us(torch, dev, [two_launch], reps=3) / sh.layers, 3),
+                         "fused_us_per_layer": round(_graph_us(torch, dev, [fused], reps=3) / sh.layers, 3)}
+    out["forms_by_T"] = forms
     return out
 
 
