@@ -691,9 +691,10 @@ def model_extras(torch, dev, live: int = 960, n: int = 48) -> dict:
     """Whole-model greedy decode of a random-weight Qwen3-4B (36 layers, tied 151,936 x 2560
     embedding, 8.05 GB of bf16 weights): one graph replay per token, tokens `live`..`live`+n-1 in the
     KV 1024 bucket over a seeded N(0,1) context, HIP events around n back-to-back replays, for the
-    fused step tail (argmax in the lm_head launch, one advance launch) and the separate-ops tail.
-    Bytes per token = every weight matrix once (the layer GEMVs and the lm_head) plus the K/V rows
-    read."""
+    model's step (each layer's qkv product inside the attention launch, the argmax in the lm_head
+    launch, one advance launch), the same step with the qkv product as its own launch
+    (`qkv_own_launch`) and the separate-ops tail.  Bytes per token = every weight matrix once (the
+    layer GEMVs and the lm_head) plus the K/V rows read."""
     from solort_amd.model import QWEN3_4B, GraphQwen3Decode, RandomQwen3
     s = QWEN3_4B
     w = RandomQwen3(s, dev, seed=1011)
@@ -704,8 +705,9 @@ def model_extras(torch, dev, live: int = 960, n: int = 48) -> dict:
     wbytes = 2 * (s.layers * s.hidden * (s.qkv_width + s.nh * 128 + 3 * s.inter) + s.vocab * s.hidden)
     kvbytes = s.layers * 2 * (live + n // 2) * s.nkv * 128 * 2
     out = {"model": s.name, "live_start": live, "tokens": n, "bytes_per_token": wbytes + kvbytes}
-    for fused in (True, False):
-        m = GraphQwen3Decode(w, 1024, fused_tail=fused)
+    # the model's path; the same with the qkv product as its own launch; the reference's separate tail ops
+    for fused, fused_qkv in ((True, True), (True, False), (False, False)):
+        m = GraphQwen3Decode(w, 1024, fused_tail=fused, fused_qkv=fused_qkv)
         m.kc[:, :live].copy_(ctx_k)
         m.vc[:, :live].copy_(ctx_v)
         m.generate(11, live, n)  # captures the bucket's graph and warms every kernel
@@ -726,7 +728,9 @@ def model_extras(torch, dev, live: int = 960, n: int = 48) -> dict:
              "gbps": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9, 1),
              "frac_hbm": round((wbytes + kvbytes) / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
              "first_tokens": m.tokens[:8].tolist()}
-        if fused:
+        if fused and not fused_qkv:
+            out["qkv_own_launch"] = r
+        elif fused:
             # the attention's cost inside the step: the same step captured without the attention
             # call of each layer (its tokens are not the model's), timed the same way
             m.attention_in_step = False

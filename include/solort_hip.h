@@ -215,6 +215,29 @@ int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int nq, int nh,
                         int n_split, void* out, int out_dtype, solort_stream_t stream);
 
 /*
+ * The decode step's qkv product and attention block for one new token:
+ * qkv = _rmsnorm(x, in_w, in_eps) @ wqkv^T (cuda_graph_executor.py:170-171),
+ * then solort_decode_layer on it (:173-184).  Results equal solort_gemv
+ * (SOLORT_GEMV_PLAIN, norm_w = in_w) followed by solort_decode_layer, bit for
+ * bit.  x [hidden] bf16 (the layer input); wqkv [(nh + 2 nkv) * hd][row
+ * stride] bf16.  Where the shapes allow (32 key splits per KV head of at most
+ * 64 keys, the in-launch merge, the packed cache layout, (group, hidden) in
+ * {(2, 1024), (4, 2560), (4, 4096)}, wqkv rows contiguous) it is one launch:
+ * the splits of each KV head compute that head's q, k and v rows, hand them
+ * over through the XCD's L2 as tagged pairs, and continue with the attention,
+ * whose first K/V loads were issued at launch; qkv_out is then not written.
+ * Otherwise it runs the two calls, the product into qkv_out [(nh + 2 nkv) *
+ * hd] bf16.  The workspace is sized by solort_decode_qkv_workspace_bytes(nh,
+ * nkv, n_split).  Other arguments as in solort_decode_layer with nq = 1.
+ */
+size_t solort_decode_qkv_workspace_bytes(int nh, int nkv, int n_split);
+int solort_decode_qkv_layer(const void* x, int hidden, const void* in_w, float in_eps, const void* wqkv,
+                            int64_t wqkv_row_stride, int nh, int nkv, int hd, const void* qn_w, const void* kn_w,
+                            float eps, const void* rope_cs, const int64_t* pos0_dev, void* k_cache, void* v_cache,
+                            int64_t kv_tok_stride, int64_t kv_head_stride, int64_t max_len, int bound, float scale,
+                            void* ws, int n_split, void* qkv_out, void* out, int out_dtype, solort_stream_t stream);
+
+/*
  * solort_decode_layer without a workspace argument.  No counterpart in the
  * reference: it is for callers that cannot allocate device memory (code
  * under graph capture that must not call hipMalloc, tight serving loops,

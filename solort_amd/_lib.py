@@ -63,6 +63,13 @@ SIGNATURES: dict[str, tuple[object, list[object]]] = {
         [c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_float,
          c_void_p, c_int, c_void_p],
     ),
+    "solort_decode_qkv_workspace_bytes": (c_size_t, [c_int, c_int, c_int]),
+    "solort_decode_qkv_layer": (
+        c_int,
+        [c_void_p, c_int, c_void_p, c_float, c_void_p, c_int64, c_int, c_int, c_int, c_void_p, c_void_p, c_float,
+         c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int64, c_int64, c_int, c_float, c_void_p, c_int, c_void_p,
+         c_void_p, c_int, c_void_p],
+    ),
     "solort_decode_layer_noalloc": (
         c_int,
         [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p, c_void_p, c_float, c_void_p, c_void_p,

@@ -229,6 +229,18 @@ __device__ __forceinline__ uint4 ld_l2(__amdgpu_buffer_rsrc_t r, int off) {
   return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 16));
 }
 
+// Small uniform values read with vector (buffer) loads: they complete in
+// order with the vector loads issued before them (vmcnt), so an LDS wait
+// (lgkmcnt), which a scalar load would share, never waits for them.
+__device__ __forceinline__ uint2 ld_vec8(const void* p) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, 8, 0x00020000);
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(r, 0, 0, 0));
+}
+__device__ __forceinline__ unsigned ld_vec4(const void* p) {
+  const __amdgpu_buffer_rsrc_t r = __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(p), (short)0, 4, 0x00020000);
+  return __builtin_amdgcn_raw_buffer_load_b32(r, 0, 0, 0);
+}
+
 // Greedy-argmax key of (value, index): high word = an order-preserving image
 // of the fp32 value (-0 and +0 equal, NaN above every number), low word =
 // 0xffffffff - index, so the integer maximum is torch.argmax's answer (the

@@ -55,6 +55,7 @@
 #include "common.h"
 #include "capi_internal.h"
 #include "qknorm_rope.h"
+#include "gemv_common.h"
 
 namespace solort {
 
@@ -90,6 +91,15 @@ struct DecodeTail {
   unsigned* epochs;
   int n_split;  // splits per KV head
   int merge;    // 1: the in-launch merge; 0: the combine kernel's second launch
+};
+
+// The qkv product computed inside the decode launch (decode_qkv_lanes_kernel):
+// x, in_w, wqkv and hidden travel among the preloaded arguments; these in the
+// tail.
+struct QkvIn {
+  const uint16_t* qn_w;
+  uint2* items;  // [nkv][(G + 2) * 64] tagged pairs (two bf16 outputs, tag)
+  float eps;     // the input RMSNorm's
 };
 
 // Element offset of the cache row at position t (head 0, dim 0).  Paged: a
@@ -325,11 +335,15 @@ __device__ __forceinline__ void split_merge(const DecodeTail& a, int kvh, int sp
 // few key rows per slot).  Grid (nkv, n_split): block (kvh, split).  qsrc:
 // fused, the qkv rows (row stride qsrc_stride); unfused, the q rows
 // [nq][nh][128] (qsrc_stride = nh*128).
-template <int NQ, int G, int U, bool FUSED, bool PAGED>
+template <int NQ, int G, int U, bool FUSED, bool PAGED, int RW = 0, int CPL = 0>
 __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, int tok_stride, int head_stride,
                                                   int chunk, int bound, const uint16_t* qsrc, int qsrc_stride,
                                                   int nh, const uint16_t* qn_w, const uint16_t* kn_w,
-                                                  const uint16_t* rope_cs, const DecodeTail& a) {
+                                                  const uint16_t* rope_cs, const DecodeTail& a,
+                                                  const uint16_t* x = nullptr, const uint16_t* wqkv = nullptr,
+                                                  const uint16_t* in_w = nullptr, int hidden = 0,
+                                                  const QkvIn* qi = nullptr) {
+  constexpr bool QKV = RW > 0;  // the qkv rows computed in this launch from x and wqkv
   constexpr int R = NQ * G;            // query rows sharing one KV head
   constexpr int KPI = 16 * U;          // keys per iteration (16 slots x U)
   constexpr int RPW = (R + 3) / 4;     // output rows per wavefront
@@ -353,8 +367,8 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
   //    load a valid row they ignore): a load skipped on some path would make
   //    the compiler wait for all of them before the first use.
   constexpr int NROWS = FUSED ? NQ * (G + 2) : R;
-  uint4 raw0, wq0 = make_uint4(0u, 0u, 0u, 0u), wk0 = wq0, c0 = wq0, s0 = wq0;
-  {
+  uint4 raw0 = make_uint4(0u, 0u, 0u, 0u), wq0 = raw0, wk0 = raw0, c0 = raw0, s0 = raw0;
+  if constexpr (!QKV) {
     const int row = min(slot, NROWS - 1);
     if constexpr (FUSED) {
       const int t = row / (G + 2), c = row % (G + 2);
@@ -387,13 +401,99 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
   }
   __builtin_amdgcn_sched_barrier(0);  // every K/V load issues before the position is read
 
-  const int64_t pos0 = a.pos0_dev[0];
-  // The KV head's merge counter, read by every wave ahead of the staging barrier below: each wave
-  // of the block has read it before any partial of the block is stored, hence before the head's
-  // row-0 merger (which waits for every split's partial) can advance it; and its round trip
-  // overlaps the prologue instead of preceding the partial stores.
-  const unsigned next = a.merge ? merge_next(a.epochs[kvh * 32]) : 0u;
+  // The qkv product in the launch: this wave's RW weight rows of the head's (G + 2) * 128 outputs
+  // (outputs i0 .. i0 + RW - 1 of q heads kvh*G .. kvh*G + G - 1, then the K and V rows), lane l
+  // taking 16-byte chunks l + 64u as the GEMV kernel does; then the prologue's own inputs.
+  constexpr int QRW = QKV ? RW : 1, QCPL = QKV ? CPL : 1;
+  uint4 wv[QRW][QCPL];
+  const int i0 = (split * 4 + wave) * RW;
+  if constexpr (QKV) {
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      const int i = i0 + r, c = i >> 7;
+      const int hs = c < G ? kvh * G + c : (c == G ? nh + kvh : nh + nkv + kvh);
+      const uint16_t* wrow = wqkv + (int64_t)(hs * SOLORT_HD + (i & 127)) * hidden;
+#pragma unroll
+      for (int u = 0; u < CPL; ++u) wv[r][u] = ld_stream(wrow + 8 * (lane + 64 * u));
+    }
+    const int row = min(slot, NROWS - 1);
+    wq0 = *reinterpret_cast<const uint4*>(qn_w + j * 8);
+    wk0 = *reinterpret_cast<const uint4*>(kn_w + j * 8);
+    c0 = *reinterpret_cast<const uint4*>(rope_cs + (row / (G + 2)) * 64 + (j & 7) * 8);
+    s0 = *reinterpret_cast<const uint4*>(rope_cs + (NQ + row / (G + 2)) * 64 + (j & 7) * 8);
+  }
+
+  int64_t pos0;
+  unsigned next;
+  uint2 posv = make_uint2(0u, 0u);
+  unsigned epv = 0u;
+  if constexpr (QKV) {
+    // Read by vector loads behind the weight loads: first used after the product, and a scalar
+    // load's wait would be shared by the LDS barriers ahead of that.  (The merge counter is read
+    // before any partial or qkv item of the block is stored, as below.)
+    posv = ld_vec8(a.pos0_dev);
+    epv = ld_vec4(a.epochs + kvh * 32);
+    pos0 = 0;
+    next = 0u;
+  } else {
+    pos0 = a.pos0_dev[0];
+    // The KV head's merge counter, read by every wave ahead of the staging barrier below: each wave
+    // of the block has read it before any partial of the block is stored, hence before the head's
+    // row-0 merger (which waits for every split's partial) can advance it; and its round trip
+    // overlaps the prologue instead of preceding the partial stores.
+    next = a.merge ? merge_next(a.epochs[kvh * 32]) : 0u;
+  }
   SOLORT_STAMP(tid == 0, kvh + nkv * split, 1);
+
+  if constexpr (QKV) {
+    // x normalised into LDS (s_v, free until the key loop), the wave's RW dot products in the GEMV
+    // kernel's order and rounding, stored as tagged pairs; then each slot polls its row of the
+    // head's qkv outputs, stored by the head's splits (all on this XCD) with this launch's tag.
+    __shared__ float s_red[4];
+    uint4* s_x = reinterpret_cast<uint4*>(s_v);
+    gemv_stage_x<true>(x, in_w, qi->eps, hidden, s_x, s_red);
+    float acc[RW];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) acc[r] = 0.f;
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) {
+      const uint4 xv = s_x[lane + 64 * u];
+#pragma unroll
+      for (int r = 0; r < RW; ++r) {
+        float d = dot2bf(wv[r][u].x, xv.x, acc[r]);
+        d = dot2bf(wv[r][u].y, xv.y, d);
+        d = dot2bf(wv[r][u].z, xv.z, d);
+        acc[r] = dot2bf(wv[r][u].w, xv.w, d);
+      }
+    }
+    next = merge_next((unsigned)__builtin_amdgcn_readfirstlane((int)epv));
+    const unsigned qtag = merge_tag(next, kvh);
+    uint2* items = qi->items + (int64_t)kvh * (G + 2) * 64;
+    uint32_t mine = 0;
+#pragma unroll
+    for (int r = 0; r < RW; r += 2) {
+      const uint32_t pr = f2bf(wave_sum64(acc[r])) | f2bf(wave_sum64(acc[r + 1])) << 16;
+      if (lane == r / 2) mine = pr;
+    }
+    if (lane < RW / 2) items[i0 / 2 + lane] = make_uint2(mine, qtag);
+    const int prow = min(slot, NROWS - 1);
+    const __amdgpu_buffer_rsrc_t rq =
+        __builtin_amdgcn_make_buffer_rsrc(items, (short)0, (G + 2) * 64 * 8, 0x00020000);
+    const int off = (prow * 64 + 4 * j) * 8;
+    uint4 a01 = make_uint4(0u, 0u, 0u, 0u), a23 = a01;
+    bool pend = true;
+    for (int it = 0; it < kMergeSpin && pend; ++it) {
+      asm volatile("" ::: "memory");  // a fresh load every round
+      a01 = ld_l2(rq, off);
+      a23 = ld_l2(rq, off + 16);
+      const bool bad = (a01.y != qtag) | (a01.w != qtag) | (a23.y != qtag) | (a23.w != qtag);
+      pend = __builtin_amdgcn_ballot_w64(bad) != 0;
+    }
+    raw0 = pend ? make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u)  // NaN: gave up
+                : make_uint4(a01.x, a01.z, a23.x, a23.z);
+    pos0 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)posv.y) << 32) |
+                     (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)posv.x));
+  }
 
   // 3. q rows (and, fused, the new tokens' K/V rows) into LDS.
   for (int row = slot; row < NROWS; row += 16) {
@@ -614,6 +714,21 @@ __global__ __launch_bounds__(256) void decode_lanes_packed_kernel(uint16_t* kc, 
   const int chunk = ((int)(geom & 3u) + 1) * 16, nh = (int)((geom >> 2) & 2047u), bound = (int)(geom >> 13);
   decode_lanes_body<1, G, U, true, false>(kc, vc, tok_stride, head_stride, chunk, bound, qkv, 0, nh, qn_w, kn_w,
                                           rope_cs, a);
+}
+
+// One new token, fused with the qkv product: x [hidden] (the layer input),
+// in_w (the input RMSNorm weight) and wqkv [(nh + 2 nkv) * 128][hidden] lead
+// the arguments, so the K/V and weight loads issue without waiting for the
+// argument fetch; 32 splits per KV head, each computing RW = G + 2 outputs per
+// wavefront (hidden = 512 CPL).  strides8 and geom as for the packed kernel.
+template <int G, int U, int RW, int CPL>
+__global__ __launch_bounds__(256) void decode_qkv_lanes_kernel(uint16_t* kc, uint16_t* vc, unsigned strides8,
+                                                         unsigned geom, const uint16_t* x, const uint16_t* wqkv,
+                                                         const uint16_t* in_w, const DecodeTail a, const QkvIn q) {
+  const int tok_stride = (int)(strides8 & 0xffffu) * 8, head_stride = (int)(strides8 >> 16) * 8;
+  const int chunk = ((int)(geom & 3u) + 1) * 16, nh = (int)((geom >> 2) & 2047u), bound = (int)(geom >> 13);
+  decode_lanes_body<1, G, U, true, false, RW, CPL>(kc, vc, tok_stride, head_stride, chunk, bound, nullptr, 0, nh,
+                                                   q.qn_w, a.kn_w, a.rope_cs, a, x, wqkv, in_w, CPL * 512, &q);
 }
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -1376,6 +1491,46 @@ static int attn_impl(const char* name, const void* q, int nq, int nh, int nkv, i
   return launch_all(name, false, nq, a, (hipStream_t)stream);
 }
 
+// The fused qkv + attention launch: one new token, packed layout, the
+// lane-parallel kernel at 32 splits per KV head with the in-launch merge, and
+// a (group, hidden) pair the kernel is built for.  Returns false when any
+// condition fails (the caller then runs the product as its own launch).
+constexpr int kQkvSplits = 32;
+
+static size_t qkv_items_bytes(int nh, int nkv) { return align256((size_t)nkv * (nh / nkv + 2) * 64 * 8); }
+
+template <int G, int RW, int CPL>
+static void launch_qkv_u(const DecodeArgs& a, unsigned strides8, unsigned geom, const void* x, const void* wqkv,
+                         const void* in_w, const QkvIn& q, hipStream_t s) {
+  const dim3 grid = a.grid();
+  if (a.U == 4)
+    hipLaunchKernelGGL((decode_qkv_lanes_kernel<G, 4, RW, CPL>), grid, dim3(256), 0, s, a.kc, a.vc, strides8, geom,
+                       (const uint16_t*)x, (const uint16_t*)wqkv, (const uint16_t*)in_w, a.tail, q);
+  else
+    hipLaunchKernelGGL((decode_qkv_lanes_kernel<G, 2, RW, CPL>), grid, dim3(256), 0, s, a.kc, a.vc, strides8, geom,
+                       (const uint16_t*)x, (const uint16_t*)wqkv, (const uint16_t*)in_w, a.tail, q);
+}
+
+static bool launch_qkv(const DecodeArgs& a, int hidden, const void* x, const void* wqkv, const void* in_w,
+                       const QkvIn& q, hipStream_t s) {
+  const int G = a.nh / a.nkv;
+  if (!a.lanes || (a.U != 2 && a.U != 4) || a.n_split != kQkvSplits || !a.tail.merge || a.tok_stride >= (1 << 19) ||
+      a.head_stride >= (1 << 19) || a.nh >= 2048 || a.bound >= (1 << 19))
+    return false;
+  const unsigned strides8 = (unsigned)(a.tok_stride / 8) | (unsigned)(a.head_stride / 8) << 16;
+  const unsigned geom = (unsigned)(a.chunk / 16 - 1) | (unsigned)a.nh << 2 | (unsigned)a.bound << 13;
+  if (G == 2 && hidden == 1024) {
+    launch_qkv_u<2, 4, 2>(a, strides8, geom, x, wqkv, in_w, q, s);
+  } else if (G == 4 && hidden == 2560) {
+    launch_qkv_u<4, 6, 5>(a, strides8, geom, x, wqkv, in_w, q, s);
+  } else if (G == 4 && hidden == 4096) {
+    launch_qkv_u<4, 6, 8>(a, strides8, geom, x, wqkv, in_w, q, s);
+  } else {
+    return false;
+  }
+  return true;
+}
+
 }  // namespace solort
 
 using namespace solort;
@@ -1434,6 +1589,50 @@ extern "C" int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int 
   a.tail.rope_cs = (const uint16_t*)rope_cs;
   a.tail.eps = eps;
   return launch_all(name, true, nq, a, (hipStream_t)stream);
+}
+
+extern "C" size_t solort_decode_qkv_workspace_bytes(int nh, int nkv, int n_split) {
+  if (nh <= 0 || nkv <= 0 || nh % nkv || n_split < 1) return 0;
+  return ws_layout(1, nh, nkv, n_split).total + qkv_items_bytes(nh, nkv);
+}
+
+extern "C" int solort_decode_qkv_layer(const void* x, int hidden, const void* in_w, float in_eps, const void* wqkv,
+                                       int64_t wqkv_row_stride, int nh, int nkv, int hd, const void* qn_w,
+                                       const void* kn_w, float eps, const void* rope_cs, const int64_t* pos0_dev,
+                                       void* k_cache, void* v_cache, int64_t kv_tok_stride, int64_t kv_head_stride,
+                                       int64_t max_len, int bound, float scale, void* ws, int n_split, void* qkv_out,
+                                       void* out, int out_dtype, solort_stream_t stream) {
+  const char* name = "decode_qkv_layer";
+  DecodeArgs a = {};
+  int rc = prepare(name, 1, nh, nkv, hd, k_cache, v_cache, kv_tok_stride, kv_head_stride, max_len, pos0_dev, bound,
+                   scale, ws, n_split, out, out_dtype, a);
+  if (rc) return rc;
+  if (!x || !in_w || !wqkv || !qn_w || !kn_w || !rope_cs || !qkv_out)
+    return set_error(SOLORT_EINVAL, "%s: null pointer", name);
+  if (!aligned16(x) || !aligned16(in_w) || !aligned16(wqkv) || !aligned16(qn_w) || !aligned16(kn_w) ||
+      !aligned16(rope_cs) || !aligned16(qkv_out))
+    return set_error(SOLORT_EINVAL, "%s: pointers must be 16-byte aligned", name);
+  if (hidden < 8 || hidden % 8 || hidden > 65536 || wqkv_row_stride < hidden || wqkv_row_stride % 8 ||
+      wqkv_row_stride > kMaxI32)
+    return set_error(SOLORT_EINVAL, "%s: hidden %d, wqkv_row_stride %lld", name, hidden, (long long)wqkv_row_stride);
+  a.qn_w = (const uint16_t*)qn_w;
+  a.tail.kn_w = (const uint16_t*)kn_w;
+  a.tail.rope_cs = (const uint16_t*)rope_cs;
+  a.tail.eps = eps;
+  QkvIn q;
+  q.qn_w = (const uint16_t*)qn_w;
+  q.items = (uint2*)((char*)ws + ws_layout(1, nh, nkv, n_split).total);
+  q.eps = in_eps;
+  if (wqkv_row_stride == hidden && launch_qkv(a, hidden, x, wqkv, in_w, q, (hipStream_t)stream))
+    return check_launch(name);
+  // Otherwise the product as its own launch, then the attention block on its output.
+  const int width = (nh + 2 * nkv) * hd;
+  rc = solort_gemv(wqkv, wqkv_row_stride, width, hidden, x, in_w, in_eps, nullptr, SOLORT_GEMV_PLAIN, 0, qkv_out,
+                   stream);
+  if (rc) return rc;
+  a.qsrc = (const uint16_t*)qkv_out;
+  a.qsrc_stride = width;
+  return launch_all(name, true, 1, a, (hipStream_t)stream);
 }
 
 extern "C" int solort_paged_decode_layer(const void* qkv, int64_t qkv_row_stride, int nq, int nh, int nkv, int hd,

@@ -30,19 +30,11 @@
 // launch after the grid reduces the slots and decodes the index.
 #include "common.h"
 #include "capi_internal.h"
+#include "gemv_common.h"
 
 namespace solort {
 
 enum { kGemvPlain = 0, kGemvResid = 1, kGemvSwiglu = 2, kGemvArgmax = 3 };
-
-__device__ __forceinline__ float wave_sum64(float v) {
-  v += xshfl(v, 1);
-  v += xshfl(v, 2);
-  v += xshfl(v, 4);
-  v += xshfl(v, 8);
-  v += xshfl(v, 16);
-  return xor32_combine(v, [](float x, float y) { return x + y; });
-}
 
 // silu(g) = g * sigmoid(g) = g / (1 + exp(-g)) in fp32 (torch's formula),
 // rounded to bf16 as F.silu on a bf16 tensor.
@@ -87,64 +79,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   SOLORT_GEMV_LOADS(lane)
 
   // x into LDS (normalised: sum of squares in fp32, one block reduction).
-  if constexpr (NORM) {
-    // The first kXReg chunks of this thread stay in registers between the two
-    // passes (k <= 8192 in one round); larger k re-reads the rest.
-    constexpr int kXReg = 4;
-    uint4 xr[kXReg], gr[kXReg];
-    float ss = 0.f;
-#pragma unroll
-    for (int q = 0; q < kXReg; ++q) {
-      const int i = tid + 256 * q;
-      if (i < nch) {
-        xr[q] = *reinterpret_cast<const uint4*>(x + 8 * i);
-        gr[q] = *reinterpret_cast<const uint4*>(norm_w + 8 * i);
-      }
-    }
-#pragma unroll
-    for (int q = 0; q < kXReg; ++q) {
-      if (tid + 256 * q < nch) {
-        float v[8];
-        unpack8(xr[q], v);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
-      }
-    }
-    for (int i = tid + 256 * kXReg; i < nch; i += 256) {
-      float v[8];
-      unpack8(*reinterpret_cast<const uint4*>(x + 8 * i), v);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
-    }
-    ss = wave_sum64(ss);
-    if (lane == 0) s_red[wave] = ss;
-    __syncthreads();
-    const float mean = (s_red[0] + s_red[1] + s_red[2] + s_red[3]) / (float)K;
-    const float r = 1.0f / __builtin_sqrtf(mean + eps);
-#pragma unroll
-    for (int q = 0; q < kXReg; ++q) {
-      const int i = tid + 256 * q;
-      if (i < nch) {
-        float v[8], g[8];
-        unpack8(xr[q], v);
-        unpack8(gr[q], g);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (v[e] * r) * g[e];
-        sx[i] = pack8(v);
-      }
-    }
-    for (int i = tid + 256 * kXReg; i < nch; i += 256) {
-      float v[8], g[8];
-      unpack8(*reinterpret_cast<const uint4*>(x + 8 * i), v);
-      unpack8(*reinterpret_cast<const uint4*>(norm_w + 8 * i), g);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = (v[e] * r) * g[e];
-      sx[i] = pack8(v);
-    }
-  } else {
-    for (int i = tid; i < nch; i += 256) sx[i] = *reinterpret_cast<const uint4*>(x + 8 * i);
-  }
-  __syncthreads();
+  gemv_stage_x<NORM>(x, norm_w, eps, K, sx, s_red);
 
   float acc[R];
 #pragma unroll

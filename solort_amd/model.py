@@ -85,14 +85,17 @@ class GraphQwen3Decode:
     """Greedy decode over a runner-owned bf16 KV cache, one captured graph per KV bucket."""
 
     def __init__(self, weights: RandomQwen3, max_len: int, eps: float = 1e-6, theta: float = 1e6,
-                 max_tokens: int = 4096, fused_tail: bool = True, spec_k: int = 4) -> None:
+                 max_tokens: int = 4096, fused_tail: bool = True, spec_k: int = 4, fused_qkv: bool = True) -> None:
         """fused_tail: the argmax folded into the lm_head launch and the token bookkeeping plus the
         next embedding row in one launch (solort_gemv_argmax + solort_greedy_advance); False runs
         the same step as the reference's separate ops (lm_head, argmax, token copy, counter adds,
-        embedding gather).  Both give the same tokens bit for bit.  spec_k: draft tokens per
-        speculative round (the verify graph scores spec_k + 1 tokens)."""
+        embedding gather).  fused_qkv: each layer's qkv product and attention block through
+        solort_decode_qkv_layer (one launch where its shapes allow); False runs solort_gemv and
+        solort_decode_layer.  All combinations give the same tokens bit for bit.  spec_k: draft
+        tokens per speculative round (the verify graph scores spec_k + 1 tokens)."""
         self.w = weights
         self.fused_tail = bool(fused_tail)
+        self.fused_qkv = bool(fused_qkv)
         # Measurement hook (bench.py): a decode graph captured with this False leaves the attention
         # call out of every layer, so the difference in step time is the attention's cost inside
         # the step.  Its tokens are not the model's.
@@ -116,7 +119,7 @@ class GraphQwen3Decode:
         self.act = torch.zeros(s.inter, **bf)
         self.logits = torch.zeros(1, s.vocab, **bf)
         self.cs = torch.zeros(2, 1, HD // 2, **bf)
-        self.ws = ops.attn_workspace(1, s.nh, s.nkv, max(decode_splits(b, s.nkv) for b in self.buckets), self.dev)
+        self.ws = ops.decode_qkv_workspace(s.nh, s.nkv, max(decode_splits(b, s.nkv) for b in self.buckets), self.dev)
         self.ws_arg = ops.gemv_argmax_workspace(s.vocab, self.dev) if fused_tail else ops.argmax_workspace(1, self.dev)
         self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
         # prefill (cuda_graph_executor.py:83-85, :104-161): one graph per prompt bucket over the padded
@@ -161,10 +164,15 @@ class GraphQwen3Decode:
         ops.rope_rows(self.inv_freq, self.pos, 1, self.cs)             # :164, once per step
         x = self.x.view(s.hidden)
         for li in range(s.layers):
-            ops.gemv(w.wqkv[li], x, self.qkv.view(-1), w.in_ln[li], self.eps)                          # :170-171
-            if self.attention_in_step:
-                ops.decode_layer(self.qkv, w.qn[li], w.kn[li], self.eps, self.cs, self.pos, self.kc[li],
-                                 self.vc[li], bound, self.scale, self.ws, ns, self.ctx, s.nh, s.nkv)   # :172-184
+            if self.fused_qkv and self.attention_in_step:                                             # :170-184
+                ops.decode_qkv_layer(x, w.in_ln[li], self.eps, w.wqkv[li], w.qn[li], w.kn[li], self.eps, self.cs,
+                                     self.pos, self.kc[li], self.vc[li], bound, self.scale, self.ws, ns,
+                                     self.qkv.view(-1), self.ctx, s.nh, s.nkv)
+            else:
+                ops.gemv(w.wqkv[li], x, self.qkv.view(-1), w.in_ln[li], self.eps)                      # :170-171
+                if self.attention_in_step:
+                    ops.decode_layer(self.qkv, w.qn[li], w.kn[li], self.eps, self.cs, self.pos, self.kc[li],
+                                     self.vc[li], bound, self.scale, self.ws, ns, self.ctx, s.nh, s.nkv)  # :172-184
             ops.gemv(w.wo[li], self.ctx.view(-1), x, res=x, mode=ops.GEMV_RESID)                       # :185
             ops.gemv(w.wgu[li], x, self.act, w.post_ln[li], self.eps, mode=ops.GEMV_SWIGLU,
                      inter=s.inter)                                                                    # :186-187

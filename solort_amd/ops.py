@@ -250,6 +250,56 @@ def decode_layer(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps:
     _lib.check(rc, "decode_layer")
 
 
+def decode_qkv_workspace(nh: int, nkv: int, n_split: int, device: torch.device | str) -> torch.Tensor:
+    """Workspace for decode_qkv_layer (the splits' partials and the handed-over qkv rows)."""
+    nbytes = _lib.load().solort_decode_qkv_workspace_bytes(nh, nkv, n_split)
+    _need(nbytes > 0, f"bad workspace request nh={nh} nkv={nkv} n_split={n_split}")
+    return torch.zeros(nbytes, dtype=torch.uint8, device=device)
+
+
+def decode_qkv_layer(x: torch.Tensor, in_w: torch.Tensor, in_eps: float, wqkv: torch.Tensor, qn_w: torch.Tensor,
+                     kn_w: torch.Tensor, eps: float, rope_cs: torch.Tensor, pos0: torch.Tensor, k_cache: torch.Tensor,
+                     v_cache: torch.Tensor, bound: int, scale: float, ws: torch.Tensor, n_split: int,
+                     qkv_out: torch.Tensor, out: torch.Tensor, nh: int, nkv: int) -> None:
+    """One token's qkv product and attention block: qkv = rmsnorm(x, in_w) @ wqkv^T, then decode_layer
+    on it into out [1, nh*128]; see solort_decode_qkv_layer (one launch where the shapes allow,
+    else the product into qkv_out [(nh+2nkv)*128] and then decode_layer)."""
+    width = (nh + 2 * nkv) * HD
+    _on_gpu("x", x, torch.bfloat16)
+    hidden = x.numel()
+    _need(x.is_contiguous() and x.data_ptr() % 16 == 0, "x must be contiguous and 16-byte aligned")
+    _on_gpu("in_w", in_w, torch.bfloat16)
+    _need(in_w.shape == (hidden,) and in_w.is_contiguous(), f"in_w must be [{hidden}] contiguous")
+    _on_gpu("wqkv", wqkv, torch.bfloat16)
+    _need(wqkv.dim() == 2 and wqkv.shape == (width, hidden) and wqkv.stride(1) == 1,
+          f"wqkv must be [{width}, {hidden}] with unit column stride")
+    for name, w in (("qn_w", qn_w), ("kn_w", kn_w)):
+        _on_gpu(name, w, torch.bfloat16)
+        _need(w.shape == (HD,) and w.is_contiguous(), f"{name} must be [{HD}] contiguous")
+    _rope_rows_ok(rope_cs, 1)
+    ts, hs, max_len = _cache_strides("k_cache", k_cache, nkv)
+    _on_gpu("v_cache", v_cache, torch.bfloat16)
+    _need(v_cache.shape == k_cache.shape and v_cache.stride() == k_cache.stride(),
+          "v_cache must match k_cache in shape and strides")
+    _need(pos0.is_cuda and pos0.dtype == torch.int64 and pos0.numel() >= 1, "pos0 must be int64 on the device")
+    _on_gpu("qkv_out", qkv_out, torch.bfloat16)
+    _need(qkv_out.numel() >= width and qkv_out.is_contiguous(), f"qkv_out must hold {width} contiguous elements")
+    _need(out.is_cuda and out.dtype in (torch.bfloat16, torch.float32), "out must be bf16 or fp32 on the device")
+    _need(out.shape == (1, nh * HD) and out.is_contiguous() and out.data_ptr() % 16 == 0,
+          f"out must be [1, {nh * HD}] contiguous and 16-byte aligned")
+    lib = _lib.load()
+    need = lib.solort_decode_qkv_workspace_bytes(nh, nkv, n_split)
+    _need(ws.is_cuda and ws.numel() * ws.element_size() >= need and ws.data_ptr() % 16 == 0,
+          f"workspace too small: need {need} bytes")
+    dt = DTYPE_F32 if out.dtype == torch.float32 else DTYPE_BF16
+    rc = lib.solort_decode_qkv_layer(
+        x.data_ptr(), hidden, in_w.data_ptr(), float(in_eps), wqkv.data_ptr(), wqkv.stride(0), nh, nkv, HD,
+        qn_w.data_ptr(), kn_w.data_ptr(), float(eps), rope_cs.data_ptr(), pos0.data_ptr(), k_cache.data_ptr(),
+        v_cache.data_ptr(), ts, hs, max_len, int(bound), float(scale), ws.data_ptr(), int(n_split),
+        qkv_out.data_ptr(), out.data_ptr(), dt, _stream(x))
+    _lib.check(rc, "decode_qkv_layer")
+
+
 def decode_layer_noalloc(qkv: torch.Tensor, qn_w: torch.Tensor, kn_w: torch.Tensor, eps: float,
                          rope_cs: torch.Tensor, pos0: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
                          bound: int, scale: float, n_split: int, out: torch.Tensor, nh: int, nkv: int) -> None:
