@@ -368,6 +368,8 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
   //    the compiler wait for all of them before the first use.
   constexpr int NROWS = FUSED ? NQ * (G + 2) : R;
   uint4 raw0 = make_uint4(0u, 0u, 0u, 0u), wq0 = raw0, wk0 = raw0, c0 = raw0, s0 = raw0;
+  XChunks xin;  // QKV: this thread's chunks of x and the input norm weight, loaded first
+  if constexpr (QKV) gemv_x_load<true>(x, in_w, hidden, xin);
   if constexpr (!QKV) {
     const int row = min(slot, NROWS - 1);
     if constexpr (FUSED) {
@@ -451,7 +453,7 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
     // head's qkv outputs, stored by the head's splits (all on this XCD) with this launch's tag.
     __shared__ float s_red[4];
     uint4* s_x = reinterpret_cast<uint4*>(s_v);
-    gemv_stage_x<true>(x, in_w, qi->eps, hidden, s_x, s_red);
+    gemv_x_finish<true>(xin, x, in_w, qi->eps, hidden, s_x, s_red);
     float acc[RW];
 #pragma unroll
     for (int r = 0; r < RW; ++r) acc[r] = 0.f;
@@ -476,6 +478,7 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
       if (lane == r / 2) mine = pr;
     }
     if (lane < RW / 2) items[i0 / 2 + lane] = make_uint2(mine, qtag);
+    SOLORT_STAMP(tid == 0, kvh + nkv * split, 8);
     const int prow = min(slot, NROWS - 1);
     const __amdgpu_buffer_rsrc_t rq =
         __builtin_amdgcn_make_buffer_rsrc(items, (short)0, (G + 2) * 64 * 8, 0x00020000);
@@ -493,6 +496,7 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
                 : make_uint4(a01.x, a01.z, a23.x, a23.z);
     pos0 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)posv.y) << 32) |
                      (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)posv.x));
+    SOLORT_STAMP(tid == 0, kvh + nkv * split, 9);
   }
 
   // 3. q rows (and, fused, the new tokens' K/V rows) into LDS.

@@ -19,31 +19,44 @@ __device__ __forceinline__ float wave_sum64(float v) {
 // x [K] bf16 into sx as K / 8 chunks of 16 bytes, every thread of a 256-thread
 // workgroup taking part; NORM: bf16(fp32(x) * rsqrt(mean(fp32(x)^2) + eps) *
 // fp32(norm_w)), the sum of squares in fp32 with one block reduction (s_red: 4
-// floats).  Ends with a workgroup barrier.
+// floats).  In two parts, so that a caller can issue the loads early:
+// gemv_x_load reads this thread's first kXReg chunks of x and norm_w (K <= 8192
+// in one round; larger K re-reads the rest in gemv_x_finish), gemv_x_finish
+// normalises and stores them and ends with a workgroup barrier.
+constexpr int kXReg = 4;
+struct XChunks {
+  uint4 x[kXReg], g[kXReg];
+};
+
 template <bool NORM>
-__device__ __forceinline__ void gemv_stage_x(const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
-                                             float eps, int K, uint4* sx, float* s_red) {
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int nch = K >> 3;
+__device__ __forceinline__ void gemv_x_load(const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w, int K,
+                                            XChunks& c) {
+  const int tid = threadIdx.x, nch = K >> 3;
   if constexpr (NORM) {
-    // The first kXReg chunks of this thread stay in registers between the two
-    // passes (k <= 8192 in one round); larger k re-reads the rest.
-    constexpr int kXReg = 4;
-    uint4 xr[kXReg], gr[kXReg];
-    float ss = 0.f;
 #pragma unroll
     for (int q = 0; q < kXReg; ++q) {
       const int i = tid + 256 * q;
       if (i < nch) {
-        xr[q] = *reinterpret_cast<const uint4*>(x + 8 * i);
-        gr[q] = *reinterpret_cast<const uint4*>(norm_w + 8 * i);
+        c.x[q] = *reinterpret_cast<const uint4*>(x + 8 * i);
+        c.g[q] = *reinterpret_cast<const uint4*>(norm_w + 8 * i);
       }
     }
+  }
+}
+
+template <bool NORM>
+__device__ __forceinline__ void gemv_x_finish(const XChunks& c, const uint16_t* __restrict__ x,
+                                              const uint16_t* __restrict__ norm_w, float eps, int K, uint4* sx,
+                                              float* s_red) {
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int nch = K >> 3;
+  if constexpr (NORM) {
+    float ss = 0.f;
 #pragma unroll
     for (int q = 0; q < kXReg; ++q) {
       if (tid + 256 * q < nch) {
         float v[8];
-        unpack8(xr[q], v);
+        unpack8(c.x[q], v);
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss = fmaf(v[e], v[e], ss);
       }
@@ -64,8 +77,8 @@ __device__ __forceinline__ void gemv_stage_x(const uint16_t* __restrict__ x, con
       const int i = tid + 256 * q;
       if (i < nch) {
         float v[8], g[8];
-        unpack8(xr[q], v);
-        unpack8(gr[q], g);
+        unpack8(c.x[q], v);
+        unpack8(c.g[q], g);
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = (v[e] * r) * g[e];
         sx[i] = pack8(v);
@@ -83,6 +96,14 @@ __device__ __forceinline__ void gemv_stage_x(const uint16_t* __restrict__ x, con
     for (int i = tid; i < nch; i += 256) sx[i] = *reinterpret_cast<const uint4*>(x + 8 * i);
   }
   __syncthreads();
+}
+
+template <bool NORM>
+__device__ __forceinline__ void gemv_stage_x(const uint16_t* __restrict__ x, const uint16_t* __restrict__ norm_w,
+                                             float eps, int K, uint4* sx, float* s_red) {
+  XChunks c;
+  gemv_x_load<NORM>(x, norm_w, K, c);
+  gemv_x_finish<NORM>(c, x, norm_w, eps, K, sx, s_red);
 }
 
 }  // namespace solort
