@@ -131,7 +131,8 @@ def main() -> int:
         print(json.dumps(verify_extras(torch, ops, wl, runners, dev, sh)), flush=True)
         return 0
     if args.only == "gemv":
-        print(json.dumps({"decode_gemv": gemv_extras(torch, ops, dev)}), flush=True)
+        print(json.dumps({"decode_gemv": gemv_extras(torch, ops, dev),
+                          "decode_qkv_layer": qkv_layer_extras(torch, ops, wl, dev)}), flush=True)
         return 0
     if args.only == "torchref":
         print(json.dumps({"torch_reference_decode": torch_reference_extras(torch, runners, dev, sh, bound)}),
@@ -220,6 +221,7 @@ def main() -> int:
         result["extras"]["decode_8b_kv32768"] = long_decode_extras(torch, ops, wl, dev)
         result["extras"]["decode_mid_kv"] = mid_decode_extras(torch, ops, wl, dev)
         result["extras"]["decode_gemv"] = gemv_extras(torch, ops, dev)
+        result["extras"]["decode_qkv_layer"] = qkv_layer_extras(torch, ops, wl, dev)
         result["extras"]["paged_decode_kv1024"] = paged_extras(torch, ops, runners, dev, sh)
         result["extras"]["torch_reference_decode"] = torch_reference_extras(torch, runners, dev, sh, bound)
         result["extras"]["decode_model"] = model_extras(torch, dev)
@@ -377,6 +379,8 @@ def floor_extras(torch, ops, runners, dev, sh) -> dict:
 STAMP_PHASES_DECODE = {0: "start", 1: "position read", 2: "q ready", 3: "key loop done", 4: "partial stored",
                        5: "end", 6: "merge poll started", 7: "merge poll done"}
 STAMP_PHASES_PREFILL = {0: "start", 3: "key loop done", 5: "end"}
+STAMP_PHASES_QKV = {0: "start", 8: "qkv outputs stored", 9: "qkv rows polled", 2: "q ready", 3: "key loop done",
+                    4: "partial stored", 6: "merge poll started", 7: "merge poll done", 5: "end"}
 
 
 def _stamp_summary(np, st, phases, groups=None) -> dict:
@@ -427,7 +431,8 @@ def stamp_extras(torch, ops, wl, runners, dev, sh, bound) -> dict:
     """In-kernel phase timelines from the tracing build (include/solort_trace.h): the last
     solort_decode_layer launch of a replayed Qwen3-4B decode step at KV 1024, the last call of a
     graph of 8 Qwen3-8B calls at KV 32768 (32 splits), the last of 4 verify calls (5 tokens at 2048,
-    the 17 splits that hold keys) and the last prefill_kernel launch of a graph at T = 1024."""
+    the 17 splits that hold keys), the last prefill_kernel launch of a graph at T = 1024 and the last
+    decode_qkv_lanes_kernel launch (qkv product in the decode launch) of a 36-layer graph at KV 1024."""
     import numpy as np
 
     from solort_amd import _lib
@@ -511,13 +516,36 @@ def stamp_extras(torch, ops, wl, runners, dev, sh, bound) -> dict:
     torch.cuda.synchronize()
     n_tiles = T // 16  # 16 positions x 4 query heads per block
     nb = n_tiles * sh.nkv
-    st = read("solort_phase_stamps_prefill", nb)
+    st_pre = read("solort_phase_stamps_prefill", nb)
     # block index of a tile by rank (0 = heaviest): the first round of blocks (one per CU) takes
     # ranks in order, the second round from the lightest up
     rnd = max(1, torch.cuda.get_device_properties(dev).multi_processor_count // sh.nkv)
     ib = [rk if rk < rnd else rnd + (n_tiles - 1 - rk) for rk in range(n_tiles)]
     tiles = [[kvh + sh.nkv * ib[rk] for kvh in range(sh.nkv)] for rk in range(n_tiles)]  # heaviest tile first
-    res["prefill_qwen3_4b_t1024"] = _stamp_summary(np, st, STAMP_PHASES_PREFILL,
+    # the qkv product inside the decode launch: the last of 36 layers (distinct weights) at KV 1024
+    nl, hidden, width = 36, 2560, sh.qkv_width
+    wq = [(torch.randn(width, hidden, generator=gen, device=dev) * hidden ** -0.5).to(torch.bfloat16)
+          for _ in range(nl)]
+    in_w = (1.0 + 0.1 * torch.randn(hidden, generator=gen, device=dev)).to(torch.bfloat16)
+    xs = torch.randn(nl, hidden, generator=gen, device=dev).to(torch.bfloat16)
+    pq = torch.tensor([1000], dtype=torch.long, device=dev)
+    csq = ops.rope_rows(r.inv_freq, pq, 1)
+    wsq = ops.decode_qkv_workspace(sh.nh, sh.nkv, 32, dev)
+    oq = torch.empty(nl, 1, sh.nh * 128, dtype=torch.bfloat16, device=dev)
+    qkv = torch.empty(width, dtype=torch.bfloat16, device=dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for li in range(nl):
+            ops.decode_qkv_layer(xs[li], in_w, wl.EPS, wq[li], r.qn_w[li], r.kn_w[li], r.eps, csq, pq, r.kc[li],
+                                 r.vc[li], 1024, sh.scale, wsq, 32, qkv, oq[li], sh.nh, sh.nkv)
+    for _ in range(3):
+        graph.replay()
+    torch.cuda.synchronize()
+    st = read("solort_phase_stamps_decode", sh.nkv * 32)
+    res["decode_qkv_layer_qwen3_4b_kv1024"] = _stamp_summary(np, st, STAMP_PHASES_QKV)
+    del wq
+    torch.cuda.empty_cache()
+    res["prefill_qwen3_4b_t1024"] = _stamp_summary(np, st_pre, STAMP_PHASES_PREFILL,
                                                    ("end, median per query tile (heaviest first)", tiles, 5))
     return res
 
@@ -858,6 +886,49 @@ def long_decode_extras(torch, ops, wl, dev, n_caches: int = 8) -> dict:
     res["frac_of_pattern_ceiling"] = round(pat[1] / best[1], 4)
     del kcs, vcs
     torch.cuda.empty_cache()
+    return res
+
+
+def qkv_layer_extras(torch, ops, wl, dev, L: int = 36) -> dict:
+    """Qwen3-4B decode layer's qkv product and attention block: solort_decode_qkv_layer (the product
+    inside the attention launch) against solort_gemv + solort_decode_layer, each as a graph of L
+    layers with distinct weights (1.1 GB) and caches, at KV 1024 and 2048 (32 splits); us per layer.
+    The bytes per layer are the wqkv matrix plus the attention's K/V rows."""
+    sh = wl.QWEN3_4B
+    hidden, width = 2560, sh.qkv_width
+    res = {"workload": f"Qwen3-4B decode, {L} layers of distinct weights and caches, one token", "by_kv": {}}
+    for bound, pos in ((1024, 1000), (2048, 2000)):
+        gen = torch.Generator(device=dev).manual_seed(77)
+        wq = [(torch.randn(width, hidden, generator=gen, device=dev) * hidden ** -0.5).to(torch.bfloat16)
+              for _ in range(L)]
+        in_w = (1.0 + 0.1 * torch.randn(hidden, generator=gen, device=dev)).to(torch.bfloat16)
+        nw = (1.0 + 0.1 * torch.randn(128, generator=gen, device=dev)).to(torch.bfloat16)
+        kc = torch.randn(L, bound, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16)
+        vc = torch.randn(L, bound, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16)
+        posb = torch.tensor([pos], dtype=torch.long, device=dev)
+        cs = ops.rope_rows(ops.inv_freq(128, wl.THETA, dev), posb, 1)
+        ws = ops.decode_qkv_workspace(sh.nh, sh.nkv, 32, dev)
+        xs = torch.randn(L, hidden, generator=gen, device=dev).to(torch.bfloat16)
+        out = torch.empty(L, 1, sh.nh * 128, dtype=torch.bfloat16, device=dev)
+        qkv = torch.empty(1, width, dtype=torch.bfloat16, device=dev)
+
+        def two_launches():
+            for li in range(L):
+                ops.gemv(wq[li], xs[li], qkv.view(-1), in_w, wl.EPS)
+                ops.decode_layer(qkv, nw, nw, wl.EPS, cs, posb, kc[li], vc[li], bound, sh.scale, ws, 32, out[li],
+                                 sh.nh, sh.nkv)
+
+        def one_launch():
+            for li in range(L):
+                ops.decode_qkv_layer(xs[li], in_w, wl.EPS, wq[li], nw, nw, wl.EPS, cs, posb, kc[li], vc[li], bound,
+                                     sh.scale, ws, 32, qkv.view(-1), out[li], sh.nh, sh.nkv)
+        us1 = _graph_us(torch, dev, [one_launch], reps=5) / L
+        us2 = _graph_us(torch, dev, [two_launches], reps=5) / L
+        nbytes = width * hidden * 2 + decode_bytes(pos + 1)
+        res["by_kv"][str(bound)] = {"one_launch_us": round(us1, 3), "two_launches_us": round(us2, 3),
+                                    "gbps": round(nbytes / (us1 * 1e-6) / 1e9, 1), "bytes": nbytes}
+        del wq, kc, vc
+        torch.cuda.empty_cache()
     return res
 
 
