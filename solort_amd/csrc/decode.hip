@@ -1510,15 +1510,18 @@ static void launch_qkv_u(const DecodeArgs& a, unsigned strides8, unsigned geom, 
   if (a.U == 4)
     hipLaunchKernelGGL((decode_qkv_lanes_kernel<G, 4, RW, CPL>), grid, dim3(256), 0, s, a.kc, a.vc, strides8, geom,
                        (const uint16_t*)x, (const uint16_t*)wqkv, (const uint16_t*)in_w, a.tail, q);
-  else
+  else if (a.U == 2)
     hipLaunchKernelGGL((decode_qkv_lanes_kernel<G, 2, RW, CPL>), grid, dim3(256), 0, s, a.kc, a.vc, strides8, geom,
+                       (const uint16_t*)x, (const uint16_t*)wqkv, (const uint16_t*)in_w, a.tail, q);
+  else
+    hipLaunchKernelGGL((decode_qkv_lanes_kernel<G, 1, RW, CPL>), grid, dim3(256), 0, s, a.kc, a.vc, strides8, geom,
                        (const uint16_t*)x, (const uint16_t*)wqkv, (const uint16_t*)in_w, a.tail, q);
 }
 
 static bool launch_qkv(const DecodeArgs& a, int hidden, const void* x, const void* wqkv, const void* in_w,
                        const QkvIn& q, hipStream_t s) {
   const int G = a.nh / a.nkv;
-  if (!a.lanes || (a.U != 2 && a.U != 4) || a.n_split != kQkvSplits || !a.tail.merge || a.tok_stride >= (1 << 19) ||
+  if (!a.lanes || a.n_split != kQkvSplits || !a.tail.merge || a.tok_stride >= (1 << 19) ||
       a.head_stride >= (1 << 19) || a.nh >= 2048 || a.bound >= (1 << 19))
     return false;
   const unsigned strides8 = (unsigned)(a.tok_stride / 8) | (unsigned)(a.head_stride / 8) << 16;

@@ -24,7 +24,8 @@ import torch
 import torch.nn.functional as F
 
 from . import ops
-from .runner import DECODE_BUCKETS, FUSED_PREFILL_MIN, HD, PREFILL_BUCKETS, decode_splits, verify_splits
+from .runner import (DECODE_BUCKETS, FUSED_PREFILL_MIN, HD, PREFILL_BUCKETS, decode_qkv_splits, decode_splits,
+                     verify_splits)
 
 
 @dataclass(frozen=True)
@@ -119,7 +120,8 @@ class GraphQwen3Decode:
         self.act = torch.zeros(s.inter, **bf)
         self.logits = torch.zeros(1, s.vocab, **bf)
         self.cs = torch.zeros(2, 1, HD // 2, **bf)
-        self.ws = ops.decode_qkv_workspace(s.nh, s.nkv, max(decode_splits(b, s.nkv) for b in self.buckets), self.dev)
+        self.ws = ops.decode_qkv_workspace(
+            s.nh, s.nkv, max(max(decode_splits(b, s.nkv), decode_qkv_splits(b, s.nkv)) for b in self.buckets), self.dev)
         self.ws_arg = ops.gemv_argmax_workspace(s.vocab, self.dev) if fused_tail else ops.argmax_workspace(1, self.dev)
         self._graphs: dict[int, torch.cuda.CUDAGraph] = {}
         # prefill (cuda_graph_executor.py:83-85, :104-161): one graph per prompt bucket over the padded
@@ -159,6 +161,7 @@ class GraphQwen3Decode:
         then argmax (:206), the token bookkeeping of :241-242 and :372, and the next step's :165."""
         s, w = self.s, self.w
         ns = decode_splits(bound, s.nkv)
+        nsq = decode_qkv_splits(bound, s.nkv)
         if not self.fused_tail:
             torch.index_select(w.embed, 0, self.tok, out=self.x)                                       # :165
         ops.rope_rows(self.inv_freq, self.pos, 1, self.cs)             # :164, once per step
@@ -166,7 +169,7 @@ class GraphQwen3Decode:
         for li in range(s.layers):
             if self.fused_qkv and self.attention_in_step:                                             # :170-184
                 ops.decode_qkv_layer(x, w.in_ln[li], self.eps, w.wqkv[li], w.qn[li], w.kn[li], self.eps, self.cs,
-                                     self.pos, self.kc[li], self.vc[li], bound, self.scale, self.ws, ns,
+                                     self.pos, self.kc[li], self.vc[li], bound, self.scale, self.ws, nsq,
                                      self.qkv.view(-1), self.ctx, s.nh, s.nkv)
             else:
                 ops.gemv(w.wqkv[li], x, self.qkv.view(-1), w.in_ln[li], self.eps)                      # :170-171

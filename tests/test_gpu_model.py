@@ -16,6 +16,7 @@ import torch
 
 from oracle import ref
 from solort_amd.model import GraphQwen3Decode, ModelShape, RandomQwen3
+from solort_amd.runner import decode_qkv_splits, decode_splits
 
 pytestmark = pytest.mark.gpu
 TINY = ModelShape("tiny", hidden=512, inter=1024, nh=4, nkv=2, layers=2, vocab=4096, tie_embeddings=True)
@@ -62,6 +63,26 @@ def test_decode_graph_replays_equal_eager_steps(gpu):
     u2.kc.copy_(u.kc)
     u2.vc.copy_(u.vc)
     assert u2.generate(7, p0, n) == toks and torch.equal(u2.kc, m.kc)
+    _say(f"  tokens {toks}")
+
+
+@pytest.mark.parametrize("p0", [400, 1000, 1500], ids=["bucket512", "bucket1024", "bucket2048"])
+def test_qkv_in_attention_launch_equals_own_launch(gpu, p0):
+    """The Qwen3-4B layer shapes (hidden 2560, 32 q / 8 kv heads, 2 layers) in the buckets where the
+    QKV product runs inside the attention launch: the same tokens as the step with the product as
+    its own launch, and the same cache bits where both run the attention with the same split count
+    (at 512 keys the fused launch runs 32 splits of 16 keys, the attention on its own 16 of 32, so
+    the merge adds the partials in another order)."""
+    n = 6
+    w, m = _model(gpu, p0, QWEN3_4B_2L, max_len=2048)
+    u = GraphQwen3Decode(w, 2048, fused_qkv=False)
+    u.kc.copy_(m.kc)
+    u.vc.copy_(m.vc)
+    toks = m.generate(5, p0, n)
+    assert u.generate(5, p0, n) == toks
+    bound = m.bucket_for(p0)
+    if decode_qkv_splits(bound, QWEN3_4B_2L.nkv) == decode_splits(bound, QWEN3_4B_2L.nkv):
+        assert torch.equal(u.kc, m.kc) and torch.equal(u.vc, m.vc)
     _say(f"  tokens {toks}")
 
 

@@ -30,6 +30,7 @@ CASES = [
     ("4B position 0", 32, 8, 2560, 1024, 1024, 0, 32),
     ("0.6B KV 1024", 16, 8, 1024, 1024, 1024, 700, 32),
     ("8B KV 1024", 32, 8, 4096, 1024, 1024, 1000, 32),
+    ("4B KV 512, 16-key splits", 32, 8, 2560, 512, 512, 300, 32),
     ("4B KV 512, 16 splits (two launches)", 32, 8, 2560, 512, 512, 300, 16),
     ("hidden 2048 (two launches)", 32, 8, 2048, 1024, 1024, 800, 32),
 ]

@@ -1,5 +1,5 @@
 """Host-side logic of the runner that needs no GPU."""
-from solort_amd.runner import DECODE_BUCKETS, PREFILL_BUCKETS, decode_splits, verify_splits
+from solort_amd.runner import DECODE_BUCKETS, PREFILL_BUCKETS, decode_qkv_splits, decode_splits, verify_splits
 
 
 def test_decode_splits_heuristic():
@@ -13,6 +13,13 @@ def test_decode_splits_heuristic():
         assert decode_splits(bound, 8) == 32
     assert decode_splits(65536, 8) == 64  # chunks of at most 1024 keys
     assert decode_splits(1024, 32) == 8 and decode_splits(1024, 1) == 64
+
+
+def test_decode_qkv_splits_heuristic():
+    for bound in (512, 1024, 2048):  # chunks of 16, 32, 64 keys: the fused QKV launch
+        assert decode_qkv_splits(bound, 8) == 32
+    for bound in (128, 256, 4096, 32768):  # elsewhere the attention's own routing
+        assert decode_qkv_splits(bound, 8) == decode_splits(bound, 8)
 
 
 def test_verify_splits_heuristic():
