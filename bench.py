@@ -892,12 +892,14 @@ def long_decode_extras(torch, ops, wl, dev, n_caches: int = 8) -> dict:
 def qkv_layer_extras(torch, ops, wl, dev, L: int = 36) -> dict:
     """Qwen3-4B decode layer's qkv product and attention block: solort_decode_qkv_layer (the product
     inside the attention launch) against solort_gemv + solort_decode_layer, each as a graph of L
-    layers with distinct weights (1.1 GB) and caches, at KV 1024 and 2048 (32 splits); us per layer.
+    layers with distinct weights (1.1 GB) and caches, at KV 1024, 2048 and 4096 (32 splits; at 4096
+    the MFMA split kernel; longer chunks run as the two launches inside the entry point); us per
+    layer.
     The bytes per layer are the wqkv matrix plus the attention's K/V rows."""
     sh = wl.QWEN3_4B
     hidden, width = 2560, sh.qkv_width
     res = {"workload": f"Qwen3-4B decode, {L} layers of distinct weights and caches, one token", "by_kv": {}}
-    for bound, pos in ((1024, 1000), (2048, 2000)):
+    for bound, pos in ((1024, 1000), (2048, 2000), (4096, 4000)):
         gen = torch.Generator(device=dev).manual_seed(77)
         wq = [(torch.randn(width, hidden, generator=gen, device=dev) * hidden ** -0.5).to(torch.bfloat16)
               for _ in range(L)]

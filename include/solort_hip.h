@@ -221,7 +221,7 @@ int solort_decode_layer(const void* qkv, int64_t qkv_row_stride, int nq, int nh,
  * (SOLORT_GEMV_PLAIN, norm_w = in_w) followed by solort_decode_layer, bit for
  * bit.  x [hidden] bf16 (the layer input); wqkv [(nh + 2 nkv) * hd][row
  * stride] bf16.  Where the shapes allow (32 key splits per KV head of 16 to
- * 64 keys, the in-launch merge, the packed cache layout, (group, hidden) in
+ * 128 keys, the in-launch merge, the packed cache layout, (group, hidden) in
  * {(2, 1024), (4, 2560), (4, 4096)}, wqkv rows contiguous) it is one launch:
  * the splits of each KV head compute that head's q, k and v rows, hand them
  * over through the XCD's L2 as tagged pairs, and continue with the attention,

@@ -331,6 +331,79 @@ __device__ __forceinline__ void split_merge(const DecodeTail& a, int kvh, int sp
   }
 }
 
+// The qkv product inside a decode launch (one new token), shared by both
+// split kernels.  qkv_issue: this wave's RW weight rows of the KV head's
+// (G + 2) * 128 outputs (outputs i0 .. i0 + RW - 1: the rows of q heads
+// kvh*G .. kvh*G + G - 1, then its K and V rows), lane l taking 16-byte chunks
+// l + 64u as the GEMV kernel does.
+template <int G, int RW, int CPL>
+__device__ __forceinline__ void qkv_issue(uint4 (&wv)[RW][CPL], const uint16_t* wqkv, int hidden, int i0, int kvh,
+                                          int nh, int nkv, int lane) {
+#pragma unroll
+  for (int r = 0; r < RW; ++r) {
+    const int i = i0 + r, c = i >> 7;
+    const int hs = c < G ? kvh * G + c : (c == G ? nh + kvh : nh + nkv + kvh);
+    const uint16_t* wrow = wqkv + (int64_t)(hs * SOLORT_HD + (i & 127)) * hidden;
+#pragma unroll
+    for (int u = 0; u < CPL; ++u) wv[r][u] = ld_stream(wrow + 8 * (lane + 64 * u));
+  }
+}
+
+// x normalised into s_x (LDS free until the caller's next use of it), the
+// wave's RW dot products in the GEMV kernel's order and rounding, stored as
+// tagged pairs (two bf16 outputs, the launch's tag); then the calling lane's 8
+// values of row prow (of the head's G + 2 rows), polled from the XCD's L2 where
+// the head's splits store them.  A lane that gives up after kMergeSpin rounds
+// returns NaN.  Every thread of the 256-thread block calls it.
+template <int G, int RW, int CPL>
+__device__ __forceinline__ uint4 qkv_handover(const uint4 (&wv)[RW][CPL], const XChunks& xin, const uint16_t* x,
+                                              const uint16_t* in_w, float eps, int hidden, uint4* s_x, float* s_red,
+                                              uint2* items, unsigned tag, int i0, int prow, int j, int lane,
+                                              int stamp_block) {
+  gemv_x_finish<true>(xin, x, in_w, eps, hidden, s_x, s_red);
+  float acc[RW];
+#pragma unroll
+  for (int r = 0; r < RW; ++r) acc[r] = 0.f;
+#pragma unroll
+  for (int u = 0; u < CPL; ++u) {
+    const uint4 xv = s_x[lane + 64 * u];
+#pragma unroll
+    for (int r = 0; r < RW; ++r) {
+      float d = dot2bf(wv[r][u].x, xv.x, acc[r]);
+      d = dot2bf(wv[r][u].y, xv.y, d);
+      d = dot2bf(wv[r][u].z, xv.z, d);
+      acc[r] = dot2bf(wv[r][u].w, xv.w, d);
+    }
+  }
+  uint32_t mine = 0;
+#pragma unroll
+  for (int r = 0; r < RW; r += 2) {
+    const uint32_t pr = f2bf(wave_sum64(acc[r])) | f2bf(wave_sum64(acc[r + 1])) << 16;
+    if (lane == r / 2) mine = pr;
+  }
+  if (lane < RW / 2) items[i0 / 2 + lane] = make_uint2(mine, tag);
+  SOLORT_STAMP(threadIdx.x == 0, stamp_block, 8);
+  const __amdgpu_buffer_rsrc_t rq = __builtin_amdgcn_make_buffer_rsrc(items, (short)0, (G + 2) * 64 * 8, 0x00020000);
+  const int off = (prow * 64 + 4 * j) * 8;
+  uint4 a01 = make_uint4(0u, 0u, 0u, 0u), a23 = a01;
+  bool pend = true;
+  for (int it = 0; it < kMergeSpin && pend; ++it) {
+    asm volatile("" ::: "memory");  // a fresh load every round
+    a01 = ld_l2(rq, off);
+    a23 = ld_l2(rq, off + 16);
+    const bool bad = (a01.y != tag) | (a01.w != tag) | (a23.y != tag) | (a23.w != tag);
+    pend = __builtin_amdgcn_ballot_w64(bad) != 0;
+  }
+  SOLORT_STAMP(threadIdx.x == 0, stamp_block, 9);
+  return pend ? make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u)  // NaN: gave up
+              : make_uint4(a01.x, a01.z, a23.x, a23.z);
+}
+
+__device__ __forceinline__ int64_t pos_from(uint2 v) {
+  return (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)v.y) << 32) |
+                   (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)v.x));
+}
+
 // Lane-parallel split kernel, for short key chunks (latency-bound: one to a
 // few key rows per slot).  Grid (nkv, n_split): block (kvh, split).  qsrc:
 // fused, the qkv rows (row stride qsrc_stride); unfused, the q rows
@@ -410,14 +483,7 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
   uint4 wv[QRW][QCPL];
   const int i0 = (split * 4 + wave) * RW;
   if constexpr (QKV) {
-#pragma unroll
-    for (int r = 0; r < RW; ++r) {
-      const int i = i0 + r, c = i >> 7;
-      const int hs = c < G ? kvh * G + c : (c == G ? nh + kvh : nh + nkv + kvh);
-      const uint16_t* wrow = wqkv + (int64_t)(hs * SOLORT_HD + (i & 127)) * hidden;
-#pragma unroll
-      for (int u = 0; u < CPL; ++u) wv[r][u] = ld_stream(wrow + 8 * (lane + 64 * u));
-    }
+    qkv_issue<G, RW, CPL>(wv, wqkv, hidden, i0, kvh, nh, nkv, lane);
     const int row = min(slot, NROWS - 1);
     wq0 = *reinterpret_cast<const uint4*>(qn_w + j * 8);
     wk0 = *reinterpret_cast<const uint4*>(kn_w + j * 8);
@@ -452,51 +518,11 @@ __device__ __forceinline__ void decode_lanes_body(uint16_t* kc, uint16_t* vc, in
     // kernel's order and rounding, stored as tagged pairs; then each slot polls its row of the
     // head's qkv outputs, stored by the head's splits (all on this XCD) with this launch's tag.
     __shared__ float s_red[4];
-    uint4* s_x = reinterpret_cast<uint4*>(s_v);
-    gemv_x_finish<true>(xin, x, in_w, qi->eps, hidden, s_x, s_red);
-    float acc[RW];
-#pragma unroll
-    for (int r = 0; r < RW; ++r) acc[r] = 0.f;
-#pragma unroll
-    for (int u = 0; u < CPL; ++u) {
-      const uint4 xv = s_x[lane + 64 * u];
-#pragma unroll
-      for (int r = 0; r < RW; ++r) {
-        float d = dot2bf(wv[r][u].x, xv.x, acc[r]);
-        d = dot2bf(wv[r][u].y, xv.y, d);
-        d = dot2bf(wv[r][u].z, xv.z, d);
-        acc[r] = dot2bf(wv[r][u].w, xv.w, d);
-      }
-    }
     next = merge_next((unsigned)__builtin_amdgcn_readfirstlane((int)epv));
-    const unsigned qtag = merge_tag(next, kvh);
-    uint2* items = qi->items + (int64_t)kvh * (G + 2) * 64;
-    uint32_t mine = 0;
-#pragma unroll
-    for (int r = 0; r < RW; r += 2) {
-      const uint32_t pr = f2bf(wave_sum64(acc[r])) | f2bf(wave_sum64(acc[r + 1])) << 16;
-      if (lane == r / 2) mine = pr;
-    }
-    if (lane < RW / 2) items[i0 / 2 + lane] = make_uint2(mine, qtag);
-    SOLORT_STAMP(tid == 0, kvh + nkv * split, 8);
-    const int prow = min(slot, NROWS - 1);
-    const __amdgpu_buffer_rsrc_t rq =
-        __builtin_amdgcn_make_buffer_rsrc(items, (short)0, (G + 2) * 64 * 8, 0x00020000);
-    const int off = (prow * 64 + 4 * j) * 8;
-    uint4 a01 = make_uint4(0u, 0u, 0u, 0u), a23 = a01;
-    bool pend = true;
-    for (int it = 0; it < kMergeSpin && pend; ++it) {
-      asm volatile("" ::: "memory");  // a fresh load every round
-      a01 = ld_l2(rq, off);
-      a23 = ld_l2(rq, off + 16);
-      const bool bad = (a01.y != qtag) | (a01.w != qtag) | (a23.y != qtag) | (a23.w != qtag);
-      pend = __builtin_amdgcn_ballot_w64(bad) != 0;
-    }
-    raw0 = pend ? make_uint4(0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u, 0x7fc07fc0u)  // NaN: gave up
-                : make_uint4(a01.x, a01.z, a23.x, a23.z);
-    pos0 = (int64_t)(((uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)posv.y) << 32) |
-                     (uint64_t)(uint32_t)__builtin_amdgcn_readfirstlane((int)posv.x));
-    SOLORT_STAMP(tid == 0, kvh + nkv * split, 9);
+    raw0 = qkv_handover<G, RW, CPL>(wv, xin, x, in_w, qi->eps, hidden, reinterpret_cast<uint4*>(s_v), s_red,
+                                    qi->items + (int64_t)kvh * (G + 2) * 64, merge_tag(next, kvh), i0,
+                                    min(slot, NROWS - 1), j, lane, kvh + nkv * split);
+    pos0 = pos_from(posv);
   }
 
   // 3. q rows (and, fused, the new tokens' K/V rows) into LDS.
@@ -790,11 +816,15 @@ __device__ __forceinline__ KVTile fetch_tile(const uint16_t* kp, const uint16_t*
 // Grid (nkv, n_split): block (kvh, split), 4 wavefronts.  qsrc: fused, the
 // qkv rows (row stride qsrc_stride); unfused, the q rows [nq][nh][128]
 // (qsrc_stride = nh*128).
-template <int NQ, int G, bool FUSED, bool PAGED>
+template <int NQ, int G, bool FUSED, bool PAGED, int RW = 0, int CPL = 0>
 __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int tok_stride, int head_stride,
                                                  int chunk, int bound, const uint16_t* qsrc, int qsrc_stride,
                                                  int nh, const uint16_t* qn_w, const uint16_t* kn_w,
-                                                 const uint16_t* rope_cs, const DecodeTail& a) {
+                                                 const uint16_t* rope_cs, const DecodeTail& a,
+                                                 const uint16_t* x = nullptr, const uint16_t* wqkv = nullptr,
+                                                 const uint16_t* in_w = nullptr, int hidden = 0,
+                                                 const QkvIn* qi = nullptr) {
+  constexpr bool QKV = RW > 0;  // the qkv rows computed in this launch from x and wqkv (one new token)
   constexpr int R = NQ * G;  // query rows sharing one KV head (<= 32)
   constexpr int NROWS = FUSED ? NQ * (G + 2) : R;
   static_assert(R <= 32, "at most 32 query rows per KV head");
@@ -823,13 +853,18 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
   //    (idle lanes load a valid row they ignore): a load skipped on some path
   //    would make the compiler wait for all of them before the first use.
   constexpr int NPASS = (NROWS + 15) / 16;
+  static_assert(!QKV || (NQ == 1 && FUSED && !PAGED), "the qkv product in the launch serves one new token");
   uint4 raw[NPASS], cr[NPASS], sr[NPASS];
   uint4 wq0 = make_uint4(0u, 0u, 0u, 0u), wk0 = wq0;
+  XChunks xin;  // QKV: this thread's chunks of x and the input norm weight, loaded first
+  if constexpr (QKV) gemv_x_load<true>(x, in_w, hidden, xin);
 #pragma unroll
   for (int ps = 0; ps < NPASS; ++ps) {
     const int row = min(slot + 16 * ps, NROWS - 1);
-    cr[ps] = sr[ps] = make_uint4(0u, 0u, 0u, 0u);
-    if constexpr (FUSED) {
+    cr[ps] = sr[ps] = raw[ps] = make_uint4(0u, 0u, 0u, 0u);
+    if constexpr (QKV) {
+      // loaded behind the weight rows below
+    } else if constexpr (FUSED) {
       const int t = row / (G + 2), c = row % (G + 2);
       const int hs = c < G ? kvh * G + c : (c == G ? nh + kvh : nh + nkv + kvh);
       raw[ps] = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + hs * SOLORT_HD + j * 8);
@@ -840,7 +875,7 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
       raw[ps] = *reinterpret_cast<const uint4*>(qsrc + (int64_t)t * qsrc_stride + (kvh * G + g) * SOLORT_HD + j * 8);
     }
   }
-  if constexpr (FUSED) {
+  if constexpr (FUSED && !QKV) {
     wq0 = *reinterpret_cast<const uint4*>(qn_w + j * 8);
     wk0 = *reinterpret_cast<const uint4*>(kn_w + j * 8);
   }
@@ -857,11 +892,42 @@ __device__ __forceinline__ void decode_mfma_body(uint16_t* kc, uint16_t* vc, int
   const int lrow = lane >> 4;  // this lane's first row of the tile; rows lrow + 4i
   KVTile kv = fetch_tile<PAGED, NQ == 1>(kp, vp, tok_stride, kbeg + kTile * wave, kbeg, kstat, kclamp, lrow, a);
 
-  const int64_t pos0 = a.pos0_dev[0];
-  // The KV head's merge counter, read ahead of the staging barrier (as in the lane kernel: before
-  // any partial of the block is stored, and off the path to the partial stores).
-  const unsigned next = a.merge ? merge_next(a.epochs[kvh * 32]) : 0u;
+  // QKV: this wave's weight rows, then the prologue's own inputs (as in the lane kernel).
+  constexpr int QRW = QKV ? RW : 1, QCPL = QKV ? CPL : 1;
+  uint4 wv[QRW][QCPL];
+  const int i0 = (split * 4 + wave) * RW;
+  if constexpr (QKV) {
+    qkv_issue<G, RW, CPL>(wv, wqkv, hidden, i0, kvh, nh, nkv, lane);
+    cr[0] = *reinterpret_cast<const uint4*>(rope_cs + (j & 7) * 8);
+    sr[0] = *reinterpret_cast<const uint4*>(rope_cs + 64 + (j & 7) * 8);
+    wq0 = *reinterpret_cast<const uint4*>(qn_w + j * 8);
+    wk0 = *reinterpret_cast<const uint4*>(kn_w + j * 8);
+  }
+  int64_t pos0;
+  unsigned next;
+  uint2 posv = make_uint2(0u, 0u);
+  unsigned epv = 0u;
+  if constexpr (QKV) {  // vector loads, first used after the product (see the lane kernel)
+    posv = ld_vec8(a.pos0_dev);
+    epv = ld_vec4(a.epochs + kvh * 32);
+    pos0 = 0;
+    next = 0u;
+  } else {
+    pos0 = a.pos0_dev[0];
+    // The KV head's merge counter, read ahead of the staging barrier (as in the lane kernel: before
+    // any partial of the block is stored, and off the path to the partial stores).
+    next = a.merge ? merge_next(a.epochs[kvh * 32]) : 0u;
+  }
   SOLORT_STAMP(tid == 0, kvh + nkv * split, 1);
+  if constexpr (QKV) {
+    // x staged past the q tile (the K/V tiles use this region only after the q barriers)
+    __shared__ float s_red[4];
+    next = merge_next((unsigned)__builtin_amdgcn_readfirstlane((int)epv));
+    raw[0] = qkv_handover<G, RW, CPL>(wv, xin, x, in_w, qi->eps, hidden, reinterpret_cast<uint4*>(s_x + 16384), s_red,
+                                      qi->items + (int64_t)kvh * (G + 2) * 64, merge_tag(next, kvh), i0,
+                                      min(slot, NROWS - 1), j, lane, kStampBlocks);
+    pos0 = pos_from(posv);
+  }
 
   // 3. q rows (and, fused, the new tokens' K/V rows) into LDS; rows R..31 of
   //    the q tile are zero.  Fused: every pass's row is normalised first,
@@ -1161,6 +1227,20 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_packed_kernel(uint16_t* kc
   const int chunk = ((int)(geom & 31u) + 1) * 32, nh = (int)((geom >> 5) & 2047u), bound = (int)(geom >> 16);
   decode_mfma_body<NQ, G, true, false>(kc, vc, tok_stride, head_stride, chunk, bound, qkv,
                                        (nh + 2 * (nh / G)) * SOLORT_HD, nh, qn_w, kn_w, rope_cs, a);
+}
+
+// One new token, fused with the qkv product (see decode_qkv_lanes_kernel), for
+// key chunks of 128 to 1024 keys; strides8 and geom as for the packed MFMA
+// kernel.  One block per CU: the weight rows in flight need the registers.
+template <int G, int RW, int CPL>
+__global__ __launch_bounds__(256, 1) void decode_qkv_mfma_kernel(uint16_t* kc, uint16_t* vc, unsigned strides8,
+                                                                 unsigned geom, const uint16_t* x,
+                                                                 const uint16_t* wqkv, const uint16_t* in_w,
+                                                                 const DecodeTail a, const QkvIn q) {
+  const int tok_stride = (int)(strides8 & 0xffffu) * 8, head_stride = (int)(strides8 >> 16) * 8;
+  const int chunk = ((int)(geom & 31u) + 1) * 32, nh = (int)((geom >> 5) & 2047u), bound = (int)(geom >> 16);
+  decode_mfma_body<1, G, true, false, RW, CPL>(kc, vc, tok_stride, head_stride, chunk, bound, nullptr, 0, nh, q.qn_w,
+                                               a.kn_w, a.rope_cs, a, x, wqkv, in_w, CPL * 512, &q);
 }
 
 // The combine kernel (two-launch mode): the log-sum-exp combine of the
@@ -1518,13 +1598,38 @@ static void launch_qkv_u(const DecodeArgs& a, unsigned strides8, unsigned geom, 
                        (const uint16_t*)x, (const uint16_t*)wqkv, (const uint16_t*)in_w, a.tail, q);
 }
 
+template <int G, int RW, int CPL>
+static void launch_qkv_mfma(const DecodeArgs& a, unsigned strides8, const void* x, const void* wqkv, const void* in_w,
+                            const QkvIn& q, hipStream_t s) {
+  const unsigned geom = (unsigned)(a.chunk / 32 - 1) | (unsigned)a.nh << 5 | (unsigned)a.bound << 16;
+  hipLaunchKernelGGL((decode_qkv_mfma_kernel<G, RW, CPL>), a.grid(), dim3(256), 0, s, a.kc, a.vc, strides8, geom,
+                     (const uint16_t*)x, (const uint16_t*)wqkv, (const uint16_t*)in_w, a.tail, q);
+}
+
 static bool launch_qkv(const DecodeArgs& a, int hidden, const void* x, const void* wqkv, const void* in_w,
                        const QkvIn& q, hipStream_t s) {
   const int G = a.nh / a.nkv;
-  if (!a.lanes || a.n_split != kQkvSplits || !a.tail.merge || a.tok_stride >= (1 << 19) ||
-      a.head_stride >= (1 << 19) || a.nh >= 2048 || a.bound >= (1 << 19))
+  if (a.n_split != kQkvSplits || !a.tail.merge || a.tok_stride >= (1 << 19) || a.head_stride >= (1 << 19) ||
+      a.nh >= 2048 || a.bound >= (1 << 19))
     return false;
   const unsigned strides8 = (unsigned)(a.tok_stride / 8) | (unsigned)(a.head_stride / 8) << 16;
+  if (!a.lanes) {
+    // MFMA split kernel, 128-key chunks.  Its geometry holds chunks up to 1024 keys, but from 256 on
+    // the two launches were as fast or faster (Qwen3-4B, us per layer: KV 4096 17.19 against 17.30,
+    // KV 8192 20.62 against 20.25): a wavefront holds one key tile before the product, and the
+    // chunk's later tiles are loaded after the handover.
+    if (a.chunk > 128 || a.bound >= (1 << 16)) return false;
+    if (G == 2 && hidden == 1024) {
+      launch_qkv_mfma<2, 4, 2>(a, strides8, x, wqkv, in_w, q, s);
+    } else if (G == 4 && hidden == 2560) {
+      launch_qkv_mfma<4, 6, 5>(a, strides8, x, wqkv, in_w, q, s);
+    } else if (G == 4 && hidden == 4096) {
+      launch_qkv_mfma<4, 6, 8>(a, strides8, x, wqkv, in_w, q, s);
+    } else {
+      return false;
+    }
+    return true;
+  }
   const unsigned geom = (unsigned)(a.chunk / 16 - 1) | (unsigned)a.nh << 2 | (unsigned)a.bound << 13;
   if (G == 2 && hidden == 1024) {
     launch_qkv_u<2, 4, 2>(a, strides8, geom, x, wqkv, in_w, q, s);

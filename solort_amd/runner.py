@@ -63,11 +63,12 @@ def decode_splits(bound: int, nkv: int) -> int:
 def decode_qkv_splits(bound: int, nkv: int) -> int:
     """Key splits per KV head for solort_decode_qkv_layer, which runs the QKV product inside the
     attention launch at 256 // nkv splits (one workgroup per CU for 8 KV heads) with chunks of 16 to
-    64 keys: that count from 512 keys on (at 512 keys, 32 splits of 16 keys against the attention's
+    128 keys: that count from 512 keys on (at 512 keys, 32 splits of 16 keys against the attention's
     own 16 of 32: 4.94 against 4.90 us per attention call, while the fused launch saves ~1.3 us of
-    the product's own), decode_splits elsewhere."""
+    the product's own; from 1024 keys on decode_splits routes 32 as well), decode_splits elsewhere
+    (up to 32768 keys also 32 splits, which the entry point runs as two launches)."""
     n = max(1, 256 // max(1, nkv))
-    return n if 512 <= bound and 16 <= bound // n <= 64 else decode_splits(bound, nkv)
+    return n if 512 <= bound and 16 <= bound // n <= 128 else decode_splits(bound, nkv)
 
 
 def verify_splits(bound: int, nkv: int = 8) -> int:

@@ -66,7 +66,7 @@ def test_decode_graph_replays_equal_eager_steps(gpu):
     _say(f"  tokens {toks}")
 
 
-@pytest.mark.parametrize("p0", [400, 1000, 1500], ids=["bucket512", "bucket1024", "bucket2048"])
+@pytest.mark.parametrize("p0", [400, 1000, 1500, 3000], ids=["bucket512", "bucket1024", "bucket2048", "bucket4096"])
 def test_qkv_in_attention_launch_equals_own_launch(gpu, p0):
     """The Qwen3-4B layer shapes (hidden 2560, 32 q / 8 kv heads, 2 layers) in the buckets where the
     QKV product runs inside the attention launch: the same tokens as the step with the product as
@@ -74,8 +74,8 @@ def test_qkv_in_attention_launch_equals_own_launch(gpu, p0):
     (at 512 keys the fused launch runs 32 splits of 16 keys, the attention on its own 16 of 32, so
     the merge adds the partials in another order)."""
     n = 6
-    w, m = _model(gpu, p0, QWEN3_4B_2L, max_len=2048)
-    u = GraphQwen3Decode(w, 2048, fused_qkv=False)
+    w, m = _model(gpu, p0, QWEN3_4B_2L, max_len=4096)
+    u = GraphQwen3Decode(w, 4096, fused_qkv=False)
     u.kc.copy_(m.kc)
     u.vc.copy_(m.vc)
     toks = m.generate(5, p0, n)

@@ -31,6 +31,10 @@ CASES = [
     ("0.6B KV 1024", 16, 8, 1024, 1024, 1024, 700, 32),
     ("8B KV 1024", 32, 8, 4096, 1024, 1024, 1000, 32),
     ("4B KV 512, 16-key splits", 32, 8, 2560, 512, 512, 300, 32),
+    ("4B KV 4096, 128-key splits (MFMA kernel)", 32, 8, 2560, 4096, 4096, 4000, 32),
+    ("4B KV 8192, early position (256-key splits: two launches)", 32, 8, 2560, 8192, 8192, 100, 32),
+    ("0.6B KV 4096 (MFMA kernel)", 16, 8, 1024, 4096, 4096, 3000, 32),
+    ("8B KV 32768, 1024-key splits (two launches)", 32, 8, 4096, 32768, 32768, 32767, 32),
     ("4B KV 512, 16 splits (two launches)", 32, 8, 2560, 512, 512, 300, 16),
     ("hidden 2048 (two launches)", 32, 8, 2048, 1024, 1024, 800, 32),
 ]

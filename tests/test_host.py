@@ -16,9 +16,9 @@ def test_decode_splits_heuristic():
 
 
 def test_decode_qkv_splits_heuristic():
-    for bound in (512, 1024, 2048):  # chunks of 16, 32, 64 keys: the fused QKV launch
+    for bound in (512, 1024, 2048, 4096):  # chunks of 16 to 128 keys: the fused QKV launch
         assert decode_qkv_splits(bound, 8) == 32
-    for bound in (128, 256, 4096, 32768):  # elsewhere the attention's own routing
+    for bound in (128, 256, 8192, 32768, 65536):  # elsewhere the attention's own routing
         assert decode_qkv_splits(bound, 8) == decode_splits(bound, 8)
 
 
