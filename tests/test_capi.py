@@ -74,6 +74,39 @@ def test_decode_rejects_bad_arguments_without_launching(lib):
     assert call(dt=7) == EINVAL
 
 
+def test_decode_qkv_layer_workspace_and_rejections(lib):
+    # The attention's partials and counters, then per KV head (G + 2) rows of 128 handed-over
+    # outputs as 8-byte (two bf16, tag) items.
+    n = lib.solort_decode_qkv_workspace_bytes(32, 8, 32)
+    assert n >= lib.solort_attn_workspace_bytes(1, 32, 8, 128, 32) + 8 * 6 * 64 * 8
+    assert n % 256 == 0
+    assert lib.solort_decode_qkv_workspace_bytes(30, 8, 32) == 0
+    assert lib.solort_decode_qkv_workspace_bytes(32, 8, 0) == 0
+
+    p = ctypes.c_void_p(16 * 1024)  # never dereferenced: validation fails first
+    args = dict(x=p, hidden=2560, in_w=p, wqkv=p, wstride=2560, nh=32, nkv=8, hd=128, qn=p, kn=p, cs=p, pos=p,
+                k=p, v=p, ts=1024, hs=128, max_len=1024, bound=1024, ws=p, n_split=32, qkv_out=p, out=p, dt=0)
+
+    def call(**kw):
+        a = {**args, **kw}
+        return lib.solort_decode_qkv_layer(a["x"], a["hidden"], a["in_w"], 1e-6, a["wqkv"], a["wstride"], a["nh"],
+                                           a["nkv"], a["hd"], a["qn"], a["kn"], 1e-6, a["cs"], a["pos"], a["k"],
+                                           a["v"], a["ts"], a["hs"], a["max_len"], a["bound"], 0.088, a["ws"],
+                                           a["n_split"], a["qkv_out"], a["out"], a["dt"], None)
+
+    assert call(hd=64) == EINVAL and "head_dim" in _err(lib)
+    assert call(bound=2048) == EINVAL and "bound" in _err(lib)
+    assert call(pos=None) == EINVAL
+    assert call(x=None) == EINVAL and "null" in _err(lib)
+    assert call(wqkv=None) == EINVAL and "null" in _err(lib)
+    assert call(qkv_out=None) == EINVAL and "null" in _err(lib)
+    assert call(x=ctypes.c_void_p(16 * 1024 + 2)) == EINVAL and "aligned" in _err(lib)
+    assert call(in_w=ctypes.c_void_p(16 * 1024 + 8)) == EINVAL and "aligned" in _err(lib)
+    assert call(hidden=2564) == EINVAL and "hidden" in _err(lib)
+    assert call(hidden=0) == EINVAL and "hidden" in _err(lib)
+    assert call(wstride=2552) == EINVAL and "wqkv_row_stride" in _err(lib)
+
+
 def test_prologue_and_argmax_reject_bad_arguments(lib):
     p = ctypes.c_void_p(4096)
     rc = lib.solort_qknorm_rope_kvwrite(p, 6144, 1, 32, 8, 100, p, p, 1e-6, p, None, p, p, p, 1024, 128, 1024,
