@@ -431,12 +431,13 @@ def stamp_extras(torch, ops, wl, runners, dev, sh, bound) -> dict:
     """In-kernel phase timelines from the tracing build (include/solort_trace.h): the last
     solort_decode_layer launch of a replayed Qwen3-4B decode step at KV 1024, the last call of a
     graph of 8 Qwen3-8B calls at KV 32768 (32 splits), the last of 4 verify calls (5 tokens at 2048,
-    the 17 splits that hold keys), the last prefill_kernel launch of a graph at T = 1024 and the last
-    decode_qkv_lanes_kernel launch (qkv product in the decode launch) of a 36-layer graph at KV 1024."""
+    the 17 of its 20 splits that hold keys), the last prefill_kernel launch of a graph at T = 1024
+    and the last decode_qkv_lanes_kernel launch (qkv product in the decode launch) of a 36-layer graph
+    at KV 1024."""
     import numpy as np
 
     from solort_amd import _lib
-    from solort_amd.runner import decode_splits
+    from solort_amd.runner import DECODE_BUCKETS, decode_splits, verify_bound, verify_splits
 
     lib = _lib.load()
     res = {"clock": "s_memrealtime, 100 MHz; microseconds after the launch's first workgroup started"}
@@ -480,25 +481,27 @@ def stamp_extras(torch, ops, wl, runners, dev, sh, bound) -> dict:
     res["decode_qwen3_8b_kv32768"].update(_wave_stamps(np, st, heads))
     del kcs, vcs
     torch.cuda.empty_cache()
-    # speculative verify, 5 tokens at 2048 over a max-4096 cache (32 splits, the combine in a second
-    # launch): the split kernel's phases
+    # speculative verify, 5 tokens at 2048 over a max-4096 cache (the runner's verify bound 2560, 20
+    # splits, the combine in a second launch): the split kernel's phases
     pos0, K1, vb = 2048, 5, 4096
     kc = torch.randn(vb, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16)
     vc = torch.randn(vb, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16)
     qv = torch.randn(K1, sh.qkv_width, generator=gen, device=dev).to(torch.bfloat16)
     pv = torch.tensor([pos0], dtype=torch.long, device=dev)
     csv = ops.rope_rows(runners[0].inv_freq, pv, K1)
-    wsv = ops.attn_workspace(K1, sh.nh, sh.nkv, 32, dev)
+    vbound = verify_bound(pos0 + K1 - 1, sorted({b for b in DECODE_BUCKETS if b < vb} | {vb}))  # 2560
+    nsv = verify_splits(vbound, sh.nkv)  # 20 splits of 128 keys
+    wsv = ops.attn_workspace(K1, sh.nh, sh.nkv, nsv, dev)
     ov = torch.empty(K1, sh.nh * 128, dtype=torch.bfloat16, device=dev)
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph):
         for li in range(4):
-            ops.decode_layer(qv, runners[0].qn_w[li], runners[0].kn_w[li], runners[0].eps, csv, pv, kc, vc, vb,
-                             sh.scale, wsv, 32, ov, sh.nh, sh.nkv)
+            ops.decode_layer(qv, runners[0].qn_w[li], runners[0].kn_w[li], runners[0].eps, csv, pv, kc, vc, vbound,
+                             sh.scale, wsv, nsv, ov, sh.nh, sh.nkv)
     for _ in range(3):
         graph.replay()
     torch.cuda.synchronize()
-    st = read("solort_phase_stamps_decode", sh.nkv * 32)
+    st = read("solort_phase_stamps_decode", sh.nkv * nsv)
     live = [kvh + sh.nkv * sp for sp in range(17) for kvh in range(sh.nkv)]  # splits holding keys 0..2052
     res["verify_qwen3_4b_5_tokens"] = _stamp_summary(np, st[live], STAMP_PHASES_DECODE)
     del kc, vc
@@ -1000,17 +1003,21 @@ def mid_decode_extras(torch, ops, wl, dev, n_caches: int = 8) -> dict:
 
 
 def verify_extras(torch, ops, wl, runners, dev, sh) -> dict:
-    """Speculative verify, Qwen3-4B shape: 5 queries at 2048..2052 over the cache (bucket 4096, the
-    runner's routing), one solort_decode_layer call per layer of every KV set; then the greedy argmax
-    of [5, 151936] bf16 logits.  Uses fresh max-4096 caches (8 sets x 36 layers rotated)."""
-    from solort_amd.runner import verify_splits
+    """Speculative verify, Qwen3-4B shape: 5 queries at 2048..2052 over the cache (the runner's
+    routing: bucket 4096, its verify bound 2560 and split count; also the whole bucket at 32
+    splits), one solort_decode_layer call per layer of every KV set; then the greedy argmax of
+    [5, 151936] bf16 logits.  Uses fresh max-4096 caches (8 sets x 36 layers rotated)."""
+    from solort_amd.runner import DECODE_BUCKETS, verify_bound, verify_splits
 
-    pos0, K1, bound = 2048, 5, 4096
+    pos0, K1, max_len = 2048, 5, 4096
+    buckets = sorted({b for b in DECODE_BUCKETS if b < max_len} | {max_len})
+    bucket = next(b for b in buckets if b > pos0 + K1 - 1)
+    bound = verify_bound(pos0 + K1 - 1, buckets)
     gen = torch.Generator(device=dev).manual_seed(1004)
     sets = []
     for _ in range(len(runners)):
-        kc = torch.randn(sh.layers, bound, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16)
-        vc = torch.randn(sh.layers, bound, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16)
+        kc = torch.randn(sh.layers, max_len, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16)
+        vc = torch.randn(sh.layers, max_len, sh.nkv, 128, generator=gen, device=dev).to(torch.bfloat16)
         sets.append((kc, vc))
     qkv = torch.randn(sh.layers, K1, sh.qkv_width, generator=gen, device=dev).to(torch.bfloat16)
     posb = torch.tensor([pos0], dtype=torch.long, device=dev)
@@ -1020,22 +1027,24 @@ def verify_extras(torch, ops, wl, runners, dev, sh) -> dict:
     out = torch.empty(K1, sh.nh * 128, dtype=torch.bfloat16, device=dev)
     vbytes = 2 * sh.nkv * (pos0 + K1) * 128 * 2 + K1 * 2 * sh.nh * 128 * 2
 
-    def time_splits(n):
+    def time_splits(n, bnd=bound):
         ws = ops.attn_workspace(K1, sh.nh, sh.nkv, n, dev)
         calls = [(lambda kc=kc, vc=vc, li=li: ops.decode_layer(qkv[li], r0.qn_w[li], r0.kn_w[li], r0.eps, cs, posb,
-                                                               kc[li], vc[li], bound, sh.scale, ws, n, out, sh.nh,
+                                                               kc[li], vc[li], bnd, sh.scale, ws, n, out, sh.nh,
                                                                sh.nkv))
                  for kc, vc in sets for li in range(sh.layers)]
         return _graph_us(torch, dev, calls, reps=3)
 
     us = time_splits(ns)
-    sweep = {str(n): round(time_splits(n), 3) for n in (16, 32, 64, 128)}
+    sweep = {str(n): round(time_splits(n), 3) for n in (10, 16, 20, 32, 40)}
+    bucket_us = time_splits(verify_splits(bucket, sh.nkv), bucket)
     gbs = vbytes / (us * 1e-6) / 1e9
     del sets
     torch.cuda.empty_cache()
     res = {"verify": {"us_per_layer_call": round(us, 3), "gbps": round(gbs, 1),
-                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "n_split": ns, "bucket": bound,
-                      "algorithmic_bytes": vbytes, "n_split_sweep": sweep}}
+                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "n_split": ns, "bucket": bucket, "bound": bound,
+                      "algorithmic_bytes": vbytes, "n_split_sweep": sweep,
+                      "whole_bucket": {"us": round(bucket_us, 3), "n_split": verify_splits(bucket, sh.nkv)}}}
     g2 = torch.Generator().manual_seed(1004)
     logits = [wl.planted_logits(g2, K1, wl.VOCAB).to(dev) for _ in range(2)]
     logits += [torch.randn(K1, wl.VOCAB, generator=gen, device=dev).to(torch.bfloat16) for _ in range(6)]

@@ -25,7 +25,7 @@ import torch.nn.functional as F
 
 from . import ops
 from .runner import (DECODE_BUCKETS, FUSED_PREFILL_MIN, HD, PREFILL_BUCKETS, decode_qkv_splits, decode_splits,
-                     verify_splits)
+                     verify_bound, verify_splits)
 
 
 @dataclass(frozen=True)
@@ -300,12 +300,12 @@ class GraphQwen3Decode:
         return logits
 
     def verify(self, pos0: int) -> torch.Tensor:
-        """Replays the verify graph of the bucket holding positions pos0..pos0+k1-1 over the tokens
-        already in vtok; tok_ver then holds the k1 argmax tokens and acc_ver [a, tg[a]].  Returns the
-        logits [k1, V] (the graph's buffer)."""
+        """Replays the verify graph of the bound holding positions pos0..pos0+k1-1 (verify_bound)
+        over the tokens already in vtok; tok_ver then holds the k1 argmax tokens and acc_ver
+        [a, tg[a]].  Returns the logits [k1, V] (the graph's buffer)."""
         if not 0 <= pos0 <= self.max_len - self.k1:
             raise RuntimeError(f"verify positions {pos0}..{pos0 + self.k1 - 1} exceed max_len {self.max_len}")
-        bound = self.bucket_for(pos0 + self.k1 - 1)
+        bound = verify_bound(pos0 + self.k1 - 1, self.buckets)
         self.vpos0.fill_(int(pos0))
         if bound not in self._ver_graphs:
             self._verify_forward(bound)  # eager once: the GEMM library initialises outside the capture

@@ -71,6 +71,21 @@ def decode_qkv_splits(bound: int, nkv: int) -> int:
     return n if 512 <= bound and 16 <= bound // n <= 128 else decode_splits(bound, nkv)
 
 
+def verify_bound(last_pos: int, buckets) -> int:
+    """Keys a K+1-token verify step scans, its last position last_pos: the decode bucket holding it
+    (the first above it, as for decode), cut at the next multiple of max(128, bucket // 8) past it,
+    so at most an eighth of the scanned keys lie past the live length (a verify graph per bound, at
+    most eight per bucket).  The reference's verify scans all max_len keys under a mask
+    (cuda_graph_executor.py:245-263).  Measured on MI355X, Qwen3-4B shape, 5 tokens at 2048..2052,
+    128-key splits (us per call, the same outputs): bound 4096 (the bucket, 32 splits, 15 without
+    a live key) 10.24, 3072 (24 splits) 10.00, 2560 (20) 9.84, 2176 (17) 9.78."""
+    for b in buckets:
+        if b > last_pos:
+            g = max(128, b // 8)
+            return min(b, (last_pos // g + 1) * g)
+    raise RuntimeError(f"verify position {last_pos} exceeds the last bucket {max(buckets)}")
+
+
 def verify_splits(bound: int, nkv: int = 8) -> int:
     """Key splits per KV head for a K+1-token verify bucket.  Up to 4096 keys: 128 keys per split
     (one key tile per wavefront), at most 64 splits; longer buckets: 256 // nkv splits (one
@@ -245,7 +260,7 @@ class GraphQwen3Attention:
         """
         if not 0 <= pos_start <= self.max_len - self.k1:
             raise RuntimeError(f"verify positions {pos_start}..{pos_start + self.k1 - 1} exceed max_len")
-        bound = self._bucket_for(pos_start + self.k1 - 1)
+        bound = verify_bound(pos_start + self.k1 - 1, self.buckets)
         if bound not in self._ver_graphs:
             graph = torch.cuda.CUDAGraph()
             with torch.cuda.graph(graph):

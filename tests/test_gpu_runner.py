@@ -11,7 +11,7 @@ import torch
 from oracle import ref
 from solort_amd import ops
 from solort_amd import workloads as wl
-from solort_amd.runner import GraphQwen3Attention, verify_splits
+from solort_amd.runner import GraphQwen3Attention, verify_bound, verify_splits
 
 pytestmark = pytest.mark.gpu
 HD = 128
@@ -93,7 +93,7 @@ def test_verify_graph_replays_match_eager(gpu):
     eager_kc, eager_vc = r.kc.clone(), r.vc.clone()
     q = torch.empty(5, sh.nh, HD, dtype=torch.bfloat16, device=gpu)
     for rep, pos0 in enumerate((2048, 17, 4091, 2048, 100)):
-        bound = r._bucket_for(pos0 + 4)
+        bound = verify_bound(pos0 + 4, r.buckets)  # 2560, 128, 4096, 2560, 128
         ns = verify_splits(bound, sh.nkv)
         ws = ops.attn_workspace(5, sh.nh, sh.nkv, ns, gpu)
         _say(f"[verify replay pos0={pos0} bound={bound}]")
@@ -116,7 +116,7 @@ def test_verify_graph_replays_match_eager(gpu):
         # in-graph acceptance (cuda_graph_executor.py:476): the planted mismatch, or all four
         assert tuple(r.acc_ver.cpu().tolist()) == ref.accept_prefix(logits.argmax(-1), draft)
         assert r.acc_ver[0].item() == (rep if rep < 4 else 4)
-    assert sorted(r._ver_graphs) == [128, 4096]
+    assert sorted(r._ver_graphs) == [128, 2560, 4096]
 
 
 def test_prefill_graph_then_decode_continues(gpu):

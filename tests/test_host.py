@@ -1,5 +1,8 @@
 """Host-side logic of the runner that needs no GPU."""
-from solort_amd.runner import DECODE_BUCKETS, PREFILL_BUCKETS, decode_qkv_splits, decode_splits, verify_splits
+import pytest
+
+from solort_amd.runner import (DECODE_BUCKETS, PREFILL_BUCKETS, decode_qkv_splits, decode_splits, verify_bound,
+                               verify_splits)
 
 
 def test_decode_splits_heuristic():
@@ -20,6 +23,25 @@ def test_decode_qkv_splits_heuristic():
         assert decode_qkv_splits(bound, 8) == 32
     for bound in (128, 256, 8192, 32768, 65536):  # elsewhere the attention's own routing
         assert decode_qkv_splits(bound, 8) == decode_splits(bound, 8)
+
+
+def test_verify_bound():
+    buckets = [128, 256, 512, 1024, 2048, 4096]
+    # the decode bucket holding the last position, cut at the next multiple of max(128, bucket / 8)
+    assert verify_bound(2052, buckets) == 2560  # 5 tokens at 2048: bucket 4096 in steps of 512
+    assert verify_bound(2047, buckets) == 2048 and verify_bound(2048, buckets) == 2560
+    assert verify_bound(4095, buckets) == 4096 and verify_bound(3584, buckets) == 4096
+    assert verify_bound(1100, buckets) == 1280  # bucket 2048 in steps of 256
+    assert verify_bound(0, buckets) == 128 and verify_bound(127, buckets) == 128 and verify_bound(128, buckets) == 256
+    odd = [128, 256, 512, 1024, 2048, 3000]  # a max_len that is not a power of two
+    assert verify_bound(2500, odd) == 2625 and verify_bound(2999, odd) == 3000
+    for b in buckets:  # every bound holds the last position, within its bucket, at most 8 per bucket
+        lo = max([x for x in buckets if x < b], default=-1)
+        bounds = {verify_bound(p, buckets) for p in range(lo + 1, b)}
+        assert len(bounds) <= 8 and max(bounds) == b
+        assert all(p < verify_bound(p, buckets) <= b for p in range(lo + 1, b))
+    with pytest.raises(RuntimeError):
+        verify_bound(4096, buckets)
 
 
 def test_verify_splits_heuristic():
