@@ -1229,9 +1229,10 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_packed_kernel(uint16_t* kc
                                        (nh + 2 * (nh / G)) * SOLORT_HD, nh, qn_w, kn_w, rope_cs, a);
 }
 
-// One new token, fused with the qkv product (see decode_qkv_lanes_kernel), for
-// key chunks of 128 to 1024 keys; strides8 and geom as for the packed MFMA
-// kernel.  One block per CU: the weight rows in flight need the registers.
+// One new token, fused with the qkv product (see decode_qkv_lanes_kernel); the
+// geometry holds key chunks of 128 to 1024 keys, launch_qkv routes 128-key
+// chunks here; strides8 and geom as for the packed MFMA kernel.  One block per
+// CU: the weight rows in flight need the registers.
 template <int G, int RW, int CPL>
 __global__ __launch_bounds__(256, 1) void decode_qkv_mfma_kernel(uint16_t* kc, uint16_t* vc, unsigned strides8,
                                                                  unsigned geom, const uint16_t* x,
