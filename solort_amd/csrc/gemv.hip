@@ -52,7 +52,8 @@ __global__ __launch_bounds__(256) void gemv_kernel(const uint16_t* __restrict__ 
   extern __shared__ uint4 sx[];  // x as K / 8 chunks of 16 bytes
   __shared__ float s_red[4];
   __shared__ uint64_t s_key[4];
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  // wave is uniform: the row pointers below live in scalar registers.
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int nch = K >> 3;
 
   // This wavefront's R weight rows; lane l streams their 16-byte chunks

@@ -20,10 +20,14 @@ __device__ __forceinline__ float wave_sum64(float v) {
 // workgroup taking part; NORM: bf16(fp32(x) * rsqrt(mean(fp32(x)^2) + eps) *
 // fp32(norm_w)), the sum of squares in fp32 with one block reduction (s_red: 4
 // floats).  In two parts, so that a caller can issue the loads early:
-// gemv_x_load reads this thread's first kXReg chunks of x and norm_w (K <= 8192
+// gemv_x_load reads this thread's first kXReg chunks of x and norm_w (K <= 4096
 // in one round; larger K re-reads the rest in gemv_x_finish), gemv_x_finish
-// normalises and stores them and ends with a workgroup barrier.
-constexpr int kXReg = 4;
+// normalises and stores them and ends with a workgroup barrier.  Two chunks
+// per thread cover K <= 4096 (every hidden size served here); four held 16
+// more VGPRs while the weight rows are in flight (gate_up, 4 rows x 5 chunks
+// per lane: 153 VGPRs then, 120 now with uniform row pointers, four
+// wavefronts per SIMD instead of three; its time did not change).
+constexpr int kXReg = 2;
 struct XChunks {
   uint4 x[kXReg], g[kXReg];
 };
