@@ -216,13 +216,17 @@ def test_argmax_failure_raises_at_the_sync(gpu):
         ops.argmax_mode(1)
 
 
-def test_verify_graph_matches_reference_ops(gpu):
+@pytest.mark.parametrize("p0,max_len,bounds", [(90, 256, [128]), (2040, 4096, [2048, 2560])],
+                         ids=["bucket-128", "bounds-2048-2560"])
+def test_verify_graph_matches_reference_ops(gpu, p0, max_len, bounds):
     """The whole-model verify graph (cuda_graph_executor.py:245-268 with the argmax and acceptance of
     :475-481): its logits against the CPU evaluations in bf16 and fp32 (the decode steps' bar), its
-    argmax tokens the argmax of its logits, and acc_ver the first-mismatch rule applied on the host."""
+    argmax tokens the argmax of its logits, and acc_ver the first-mismatch rule applied on the host.
+    From 2040 the three rounds end at 2044, 2049 and 2054: verify bounds 2048 (bucket 2048) and
+    2560 (bucket 4096 cut at a multiple of 512)."""
     shape = TINY_UNTIED
-    p0 = 90
-    w, m = _model(gpu, p0, shape)
+    _say(f"[verify graph at {p0}, max_len {max_len}]")
+    w, m = _model(gpu, p0, shape, max_len=max_len)
     bf = {k: (v.cpu() if torch.is_tensor(v) else [t.cpu() for t in v]) for k, v in vars(w).items() if k != "shape"}
     f32 = {k: (v.float() if torch.is_tensor(v) else [t.float() for t in v]) for k, v in bf.items()}
     kc, vc = m.kc.cpu(), m.vc.cpu()
@@ -247,6 +251,7 @@ def test_verify_graph_matches_reference_ops(gpu):
     kd = (m.kc[:, : p0 + 3 * m.k1].float().cpu() - kc32[:, : p0 + 3 * m.k1]).abs().max().item()
     kr = (kc[:, : p0 + 3 * m.k1].float() - kc32[:, : p0 + 3 * m.k1]).abs().max().item()
     assert kd <= 2.0 * kr + 2e-3
+    assert sorted(m._ver_graphs) == bounds
 
 
 @pytest.mark.parametrize("draft_seed", [None, 99], ids=["draft-same-weights", "draft-other-weights"])
