@@ -119,6 +119,34 @@ def test_verify_graph_replays_match_eager(gpu):
     assert sorted(r._ver_graphs) == [128, 2560, 4096]
 
 
+def test_verify_bound_changes_no_bit(gpu):
+    """A verify bound below the bucket only drops splits past the live length: with 128-key splits
+    the outputs and cache rows over bounds 2560 (the routed one at 2048..2052), 3072 and 4096 are
+    bit-identical (an empty split's partial folds in as an exact zero)."""
+    r, g, sh = _make(gpu, layers=1, max_len=4096)
+    pos0, k1 = 2048, 5
+    assert verify_bound(pos0 + k1 - 1, r.buckets) == 2560
+    qkv = torch.randn(k1, r.width, generator=g).to(torch.bfloat16).to(gpu)
+    p = torch.tensor([pos0], dtype=torch.long, device=gpu)
+    cs = ops.rope_rows(r.inv_freq, p, k1)
+    outs = []
+    for bound in (2560, 3072, 4096):
+        _say(f"[verify bound {bound}]")
+        ns = verify_splits(bound, sh.nkv)
+        assert bound // ns == 128
+        kc, vc = r.kc[0].clone(), r.vc[0].clone()
+        ws = ops.attn_workspace(k1, sh.nh, sh.nkv, ns, gpu)
+        out = torch.empty(k1, sh.nh * HD, dtype=torch.float32, device=gpu)
+        ops.decode_layer(qkv, r.qn_w[0], r.kn_w[0], r.eps, cs, p, kc, vc, bound, r.scale, ws, ns, out,
+                         sh.nh, sh.nkv)
+        torch.cuda.synchronize()
+        assert torch.isfinite(out).all()
+        outs.append((out, kc, vc))
+    for out, kc, vc in outs[1:]:
+        assert torch.equal(out, outs[0][0])
+        assert torch.equal(kc, outs[0][1]) and torch.equal(vc, outs[0][2])
+
+
 def test_prefill_graph_then_decode_continues(gpu):
     """Graphed bucketed prefill of a 300-row prompt equals eager launches; a decode step at position 300
     then attends the prefilled rows exactly like decode over an eagerly written cache."""
