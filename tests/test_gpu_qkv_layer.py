@@ -74,6 +74,42 @@ def test_qkv_layer_equals_product_then_layer(gpu, case):
         assert torch.equal(kc2, kc) and torch.equal(vc2, vc), (name, call)
 
 
+def test_qkv_layer_strided_weight_rows(gpu):
+    """wqkv rows padded past hidden (row stride hidden + 64): the entry point takes the two-launch
+    path, with the same output and cache bits as the product followed by the attention block."""
+    nh, nkv, hidden, bound, pos = 32, 8, 2560, 1024, 1000
+    _say("[qkv layer: padded weight rows]")
+    g = torch.Generator().manual_seed(91)
+    width = (nh + 2 * nkv) * HD
+    wfull = (torch.randn(width, hidden + 64, generator=g) * hidden ** -0.5).to(torch.bfloat16).to(gpu)
+    wqkv = wfull[:, :hidden]
+    assert wqkv.stride(0) == hidden + 64
+    in_w = (1.0 + 0.1 * torch.randn(hidden, generator=g)).to(torch.bfloat16).to(gpu)
+    qn_w = (1.0 + 0.1 * torch.randn(HD, generator=g)).to(torch.bfloat16).to(gpu)
+    kn_w = (1.0 + 0.1 * torch.randn(HD, generator=g)).to(torch.bfloat16).to(gpu)
+    kc = torch.randn(bound, nkv, HD, generator=g).to(torch.bfloat16).to(gpu)
+    vc = torch.randn(bound, nkv, HD, generator=g).to(torch.bfloat16).to(gpu)
+    kc2, vc2 = kc.clone(), vc.clone()
+    posb = torch.tensor([pos], dtype=torch.long, device=gpu)
+    cs = ops.rope_rows(ops.inv_freq(HD, wl.THETA, gpu), posb, 1)
+    ws = ops.decode_qkv_workspace(nh, nkv, 32, gpu)
+    ws_ref = ops.attn_workspace(1, nh, nkv, 32, gpu)
+    qkv = torch.empty(1, width, dtype=torch.bfloat16, device=gpu)
+    scratch = torch.empty(width, dtype=torch.bfloat16, device=gpu)
+    for call in range(3):
+        x = torch.randn(hidden, generator=g).to(torch.bfloat16).to(gpu)
+        want = torch.empty(1, nh * HD, dtype=torch.bfloat16, device=gpu)
+        got = torch.empty_like(want)
+        ops.gemv(wqkv, x, qkv.view(-1), in_w, wl.EPS)
+        ops.decode_layer(qkv, qn_w, kn_w, wl.EPS, cs, posb, kc, vc, bound, HD ** -0.5, ws_ref, 32, want, nh, nkv)
+        ops.decode_qkv_layer(x, in_w, wl.EPS, wqkv, qn_w, kn_w, wl.EPS, cs, posb, kc2, vc2, bound, HD ** -0.5, ws,
+                             32, scratch, got, nh, nkv)
+        torch.cuda.synchronize()
+        assert torch.equal(got, want), call
+        assert torch.equal(kc2, kc) and torch.equal(vc2, vc), call
+        assert torch.equal(scratch, qkv.view(-1)), call  # the product went through qkv_out
+
+
 def test_qkv_layer_graph_replays(gpu):
     """A graph of 36 calls over distinct layer caches and weights, replayed several times with eager
     work between the replays, against the two-launch path."""
