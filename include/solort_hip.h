@@ -317,7 +317,7 @@ int solort_paged_kv_gather(const void* k_pages, const void* v_pages, int64_t pag
  * positions 0..T-1, with K/V read from cache rows 0..T-1 (written first by
  * solort_qknorm_rope_kvwrite, as the reference writes them at :122-123).
  * q   [T, nh, 128] bf16; out [T, nh * 128] bf16 or fp32.  T <= max_len.
- * Query groups g = nh / nkv of 1, 2 or 4.  Accumulation and softmax are
+ * Query groups g = nh / nkv of 1, 2, 4 or 8.  Accumulation and softmax are
  * fp32; with a bf16 output the probabilities enter the second matrix product
  * rounded to bf16, with an fp32 output as bf16 high + low parts (~16 bits),
  * which keeps it within 1e-4 of exact attention over the same bf16 q/K/V.

@@ -8,7 +8,7 @@
 // the query heads of a KV head share every K/V tile staged in LDS.
 //
 // Block = 4 wavefronts = one KV head x 64 query rows: 16 positions x 4 query
-// heads at g = 4 (32 x 2 at g = 2, 64 positions at g = 1); block row R is
+// heads at g = 4 (8 x 8 at g = 8, 32 x 2 at g = 2, 64 positions at g = 1); block row R is
 // query head kvh*g + R / PB at position p0 + R % PB (PB = 64 / g positions).
 // Wave w = (row group rg = w % 2, key half kh = w / 2) owns rows 32 rg ..
 // 32 rg + 31.  Each iteration stages 64 keys of K and V, both row-major, in
@@ -143,7 +143,7 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(
   const int p0 = tile * PB;
   const int qrow = p0 + (32 * rg + l32) % PB;                // the query row of this lane's scores
   const int pw = p0 + (G == 1 ? 32 * rg : 0);                // this wave's first position
-  const int kend_w = min(T, pw + (G == 4 ? 16 : 32));        // keys this wave attends (wave-uniform)
+  const int kend_w = min(T, pw + (PB < 32 ? PB : 32));       // keys this wave attends (wave-uniform)
 
   // The block's 64 Q rows, loaded coalesced: thread t takes rows t / 16 + 16 i, bytes
   // 16 (t % 16) .. +15 (positions past T repeat row T-1).  They pass through the second K buffer.
@@ -155,15 +155,15 @@ __global__ __launch_bounds__(kThreads, 2) void prefill_kernel(
     qv[i] = *reinterpret_cast<const uint4*>(q + (int64_t)pos * q_stride + (kvh * G + R / PB) * SOLORT_HD +
                                            8 * (tid & 15));
   }
-  // FUSED: this lane's weights and cos/sin values of the q rows it stages (4 / G distinct
-  // positions: row i at position offset (t / 16 + 16 i) % PB, i.e. group i % (4 / G)).
-  constexpr int NP = FUSED ? 4 / G : 1;
+  // FUSED: this lane's weights and cos/sin values of the q rows it stages (row i at position
+  // offset (t / 16 + 16 i) % PB: 4 / G distinct positions, group i % NP; one from G = 4 on).
+  constexpr int NP = FUSED && G < 4 ? 4 / G : 1;
   uint4 wq{}, cs4[NP], sn4[NP];
   if constexpr (FUSED) {
     wq = *reinterpret_cast<const uint4*>(qn_w + 8 * (tid & 15));
 #pragma unroll
     for (int pp = 0; pp < NP; ++pp) {
-      const int pos = min(p0 + (tid >> 4) + 16 * pp, T - 1);
+      const int pos = min(p0 + ((tid >> 4) + 16 * pp) % PB, T - 1);
       cs4[pp] = *reinterpret_cast<const uint4*>(rope_cs + (int64_t)pos * 64 + (tid & 7) * 8);
       sn4[pp] = *reinterpret_cast<const uint4*>(rope_cs + ((int64_t)T + pos) * 64 + (tid & 7) * 8);
     }
@@ -442,7 +442,8 @@ static int check_prefill(const char* name, int T, int nh, int nkv, int hd, const
   if (nh <= 0 || nkv <= 0 || nh % nkv != 0)
     return set_error(SOLORT_EINVAL, "%s: nh=%d must be a positive multiple of nkv=%d", name, nh, nkv);
   const int G = nh / nkv;
-  if (G != 1 && G != 2 && G != 4) return set_error(SOLORT_EINVAL, "%s: query group %d not in {1,2,4}", name, G);
+  if (G != 1 && G != 2 && G != 4 && G != 8)
+    return set_error(SOLORT_EINVAL, "%s: query group %d not in {1,2,4,8}", name, G);
   if (nkv > 255) return set_error(SOLORT_EINVAL, "%s: nkv=%d above 255", name, nkv);
   if (T < 0 || T > max_len || T >= (1 << 24))
     return set_error(SOLORT_EINVAL, "%s: T=%d outside [0, max_len=%lld]", name, T, (long long)max_len);
@@ -499,6 +500,10 @@ static int launch_prefill(const char* name, const void* q, int64_t q_stride, boo
     case 17: SOLORT_PREFILL_LAUNCH(4, false, true); break;
     case 18: SOLORT_PREFILL_LAUNCH(4, true, false); break;
     case 19: SOLORT_PREFILL_LAUNCH(4, true, true); break;
+    case 32: SOLORT_PREFILL_LAUNCH(8, false, false); break;
+    case 33: SOLORT_PREFILL_LAUNCH(8, false, true); break;
+    case 34: SOLORT_PREFILL_LAUNCH(8, true, false); break;
+    case 35: SOLORT_PREFILL_LAUNCH(8, true, true); break;
   }
 #undef SOLORT_PREFILL_LAUNCH
   return check_launch(name);

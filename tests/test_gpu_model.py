@@ -24,6 +24,8 @@ TINY = ModelShape("tiny", hidden=512, inter=1024, nh=4, nkv=2, layers=2, vocab=4
 # untied one walks through varied tokens
 TINY_UNTIED = ModelShape("tiny-untied", hidden=512, inter=1024, nh=8, nkv=2, layers=3, vocab=4096,
                          tie_embeddings=False)
+# a query group of 8 (as Qwen3-32B's 64 query heads over 8 KV heads), one KV head
+TINY_G8 = ModelShape("tiny-g8", hidden=512, inter=1024, nh=8, nkv=1, layers=2, vocab=4096, tie_embeddings=False)
 # the Qwen3-4B widths (hidden, intermediate, heads, vocabulary, tied embedding) with two layers
 QWEN3_4B_2L = ModelShape("qwen3-4b-2layers", hidden=2560, inter=9728, nh=32, nkv=8, layers=2, vocab=151936,
                          tie_embeddings=True)
@@ -86,7 +88,7 @@ def test_qkv_in_attention_launch_equals_own_launch(gpu, p0):
     _say(f"  tokens {toks}")
 
 
-@pytest.mark.parametrize("shape", [TINY, TINY_UNTIED, QWEN3_4B_2L], ids=lambda s: s.name)
+@pytest.mark.parametrize("shape", [TINY, TINY_UNTIED, TINY_G8, QWEN3_4B_2L], ids=lambda s: s.name)
 def test_decode_steps_match_reference_ops(gpu, shape):
     """Each step's logits against two CPU evaluations of cuda_graph_executor.py:163-190 fed the same
     tokens: the reference's bf16 arithmetic, and the same weights and cache in fp32 (no intermediate
@@ -131,15 +133,15 @@ def test_decode_steps_match_reference_ops(gpu, shape):
     assert kd <= 2.0 * kr + 2e-3
 
 
-@pytest.mark.parametrize("plen,max_len", [(37, 256), (300, 512)], ids=["bucket64", "bucket512-fused"])
-def test_prompt_prefill_then_decode_match_reference_ops(gpu, plen, max_len):
+@pytest.mark.parametrize("plen,max_len,shape", [(37, 256, TINY_UNTIED), (300, 512, TINY_UNTIED), (300, 512, TINY_G8)],
+                         ids=["bucket64", "bucket512-fused", "g8-bucket512-fused"])
+def test_prompt_prefill_then_decode_match_reference_ops(gpu, plen, max_len, shape):
     """Prompt prefill (cuda_graph_executor.py:104-161: library GEMMs around solort_prefill_layer or
     the prologue + solort_prefill_attn) and the decode steps after it, against the CPU evaluations of
     the same model in bf16 and fp32.  The first token's logits and the KV rows of the prompt are
     held to the bf16 reference's own distance from the fp32 model (as the decode steps are); the
     first token is the device argmax of its logits and becomes the decode input at position plen;
     three teacher-forced decode steps follow on each side's own cache."""
-    shape = TINY_UNTIED
     w = RandomQwen3(shape, gpu, seed=83)
     m = GraphQwen3Decode(w, max_len)
     g = torch.Generator().manual_seed(84)

@@ -101,7 +101,8 @@ def test_prefill_row0_and_last_row_pins(gpu):
     assert torch.allclose(o[T - 1], dec.reshape(sh.nh, HD), atol=F32_MAX, rtol=0)
 
 
-@pytest.mark.parametrize("shape", [wl.QWEN3_0_6B, wl.AttnShape("g1", 8, 8, 1)], ids=["g2", "g1"])
+@pytest.mark.parametrize("shape", [wl.QWEN3_0_6B, wl.AttnShape("g1", 8, 8, 1), wl.AttnShape("g8", 16, 2, 1)],
+                         ids=["g2", "g1", "g8"])
 def test_prefill_other_groups(gpu, shape):
     T = 200
     _say(f"[prefill {shape.name} T={T}]")
@@ -117,8 +118,9 @@ def test_prefill_other_groups(gpu, shape):
 
 
 @pytest.mark.parametrize("T,shape", [(1, wl.QWEN3_4B), (17, wl.QWEN3_4B), (128, wl.QWEN3_4B), (333, wl.QWEN3_4B),
-                                     (1024, wl.QWEN3_4B), (200, wl.QWEN3_0_6B), (150, wl.AttnShape("g1", 8, 8, 1))],
-                         ids=["4b-1", "4b-17", "4b-128", "4b-333", "4b-1024", "g2-200", "g1-150"])
+                                     (1024, wl.QWEN3_4B), (200, wl.QWEN3_0_6B), (150, wl.AttnShape("g1", 8, 8, 1)),
+                                     (131, wl.AttnShape("g8", 16, 2, 1))],
+                         ids=["4b-1", "4b-17", "4b-128", "4b-333", "4b-1024", "g2-200", "g1-150", "g8-131"])
 def test_prefill_layer_equals_prologue_then_attention(gpu, T, shape):
     """solort_prefill_layer (K/V prologue + attention normalising q itself) writes the same cache
     rows and the same outputs, bit for bit, as solort_qknorm_rope_kvwrite_cs followed by
